@@ -1,0 +1,216 @@
+"""Headline benchmark: ALIF forward + fast_sigmoid surrogate backward on one MI355X.
+
+Workload: input currents [T=256, B=128, N=4096] fp32 ~ N(0.25, 0.6),
+ALIFParams(tau_mem=20 (decay 0.95), tau_adaptation=50 (rho 0.98),
+threshold=1, reset=0 (hard reset), beta=1.8), fast_sigmoid slope 10, upstream
+dL/ds ~ N(0, 1).  One step = the public-API forward
+(``surrogate_alif_forward``) plus ``spikes.backward(dL/ds)``, inputs resident
+in HBM.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+METRIC = "neuron-steps/sec (T·B·N) LIF fwd+bwd at 1 GPU; % of HBM roofline"
+T, B, N = 256, 128, 4096
+HBM_PEAK_GBPS = 8000.0
+# algorithmic bytes per neuron-step: forward reads x and writes spikes;
+# backward re-reads x, reads dL/ds, writes dL/dx
+FWD_BYTES, BWD_BYTES = 8, 12
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_alif_fast_sigmoid_T256_B128_N4096.json"
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--cpu-sample-batch", type=int, default=32)
+    return ap.parse_args()
+
+
+def _kernel_times(torch, myelin, x, gs, reps: int):
+    """Average duration (ms) of the forward and backward kernels, launched
+    through the C ABI on the current stream and timed with HIP events on
+    that stream."""
+
+    from myelin_amd import _lib
+    from myelin_amd.autograd import BWD_CHUNK
+
+    p = myelin.ALIFParams(20.0, 50.0, 1.0, 0.0, 1.8)
+    dev = x.device
+    z = torch.zeros((B, N), device=dev)
+    K = math.ceil(T / BWD_CHUNK)
+    mT, aT = torch.empty_like(z), torch.empty_like(z)
+    spikes = torch.empty_like(x)
+    ck_m = torch.empty((K, B, N), device=dev)
+    ck_a = torch.empty_like(ck_m)
+    gx = torch.empty_like(x)
+    gm0, ga0 = torch.empty_like(z), torch.empty_like(z)
+    stream = _lib.stream(dev)
+
+    def fwd():
+        _lib.call("myelin_alif_fwd_f32", x.data_ptr(), z.data_ptr(), z.data_ptr(), mT.data_ptr(), aT.data_ptr(),
+                  spikes.data_ptr(), None, ck_m.data_ptr(), ck_a.data_ptr(), T, B, N, p.decay,
+                  p.adaptation_decay, p.threshold, p.beta, p.reset, 10.0, _lib.RULE_SURROGATE, BWD_CHUNK, stream)
+
+    def bwd():
+        _lib.call("myelin_alif_bwd_f32", x.data_ptr(), ck_m.data_ptr(), ck_a.data_ptr(), gs.data_ptr(), None, None,
+                  gx.data_ptr(), gm0.data_ptr(), ga0.data_ptr(), T, B * N, p.decay, p.adaptation_decay,
+                  p.threshold, p.beta, p.reset, 10.0, 1, BWD_CHUNK, stream)
+
+    out = {}
+    for name, fn in (("fwd", fwd), ("bwd", bwd)):
+        fn()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+        for i in range(reps):
+            ev[2 * i].record()
+            fn()
+            ev[2 * i + 1].record()
+        torch.cuda.synchronize()
+        out[name] = sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
+    return out
+
+
+def _cpu_baseline(torch, sample_b: int):
+    """myelin's torch path (restated in the oracle) on the host cores, on a
+    bounded sample: the same T and N, the first `sample_b` batch rows."""
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_ref as R
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(2)
+
+    def run(b):
+        x = (0.25 + 0.6 * torch.randn(T, b, N, generator=g)).requires_grad_()
+        gs = torch.randn(T, b, N, generator=g)
+        z = torch.zeros(b, N)
+        t0 = time.perf_counter()
+        _, _, s = R.surrogate_alif_unroll(x, z, z, 20.0, 50.0, 1.0, 0.0, 1.8, "fast_sigmoid", 10.0)
+        s.backward(gs)
+        return time.perf_counter() - t0
+
+    run(2)  # warmup, excluded
+    dt = run(sample_b)
+    return {
+        "value": T * sample_b * N / dt,
+        "unit": "neuron-steps/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle torch_ref.surrogate_alif_unroll fwd + autograd bwd, T={T}, B={sample_b} of {B}, "
+        f"N={N}, fp32, 1 repeat after a B=2 warmup ({dt:.1f} s)",
+    }
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards over B*N with "
+            "no exchange; multi-GPU runs are not part of this build)",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    import myelin_amd as myelin
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(2)
+    x = (0.25 + 0.6 * torch.randn(T, B, N, generator=g)).to(dev)
+    gs = torch.randn(T, B, N, generator=g).to(dev)
+    z = torch.zeros((B, N), device=dev)
+    p = myelin.ALIFParams(20.0, 50.0, 1.0, 0.0, 1.8)
+    xd = x.clone().requires_grad_()
+
+    def step():
+        xd.grad = None
+        _, s = myelin.surrogate_alif_forward(xd, myelin.ALIFState(z, z), p, surrogate="fast_sigmoid",
+                                             surrogate_slope=10.0)
+        s.backward(gs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    E = T * B * N
+    value = E / (ms * 1e-3)
+
+    kt = _kernel_times(torch, myelin, x, gs, reps=max(5, args.steps))
+    fwd_gbps = FWD_BYTES * E / (kt["fwd"] * 1e-3) / 1e9
+    bwd_gbps = BWD_BYTES * E / (kt["bwd"] * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bwd_hbm_bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "neuron-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "ALIF forward + fast_sigmoid surrogate backward (surrogate_alif_forward + backward)",
+            "T": T,
+            "B": B,
+            "N": N,
+            "tau_mem": 20.0,
+            "tau_adaptation": 50.0,
+            "beta": 1.8,
+            "threshold": 1.0,
+            "reset": 0.0,
+            "surrogate_slope": 10.0,
+            "x": "N(0.25, 0.6)",
+            "grad_spikes": "N(0, 1)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "bwd_chunked<ALIF, C=16, fast_sigmoid>",
+            "achieved": bwd_gbps,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": bwd_gbps / HBM_PEAK_GBPS,
+            "traffic": traffic,
+        },
+        "kernels": {
+            "fwd_ms": kt["fwd"],
+            "bwd_ms": kt["bwd"],
+            "fwd_GBps_algorithmic": fwd_gbps,
+            "bwd_GBps_algorithmic": bwd_gbps,
+            "step_GBps_algorithmic": (FWD_BYTES + BWD_BYTES) * E / (ms * 1e-3) / 1e9,
+            "step_hbm_frac": (FWD_BYTES + BWD_BYTES) * E / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = _cpu_baseline(torch, args.cpu_sample_batch)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

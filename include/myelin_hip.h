@@ -1,0 +1,182 @@
+/*
+ * myelin_hip.h -- C ABI of libmyelin_hip.so, the MI355X (gfx950) kernels of
+ * myelin's fused-time spiking-neuron path.
+ *
+ * Conventions
+ *   - Plain pointers to device memory, int64 sizes, fp32 scalars; no torch
+ *     or HIP types.  `myelin_stream_t` is layout-compatible with hipStream_t
+ *     (pass torch.cuda.current_stream().cuda_stream).
+ *   - Every call is asynchronous on `stream`, allocates nothing, holds no
+ *     global mutable state, and may be called from any host thread (the
+ *     autograd engine runs backward on its own device thread).
+ *   - Return value: 0 on success, MYELIN_EINVAL for a rejected argument,
+ *     MYELIN_EHIP for a HIP launch error.  myelin_last_error() returns the
+ *     message of the calling thread's last failure.
+ *   - Time-major layout: a [T, B, N] tensor is passed as T rows of BN = B*N
+ *     contiguous floats.  Chunk-start checkpoints are [ceil(T/chunk), BN]:
+ *     row k holds the state *before* step k*chunk (row 0 = initial state).
+ *
+ * Citations are file:line in djsaunde/myelin (src/myelin/...).
+ */
+#ifndef MYELIN_HIP_H
+#define MYELIN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *myelin_stream_t;
+
+#define MYELIN_OK 0
+#define MYELIN_EINVAL 1
+#define MYELIN_EHIP 2
+
+/* spike rules */
+#define MYELIN_RULE_THRESHOLD 0 /* s = m' >= th            (neurons.py:112,124) */
+#define MYELIN_RULE_SURROGATE 1 /* s = slope*(m' - th) >= 0 (surrogates.py:108) */
+
+/* surrogate ids, same numbering as triton/lif.py:356-370 */
+#define MYELIN_SG_SIGMOID 0
+#define MYELIN_SG_FAST_SIGMOID 1
+#define MYELIN_SG_ATAN 2
+#define MYELIN_SG_TRIANGULAR 3
+#define MYELIN_SG_SUPERSPIKE 4
+#define MYELIN_SG_MULTI_GAUSSIAN 5
+/* hard threshold, zero spike derivative: the adjoint of the plain
+ * lif_unroll / alif_unroll through the membrane path only (their spikes
+ * carry no gradient, functional.py:21-78) */
+#define MYELIN_SG_NONE 6
+
+/* element type codes for pack / unpack */
+#define MYELIN_DT_F32 0
+#define MYELIN_DT_F16 1
+#define MYELIN_DT_BF16 2
+#define MYELIN_DT_U8 3 /* bool, uint8, int8 */
+#define MYELIN_DT_I32 4
+#define MYELIN_DT_I64 5
+#define MYELIN_DT_F64 6
+
+const char *myelin_last_error(void);
+int myelin_abi_version(void);
+
+/*
+ * Fused-time LIF forward over T steps in one launch, state in registers.
+ *   m' = m*decay + x_t ; s_t = rule(m', threshold) ; m = s_t ? reset : m'
+ * spikes   [T, BN] fp32 0/1, or NULL when `packed` is given
+ * packed   [T, B, ceil(N/32)] int32 words (bit i = neuron 32w+i), or NULL
+ * ckpt_m   [ceil(T/chunk), BN] chunk-start membranes, or NULL
+ * Replaces: _lif_forward_kernel + lif_forward (triton/lif.py:16-95),
+ *   _surrogate_lif_forward_kernel + surrogate_lif_forward (triton/lif.py:195-222,
+ *   373-405), _lif_forward_packed_spikes_kernel + lif_forward_packed_spikes
+ *   (triton/lif.py:98-192); semantics of functional.py:21-45,115-146.
+ */
+int myelin_lif_fwd_f32(const float *x, const float *m0, float *m_final,
+                       float *spikes, int32_t *packed, float *ckpt_m,
+                       int64_t T, int64_t B, int64_t N, float decay,
+                       float threshold, float reset, float slope, int rule,
+                       int64_t chunk, myelin_stream_t stream);
+
+/*
+ * Fused-time ALIF forward.
+ *   m' = m*decay + x ; th = threshold + beta*a ; s = rule(m', th)
+ *   m = s ? reset : m' ; a = a*rho + s
+ * Replaces: generated_alif_forward (triton/generated.py:1159-1189, whose
+ *   step body is dsl.py:1064-1089) and the forward of surrogate_alif_unroll
+ *   (functional.py:149-189); semantics of neurons.py:117-128.
+ */
+int myelin_alif_fwd_f32(const float *x, const float *m0, const float *a0,
+                        float *m_final, float *a_final, float *spikes,
+                        int32_t *packed, float *ckpt_m, float *ckpt_a,
+                        int64_t T, int64_t B, int64_t N, float decay,
+                        float rho, float threshold, float beta, float reset,
+                        float slope, int rule, int64_t chunk,
+                        myelin_stream_t stream);
+
+/*
+ * Reverse-time surrogate backward with chunked recompute: each chunk is
+ * re-run forward from its checkpoint (x re-read once), staged in
+ * registers, then walked backward.  grad_spikes / grad_m_final may be NULL.
+ * chunk must be 8, 16 or 32 (the value the forward used for ckpt_m).
+ * surrogate_id MYELIN_SG_NONE recomputes with the threshold rule and
+ * propagates only through the membrane (grad_spikes is then ignored).
+ * Replaces: _surrogate_lif_backward_kernel + surrogate_lif_backward
+ *   (triton/lif.py:252-288,408-475) together with the recompute Function
+ *   (autograd.py:232-312).
+ */
+int myelin_lif_bwd_f32(const float *x, const float *ckpt_m,
+                       const float *grad_spikes, const float *grad_m_final,
+                       float *grad_x, float *grad_m0, int64_t T, int64_t BN,
+                       float decay, float threshold, float reset, float slope,
+                       int surrogate_id, int64_t chunk, myelin_stream_t stream);
+
+/*
+ * Two-state (membrane, adaptation) adjoint of surrogate_alif_unroll
+ * (functional.py:149-189).  The reference has no fused kernel for it
+ * (kernels.py:368-372 raise); this replaces its torch-autograd route.
+ */
+int myelin_alif_bwd_f32(const float *x, const float *ckpt_m,
+                        const float *ckpt_a, const float *grad_spikes,
+                        const float *grad_m_final, const float *grad_a_final,
+                        float *grad_x, float *grad_m0, float *grad_a0,
+                        int64_t T, int64_t BN, float decay, float rho,
+                        float threshold, float beta, float reset, float slope,
+                        int surrogate_id, int64_t chunk,
+                        myelin_stream_t stream);
+
+/*
+ * Pack nonzero elements of a [rows, n] tensor into [rows, ceil(n/32)] int32
+ * words, LSB first, padding bits zero.
+ * Replaces: _pack_spikes_kernel + pack_spikes_triton (triton/packing.py:20-41,
+ *   100-130); semantics of pack_spikes (packing.py:45-71).
+ */
+int myelin_pack(const void *src, int dtype, int32_t *words, int64_t rows,
+                int64_t n, myelin_stream_t stream);
+
+/*
+ * Unpack words to 0/1 elements of `dtype` ([rows, n]).
+ * Replaces: _unpack_spikes_kernel (triton/packing.py:44-66); semantics of
+ *   unpack_spikes (packing.py:74-81).
+ */
+int myelin_unpack(const int32_t *words, void *dst, int dtype, int64_t rows,
+                  int64_t n, myelin_stream_t stream);
+
+/*
+ * Spike counts reduced over the last (packed) dim and over every leading dim
+ * whose bit is set in `reduce_mask`.  lead_shape (host memory, ndim_lead <= 8
+ * entries) is the shape of the leading dims; out has the shape of the kept
+ * leading dims (a scalar when all are reduced), int64.
+ * Replaces: _packed_spike_row_counts_kernel + packed_spike_counts_triton
+ *   (triton/packing.py:69-91,160-225); semantics of packed_spike_counts
+ *   (packing.py:110-142).
+ */
+int myelin_packed_counts(const int32_t *words, int ndim_lead,
+                         const int64_t *lead_shape, uint32_t reduce_mask,
+                         int64_t n, int64_t *out, myelin_stream_t stream);
+
+/*
+ * Per-neuron counts over a block of leading rows that are NOT packed:
+ * words viewed as [R, K, ceil(n/32)]; out[k, j] = sum_r bit j of row (r, k),
+ * int64 [K, n].
+ * Replaces: the unpack-and-sum branches of packed_spike_count
+ *   (packing.py:97-107,209-216).
+ */
+int myelin_packed_counts_keep_last(const int32_t *words, int64_t R, int64_t K,
+                                   int64_t n, int64_t *out,
+                                   myelin_stream_t stream);
+
+/*
+ * rate[i] = (float)count[i] / (float)denominator, IEEE division.
+ * Replaces: counts.to(dtype) / denominator in packed_spike_rate
+ *   (packing.py:145-162) for float32 (dtype F32) and float64 (dtype F64).
+ */
+int myelin_counts_to_rate(const int64_t *counts, void *out, int dtype,
+                          int64_t numel, int64_t denominator,
+                          myelin_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MYELIN_HIP_H */

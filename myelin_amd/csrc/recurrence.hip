@@ -1,0 +1,626 @@
+// Fused-time LIF / ALIF recurrence (forward) and reverse-time surrogate
+// adjoint with chunked recompute (backward) for gfx950.
+//
+// Layout: x, spikes, grad tensors are time-major [T, BN] fp32 (BN = B*N).
+// One lane owns V adjacent neurons for all T steps; membrane (and
+// adaptation) live in registers for the whole launch, so HBM sees exactly
+// one read of x and one write of spikes per neuron-step in the forward.
+//
+// Forward: the time loop is software-pipelined -- the U inputs of the next
+// block of steps are in flight while the current block is computed -- so a
+// lane keeps U*V*4 bytes of loads outstanding (x does not depend on the
+// state, only the arithmetic is serial in t).
+//
+// Backward: chunks of C steps are walked in reverse.  For each chunk the
+// lane reloads its checkpointed state, recomputes the C forward steps from
+// x (registers hold m' and c = slope*(m'-th) per step), then runs the
+// adjoint backwards through the chunk.  The x loads of the previous chunk
+// and the grad_spikes loads of the current chunk are issued before the
+// dependent arithmetic so each lane has ~2*C*V loads in flight.
+//
+// fp32 rounding: build with -ffp-contract=off; every multiply and add is
+// rounded separately in the order myelin's torch backend evaluates it
+// (neurons.py:111-127, functional.py:140-187).
+
+#include "common.h"
+
+#ifndef MYELIN_FWD_VEC
+#define MYELIN_FWD_VEC 2
+#endif
+#ifndef MYELIN_FWD_UNROLL
+#define MYELIN_FWD_UNROLL 8
+#endif
+#ifndef MYELIN_BWD_VEC
+#define MYELIN_BWD_VEC 1
+#endif
+
+namespace {
+
+using myelin::kWave;
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int V>
+__device__ __forceinline__ void ld_stream(float (&r)[V], const float *p) {
+  if constexpr (V == 1) {
+    r[0] = __builtin_nontemporal_load(p);
+  } else if constexpr (V == 2) {
+    f2 t = __builtin_nontemporal_load(reinterpret_cast<const f2 *>(p));
+    r[0] = t.x;
+    r[1] = t.y;
+  } else {
+    f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+    r[0] = t.x;
+    r[1] = t.y;
+    r[2] = t.z;
+    r[3] = t.w;
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void st_stream(float *p, const float (&r)[V]) {
+  if constexpr (V == 1) {
+    __builtin_nontemporal_store(r[0], p);
+  } else if constexpr (V == 2) {
+    f2 t = {r[0], r[1]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f2 *>(p));
+  } else {
+    f4 t = {r[0], r[1], r[2], r[3]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f4 *>(p));
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void ld(float (&r)[V], const float *p) {
+  if constexpr (V == 1) {
+    r[0] = *p;
+  } else if constexpr (V == 2) {
+    f2 t = *reinterpret_cast<const f2 *>(p);
+    r[0] = t.x;
+    r[1] = t.y;
+  } else {
+    f4 t = *reinterpret_cast<const f4 *>(p);
+    r[0] = t.x;
+    r[1] = t.y;
+    r[2] = t.z;
+    r[3] = t.w;
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void st(float *p, const float (&r)[V]) {
+  if constexpr (V == 1) {
+    *p = r[0];
+  } else if constexpr (V == 2) {
+    f2 t = {r[0], r[1]};
+    *reinterpret_cast<f2 *>(p) = t;
+  } else {
+    f4 t = {r[0], r[1], r[2], r[3]};
+    *reinterpret_cast<f4 *>(p) = t;
+  }
+}
+
+struct FwdArgs {
+  const float *x;
+  const float *m0;
+  const float *a0;
+  float *m_final;
+  float *a_final;
+  float *spikes;
+  int32_t *packed;
+  float *ckpt_m;
+  float *ckpt_a;
+  int64_t T, B, N, BN, W;
+  float decay, rho, thr, beta, reset, slope;
+  int64_t chunk;
+};
+
+// One neuron step.  Returns the spike; updates m (and a for ALIF).
+template <bool ALIF, int RULE>
+__device__ __forceinline__ bool neuron_step(float &m, float &a, float x, const FwdArgs &p) {
+  float mp = m * p.decay;
+  mp = mp + x;
+  float th = p.thr;
+  if constexpr (ALIF) {
+    float ba = p.beta * a;
+    th = p.thr + ba;
+  }
+  bool s;
+  if constexpr (RULE == MYELIN_RULE_THRESHOLD) {
+    s = mp >= th;
+  } else {
+    float c = p.slope * (mp - th);
+    s = c >= 0.0f;
+  }
+  m = s ? p.reset : mp;
+  if constexpr (ALIF) {
+    float ra = a * p.rho;
+    a = ra + (s ? 1.0f : 0.0f);
+  }
+  return s;
+}
+
+// Dense-spike forward: lane owns neurons [V*gid, V*gid + V) of the flat BN axis.
+template <bool ALIF, int RULE, int V, int U>
+__global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t base = gid * V;
+  if (base >= p.BN) return;
+  const int64_t T = p.T, BN = p.BN;
+
+  float m[V], a[V];
+  ld<V>(m, p.m0 + base);
+  if constexpr (ALIF) {
+    ld<V>(a, p.a0 + base);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a[v] = 0.0f;
+  }
+
+  float nxt[U][V];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (u < T) ld_stream<V>(nxt[u], p.x + u * BN + base);
+
+  int64_t cc = 0;  // position inside the current checkpoint chunk
+  for (int64_t t0 = 0; t0 < T; t0 += U) {
+    float cur[U][V];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < V; ++v) cur[u][v] = nxt[u][v];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + U + u;
+      if (t < T) ld_stream<V>(nxt[u], p.x + t * BN + base);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + u;
+      if (t < T) {
+        if (p.ckpt_m != nullptr && cc == 0) {
+          const int64_t k = t / p.chunk;
+          st<V>(p.ckpt_m + k * BN + base, m);
+          if constexpr (ALIF) st<V>(p.ckpt_a + k * BN + base, a);
+        }
+        cc = (cc + 1 == p.chunk) ? 0 : cc + 1;
+        float sp[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p) ? 1.0f : 0.0f;
+        st_stream<V>(p.spikes + t * BN + base, sp);
+      }
+    }
+  }
+  st<V>(p.m_final + base, m);
+  if constexpr (ALIF) st<V>(p.a_final + base, a);
+}
+
+// Packed-spike forward: lanes map to (b, word, bit) so that each half-wave
+// owns one output word; a wave ballot yields two words per step.  Neurons
+// past N in the last word of a row are inactive (their bits are 0).
+template <bool ALIF, int RULE, int U>
+__global__ __launch_bounds__(256) void fwd_packed(FwdArgs p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t g = gid >> 5;  // global word index over [B, W]
+  const int bit = static_cast<int>(gid & 31);
+  const int64_t b = g / p.W;
+  const int64_t n = (g - b * p.W) * 32 + bit;
+  const bool active = (b < p.B) && (n < p.N);
+  const int64_t flat = b * p.N + n;
+  const int64_t T = p.T, BN = p.BN;
+  const int64_t words_per_step = p.B * p.W;
+  const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
+  // the wave's first word; waves start at multiples of 64 lanes, i.e. even words
+  const int64_t g_wave = (gid - lane) >> 5;
+
+  float m = active ? p.m0[flat] : 0.0f;
+  float a = (ALIF && active) ? p.a0[flat] : 0.0f;
+
+  float nxt[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) nxt[u] = (active && u < T) ? __builtin_nontemporal_load(p.x + u * BN + flat) : 0.0f;
+
+  int64_t cc = 0;
+  for (int64_t t0 = 0; t0 < T; t0 += U) {
+    float cur[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + U + u;
+      if (t < T && active) nxt[u] = __builtin_nontemporal_load(p.x + t * BN + flat);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + u;
+      if (t < T) {
+        if (p.ckpt_m != nullptr && cc == 0 && active) {
+          const int64_t k = t / p.chunk;
+          p.ckpt_m[k * BN + flat] = m;
+          if constexpr (ALIF) p.ckpt_a[k * BN + flat] = a;
+        }
+        cc = (cc + 1 == p.chunk) ? 0 : cc + 1;
+        bool s = false;
+        if (active) s = neuron_step<ALIF, RULE>(m, a, cur[u], p);
+        const uint64_t bits = __ballot(s);
+        int32_t *row = p.packed + t * words_per_step;
+        if (lane == 0 && g_wave < words_per_step) row[g_wave] = static_cast<int32_t>(bits & 0xffffffffu);
+        if (lane == 32 && g_wave + 1 < words_per_step) row[g_wave + 1] = static_cast<int32_t>(bits >> 32);
+      }
+    }
+  }
+  if (active) {
+    p.m_final[flat] = m;
+    if constexpr (ALIF) p.a_final[flat] = a;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// surrogate derivatives sigma'(c) (surrogates.py:78-102), ids as
+// triton/lif.py:356-370.
+// ---------------------------------------------------------------------------
+template <int SID>
+__device__ __forceinline__ float sg_deriv(float c) {
+  if constexpr (SID == MYELIN_SG_SIGMOID) {
+    // v(1-v) written as e/(1+e)^2 with e = exp(-|c|): no cancellation
+    const float e = expf(-fabsf(c));
+    const float d = 1.0f + e;
+    return e / (d * d);
+  } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
+    float d = 1.0f + fabsf(c);
+    return 0.5f / (d * d);
+  } else if constexpr (SID == MYELIN_SG_ATAN) {
+    float s = 1.5707963267948966f * c;
+    return 0.5f / (1.0f + s * s);
+  } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
+    float sg = (c > 0.0f) ? 1.0f : ((c < 0.0f) ? -1.0f : 0.0f);
+    return fabsf(c) < 1.0f ? -sg : 0.0f;
+  } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
+    float d = 1.0f + fabsf(c);
+    return 1.0f / (d * d);
+  } else if constexpr (SID == MYELIN_SG_NONE) {
+    return 0.0f;
+  } else {
+    float z = c / 0.5f, r = c - 1.0f, l = c + 1.0f;
+    return 0.47873073648171924f * expf(-0.5f * z * z) + 0.07978845608028655f * expf(-0.5f * r * r) +
+           0.07978845608028655f * expf(-0.5f * l * l);
+  }
+}
+
+struct BwdArgs {
+  const float *x;
+  const float *ckpt_m;
+  const float *ckpt_a;
+  const float *gs;
+  const float *gmT;
+  const float *gaT;
+  float *gx;
+  float *gm0;
+  float *ga0;
+  int64_t T, BN;
+  float decay, rho, thr, beta, reset, slope;
+};
+
+// Reverse-time adjoint.  Per step, with gm = dL/dm_{t+1}, ga = dL/da_{t+1}:
+//   q  = gm*(reset - m') + gs_t + ga
+//   gc = q * slope * sigma'(c),  c = slope*(m' - th)
+//   gp = gm*(1 - s) + gc         -> grad_x[t]
+//   ga = ga*rho - beta*gc ;  gm = gp*decay
+template <bool ALIF, int C, int SID, int V>
+__global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t base = gid * V;
+  if (base >= p.BN) return;
+  const int64_t T = p.T, BN = p.BN;
+  const int64_t K = (T + C - 1) / C;
+  const bool has_gs = (SID != MYELIN_SG_NONE) && p.gs != nullptr;
+
+  float gm[V], ga[V];
+  if (p.gmT != nullptr) {
+    ld<V>(gm, p.gmT + base);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) gm[v] = 0.0f;
+  }
+  if (ALIF && p.gaT != nullptr) {
+    ld<V>(ga, p.gaT + base);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) ga[v] = 0.0f;
+  }
+
+  float xb[C][V];
+  {
+    const int64_t t0 = (K - 1) * C;
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+      if (t0 + j < T) ld_stream<V>(xb[j], p.x + (t0 + j) * BN + base);
+  }
+
+  for (int64_t k = K - 1; k >= 0; --k) {
+    const int64_t t0 = k * C;
+    float gsb[C][V];
+    if (has_gs) {
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (t0 + j < T) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+    }
+    float m[V], a[V];
+    ld<V>(m, p.ckpt_m + k * BN + base);
+    if constexpr (ALIF) {
+      ld<V>(a, p.ckpt_a + k * BN + base);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) a[v] = 0.0f;
+    }
+
+    // recompute the chunk forward
+    float pre[C][V], cv[C][V];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      if (t0 + j < T) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float mp = m[v] * p.decay;
+          mp = mp + xb[j][v];
+          float th = p.thr;
+          if constexpr (ALIF) {
+            float ba = p.beta * a[v];
+            th = p.thr + ba;
+          }
+          // the plain unrolls spike on m' >= th; store c so that c >= 0 is that test
+          const float c = (SID == MYELIN_SG_NONE) ? mp - th : p.slope * (mp - th);
+          const bool s = (SID == MYELIN_SG_NONE) ? (mp >= th) : (c >= 0.0f);
+          pre[j][v] = mp;
+          cv[j][v] = c;
+          m[v] = s ? p.reset : mp;
+          if constexpr (ALIF) {
+            float ra = a[v] * p.rho;
+            a[v] = ra + (s ? 1.0f : 0.0f);
+          }
+        }
+      }
+    }
+
+    // inputs of the previous chunk (always a full chunk) go in flight now
+    if (k > 0) {
+#pragma unroll
+      for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
+    }
+
+#pragma unroll
+    for (int j = C - 1; j >= 0; --j) {
+      if (t0 + j < T) {
+        float g[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float c = cv[j][v];
+          const float s = c >= 0.0f ? 1.0f : 0.0f;
+          if constexpr (SID == MYELIN_SG_NONE) {
+            // where(s, reset, m') passes gradient to m' only where s == 0
+            const float gp = s != 0.0f ? 0.0f : gm[v];
+            g[v] = gp;
+            if constexpr (ALIF) ga[v] = ga[v] * p.rho;
+            gm[v] = gp * p.decay;
+          } else {
+            const float dsdm = p.slope * sg_deriv<SID>(c);
+            float q = gm[v] * (p.reset - pre[j][v]);
+            if (has_gs) q = q + gsb[j][v];
+            if constexpr (ALIF) q = q + ga[v];
+            const float gc = q * dsdm;
+            const float gp = gm[v] * (1.0f - s) + gc;
+            g[v] = gp;
+            if constexpr (ALIF) {
+              float r = ga[v] * p.rho;
+              ga[v] = r - p.beta * gc;
+            }
+            gm[v] = gp * p.decay;
+          }
+        }
+        st_stream<V>(p.gx + (t0 + j) * BN + base, g);
+      }
+    }
+  }
+  st<V>(p.gm0 + base, gm);
+  if constexpr (ALIF) st<V>(p.ga0 + base, ga);
+}
+
+// ---------------------------------------------------------------------------
+// host dispatch
+// ---------------------------------------------------------------------------
+
+int64_t blocks_for(int64_t lanes) { return (lanes + 255) / 256; }
+
+template <bool ALIF, int RULE>
+int launch_fwd(const FwdArgs &a, hipStream_t stream) {
+  if (a.packed != nullptr) {
+    const int64_t lanes = a.B * a.W * 32;
+    fwd_packed<ALIF, RULE, MYELIN_FWD_UNROLL><<<dim3(blocks_for(lanes)), dim3(256), 0, stream>>>(a);
+    return myelin::launched("fwd_packed");
+  }
+  // widest vector the pointers and BN allow
+  const void *ptrs[] = {a.x, a.m0, a.m_final, a.spikes, a.ckpt_m, ALIF ? a.a0 : nullptr,
+                        ALIF ? a.a_final : nullptr, ALIF ? a.ckpt_a : nullptr};
+  int v = MYELIN_FWD_VEC;
+  while (v > 1) {
+    bool ok = (a.BN % v) == 0;
+    for (const void *q : ptrs)
+      if (q != nullptr && !myelin::aligned(q, 4 * v)) ok = false;
+    if (ok) break;
+    v >>= 1;
+  }
+  const int64_t lanes = (a.BN + v - 1) / v;
+  const dim3 grid(blocks_for(lanes));
+  if (v == 4)
+    fwd_dense<ALIF, RULE, 4, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+  else if (v == 2)
+    fwd_dense<ALIF, RULE, 2, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+  else
+    fwd_dense<ALIF, RULE, 1, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+  return myelin::launched("fwd_dense");
+}
+
+template <bool ALIF>
+int fwd_entry(FwdArgs &a, int rule, hipStream_t stream) {
+  if (a.T < 1 || a.B < 1 || a.N < 1) return myelin::invalid("T, B and N must be positive");
+  if (a.x == nullptr || a.m0 == nullptr || a.m_final == nullptr)
+    return myelin::invalid("x, m0 and m_final are required");
+  if (ALIF && (a.a0 == nullptr || a.a_final == nullptr))
+    return myelin::invalid("a0 and a_final are required for ALIF");
+  if ((a.spikes == nullptr) == (a.packed == nullptr))
+    return myelin::invalid("exactly one of spikes / packed must be given");
+  if (a.ckpt_m != nullptr && a.chunk < 1) return myelin::invalid("chunk must be positive");
+  if (ALIF && (a.ckpt_m == nullptr) != (a.ckpt_a == nullptr))
+    return myelin::invalid("ckpt_m and ckpt_a must be given together");
+  if (a.chunk < 1) a.chunk = 1;
+  a.BN = a.B * a.N;
+  a.W = (a.N + 31) / 32;
+  if (rule == MYELIN_RULE_THRESHOLD) return launch_fwd<ALIF, MYELIN_RULE_THRESHOLD>(a, stream);
+  if (rule == MYELIN_RULE_SURROGATE) return launch_fwd<ALIF, MYELIN_RULE_SURROGATE>(a, stream);
+  return myelin::invalid("unknown spike rule %d", rule);
+}
+
+template <bool ALIF, int C, int SID>
+int launch_bwd_sid(const BwdArgs &a, hipStream_t stream) {
+  const void *ptrs[] = {a.x, a.ckpt_m, a.gs, a.gmT, a.gx, a.gm0, a.ckpt_a, a.gaT, a.ga0};
+  int v = MYELIN_BWD_VEC;
+  while (v > 1) {
+    bool ok = (a.BN % v) == 0;
+    for (const void *q : ptrs)
+      if (q != nullptr && !myelin::aligned(q, 4 * v)) ok = false;
+    if (ok) break;
+    v >>= 1;
+  }
+  const dim3 grid(blocks_for((a.BN + v - 1) / v));
+  if (v == 2)
+    bwd_chunked<ALIF, C, SID, 2><<<grid, dim3(256), 0, stream>>>(a);
+  else
+    bwd_chunked<ALIF, C, SID, 1><<<grid, dim3(256), 0, stream>>>(a);
+  return myelin::launched("bwd_chunked");
+}
+
+template <bool ALIF, int C>
+int launch_bwd_c(const BwdArgs &a, int sid, hipStream_t stream) {
+  switch (sid) {
+    case MYELIN_SG_SIGMOID: return launch_bwd_sid<ALIF, C, MYELIN_SG_SIGMOID>(a, stream);
+    case MYELIN_SG_FAST_SIGMOID: return launch_bwd_sid<ALIF, C, MYELIN_SG_FAST_SIGMOID>(a, stream);
+    case MYELIN_SG_ATAN: return launch_bwd_sid<ALIF, C, MYELIN_SG_ATAN>(a, stream);
+    case MYELIN_SG_TRIANGULAR: return launch_bwd_sid<ALIF, C, MYELIN_SG_TRIANGULAR>(a, stream);
+    case MYELIN_SG_SUPERSPIKE: return launch_bwd_sid<ALIF, C, MYELIN_SG_SUPERSPIKE>(a, stream);
+    case MYELIN_SG_MULTI_GAUSSIAN: return launch_bwd_sid<ALIF, C, MYELIN_SG_MULTI_GAUSSIAN>(a, stream);
+    case MYELIN_SG_NONE: return launch_bwd_sid<ALIF, C, MYELIN_SG_NONE>(a, stream);
+    default: return myelin::invalid("unknown surrogate id %d", sid);
+  }
+}
+
+template <bool ALIF>
+int bwd_entry(const BwdArgs &a, int sid, int64_t chunk, hipStream_t stream) {
+  if (a.T < 1 || a.BN < 1) return myelin::invalid("T and BN must be positive");
+  if (a.x == nullptr || a.ckpt_m == nullptr || a.gx == nullptr || a.gm0 == nullptr)
+    return myelin::invalid("x, ckpt_m, grad_x and grad_m0 are required");
+  if (ALIF && (a.ckpt_a == nullptr || a.ga0 == nullptr))
+    return myelin::invalid("ckpt_a and grad_a0 are required for ALIF");
+  switch (chunk) {
+    case 8: return launch_bwd_c<ALIF, 8>(a, sid, stream);
+    case 16: return launch_bwd_c<ALIF, 16>(a, sid, stream);
+    case 32: return launch_bwd_c<ALIF, 32>(a, sid, stream);
+    default: return myelin::invalid("backward chunk must be 8, 16 or 32; got %lld", (long long)chunk);
+  }
+}
+
+}  // namespace
+
+extern "C" int myelin_lif_fwd_f32(const float *x, const float *m0, float *m_final, float *spikes, int32_t *packed,
+                                  float *ckpt_m, int64_t T, int64_t B, int64_t N, float decay, float threshold,
+                                  float reset, float slope, int rule, int64_t chunk, myelin_stream_t stream) {
+  FwdArgs a{};
+  a.x = x;
+  a.m0 = m0;
+  a.m_final = m_final;
+  a.spikes = spikes;
+  a.packed = packed;
+  a.ckpt_m = ckpt_m;
+  a.T = T;
+  a.B = B;
+  a.N = N;
+  a.decay = decay;
+  a.thr = threshold;
+  a.reset = reset;
+  a.slope = slope;
+  a.chunk = chunk;
+  return fwd_entry<false>(a, rule, myelin::as_hip(stream));
+}
+
+extern "C" int myelin_alif_fwd_f32(const float *x, const float *m0, const float *a0, float *m_final, float *a_final,
+                                   float *spikes, int32_t *packed, float *ckpt_m, float *ckpt_a, int64_t T,
+                                   int64_t B, int64_t N, float decay, float rho, float threshold, float beta,
+                                   float reset, float slope, int rule, int64_t chunk, myelin_stream_t stream) {
+  FwdArgs a{};
+  a.x = x;
+  a.m0 = m0;
+  a.a0 = a0;
+  a.m_final = m_final;
+  a.a_final = a_final;
+  a.spikes = spikes;
+  a.packed = packed;
+  a.ckpt_m = ckpt_m;
+  a.ckpt_a = ckpt_a;
+  a.T = T;
+  a.B = B;
+  a.N = N;
+  a.decay = decay;
+  a.rho = rho;
+  a.thr = threshold;
+  a.beta = beta;
+  a.reset = reset;
+  a.slope = slope;
+  a.chunk = chunk;
+  return fwd_entry<true>(a, rule, myelin::as_hip(stream));
+}
+
+extern "C" int myelin_lif_bwd_f32(const float *x, const float *ckpt_m, const float *grad_spikes,
+                                  const float *grad_m_final, float *grad_x, float *grad_m0, int64_t T, int64_t BN,
+                                  float decay, float threshold, float reset, float slope, int surrogate_id,
+                                  int64_t chunk, myelin_stream_t stream) {
+  BwdArgs a{};
+  a.x = x;
+  a.ckpt_m = ckpt_m;
+  a.gs = grad_spikes;
+  a.gmT = grad_m_final;
+  a.gx = grad_x;
+  a.gm0 = grad_m0;
+  a.T = T;
+  a.BN = BN;
+  a.decay = decay;
+  a.thr = threshold;
+  a.reset = reset;
+  a.slope = slope;
+  return bwd_entry<false>(a, surrogate_id, chunk, myelin::as_hip(stream));
+}
+
+extern "C" int myelin_alif_bwd_f32(const float *x, const float *ckpt_m, const float *ckpt_a,
+                                   const float *grad_spikes, const float *grad_m_final, const float *grad_a_final,
+                                   float *grad_x, float *grad_m0, float *grad_a0, int64_t T, int64_t BN, float decay,
+                                   float rho, float threshold, float beta, float reset, float slope, int surrogate_id,
+                                   int64_t chunk, myelin_stream_t stream) {
+  BwdArgs a{};
+  a.x = x;
+  a.ckpt_m = ckpt_m;
+  a.ckpt_a = ckpt_a;
+  a.gs = grad_spikes;
+  a.gmT = grad_m_final;
+  a.gaT = grad_a_final;
+  a.gx = grad_x;
+  a.gm0 = grad_m0;
+  a.ga0 = grad_a0;
+  a.T = T;
+  a.BN = BN;
+  a.decay = decay;
+  a.rho = rho;
+  a.thr = threshold;
+  a.beta = beta;
+  a.reset = reset;
+  a.slope = slope;
+  return bwd_entry<true>(a, surrogate_id, chunk, myelin::as_hip(stream));
+}

@@ -1,0 +1,600 @@
+"""Op-by-op CPU restatement of myelin's ``torch`` backend (the oracle).
+
+TEST INFRASTRUCTURE ONLY -- never imported by ``myelin_amd``.
+
+Every function below restates one reference function; the citation in its
+docstring is ``file:line`` inside djsaunde/myelin (``src/myelin/...``).  The
+arithmetic is written with the same ATen ops in the same evaluation order as
+the reference so that, on the CPU, forward results are bit-identical to what
+myelin computes, and gradients are produced by ``torch.autograd`` exactly as
+the reference's surrogate unrolls produce them.
+
+How each function is pinned (checked against something other than itself;
+see ``tests/test_oracle_*.py``):
+
+* ``lif_unroll`` / ``alif_unroll`` -- the reference's own closed-form step
+  vectors (``tests/test_lif_reference.py:15-27,72-113``, restated in
+  ``tests/golden/reference_vectors.json``), a brute-force Python-float loop
+  with fp32 rounding after every op, and bit equality with the independent C
+  restatement ``oracle/c/oracle.c``.
+* surrogate primitives / derivatives -- derivatives are checked against
+  float64 ``torch.autograd`` of the primitives (an independent library
+  routine) and against hand values at fixed points.
+* ``surrogate_lif_unroll`` / ``surrogate_alif_unroll`` gradients -- against
+  the closed-form adjoint in ``oracle/c/oracle.c`` (independently derived),
+  float64 finite differences through the smooth (``hard_forward=False``)
+  path, and golden vectors written from the reference itself
+  (``tests/golden/make_golden.py``).
+* packing -- ``numpy.packbits(bitorder="little")`` viewed as little-endian
+  int32 (independent routine), the reference's vectors
+  (``tests/test_packing.py:66-74,193-201``) and golden vectors.
+* linear stream / checkpoint / rate functions -- invariance of every output
+  and gradient to the checkpoint size (C=1, C=T, ragged C), the stream path
+  against autograd through an explicit ``matmul`` + ``surrogate_lif_unroll``
+  composition, ``rate == spikes.mean(0)`` (``tests/test_modules.py:892-936``),
+  and golden vectors from the reference.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+
+import torch
+
+# ---------------------------------------------------------------------------
+# parameters  (neurons.py:15-62)
+# ---------------------------------------------------------------------------
+
+
+def decay_from_tau(tau: float) -> float:
+    """``LIFParams.decay`` / ``ALIFParams.adaptation_decay`` (neurons.py:22-28,56-62).
+
+    Computed in Python double precision; ATen rounds it to fp32 when it
+    multiplies an fp32 tensor.
+    """
+
+    if tau <= 0:
+        raise ValueError("tau must be positive")
+    return 1.0 - (1.0 / tau)
+
+
+# ---------------------------------------------------------------------------
+# surrogates  (surrogates.py:19-110)
+# ---------------------------------------------------------------------------
+
+SURROGATE_NAMES = ("sigmoid", "fast_sigmoid", "atan", "triangular", "superspike", "multi_gaussian")
+
+
+def _ncdf(c: torch.Tensor, mean: float, sigma: float) -> torch.Tensor:
+    # surrogates.py:64-65
+    return 0.5 * (1.0 + torch.erf((c - mean) / (1.4142135623730951 * sigma)))
+
+
+def surrogate_primitive(name: str, c: torch.Tensor) -> torch.Tensor:
+    """Smooth primitive sigma(c) (surrogates.py:29-75)."""
+
+    if name == "sigmoid":
+        return torch.sigmoid(c)
+    if name == "fast_sigmoid":
+        return 0.5 * (c / (1.0 + c.abs()) + 1.0)
+    if name == "atan":
+        return torch.atan(torch.pi * c / 2.0) / torch.pi + 0.5
+    if name == "triangular":
+        return (1.0 - c.abs()).clamp(min=0.0, max=1.0)
+    if name == "superspike":
+        return c / (1.0 + c.abs()) + 0.5
+    if name == "multi_gaussian":
+        return 0.6 * _ncdf(c, 0.0, 0.5) + 0.2 * _ncdf(c, 1.0, 1.0) + 0.2 * _ncdf(c, -1.0, 1.0)
+    raise ValueError(f"unknown surrogate {name!r}")
+
+
+def surrogate_derivative(name: str, c: torch.Tensor) -> torch.Tensor:
+    """Closed-form sigma'(c) (surrogates.py:78-102)."""
+
+    if name == "sigmoid":
+        v = torch.sigmoid(c)
+        return v * (1.0 - v)
+    if name == "fast_sigmoid":
+        return 0.5 / (1.0 + c.abs()).square()
+    if name == "atan":
+        s = torch.pi * c / 2.0
+        return 0.5 / (1.0 + s.square())
+    if name == "triangular":
+        return torch.where(c.abs() < 1.0, -c.sign(), torch.zeros_like(c))
+    if name == "superspike":
+        return 1.0 / (1.0 + c.abs()).square()
+    if name == "multi_gaussian":
+        k = 0.3989422804014327
+        return (
+            0.6 * (k / 0.5) * torch.exp(-0.5 * (c / 0.5).square())
+            + 0.2 * k * torch.exp(-0.5 * (c - 1.0).square())
+            + 0.2 * k * torch.exp(-0.5 * (c + 1.0).square())
+        )
+    raise ValueError(f"unknown surrogate {name!r}")
+
+
+def hard_spike(name: str, c: torch.Tensor) -> torch.Tensor:
+    """Straight-through spike ``H(c) + sigma(c) - sigma(c).detach()`` (surrogates.py:105-110).
+
+    Note the fp32 value is ``(H + sigma) - sigma``, which is 0.99999994 rather
+    than 1.0 for a fraction of spikes; the reference carries that value into
+    the reset and adaptation updates.
+    """
+
+    h = (c >= 0).to(c.dtype)
+    smooth = surrogate_primitive(name, c)
+    return h + smooth - smooth.detach()
+
+
+# ---------------------------------------------------------------------------
+# unrolls  (neurons.py:106-128, functional.py:21-78,115-189)
+# ---------------------------------------------------------------------------
+
+
+def _check_tbn(inputs: torch.Tensor, *states: torch.Tensor) -> None:
+    if inputs.ndim != 3:
+        raise ValueError(f"inputs must be shaped [T, B, N]; got {tuple(inputs.shape)}")
+    for s in states:
+        if s.shape != inputs.shape[1:]:
+            raise ValueError("initial state must match inputs.shape[1:]")
+
+
+def lif_unroll(
+    inputs: torch.Tensor, m0: torch.Tensor, tau: float, threshold: float, reset: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Hard-reset LIF over ``[T,B,N]`` (functional.py:21-45 via neurons.py:106-114)."""
+
+    _check_tbn(inputs, m0)
+    d = decay_from_tau(tau)
+    m = m0
+    out = []
+    for x in inputs.unbind(0):
+        m = m * d + x
+        s = m >= threshold
+        m = torch.where(s, reset, m)
+        out.append(s.to(x.dtype))
+    return m, torch.stack(out, 0)
+
+
+def alif_unroll(
+    inputs: torch.Tensor,
+    m0: torch.Tensor,
+    a0: torch.Tensor,
+    tau_mem: float,
+    tau_adaptation: float,
+    threshold: float,
+    reset: float,
+    beta: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Adaptive LIF (functional.py:48-78 via neurons.py:117-128)."""
+
+    _check_tbn(inputs, m0, a0)
+    d = decay_from_tau(tau_mem)
+    rho = decay_from_tau(tau_adaptation)
+    m, a = m0, a0
+    out = []
+    for x in inputs.unbind(0):
+        m = m * d + x
+        th = threshold + beta * a
+        s = m >= th
+        sf = s.to(x.dtype)
+        m = torch.where(s, reset, m)
+        a = a * rho + sf
+        out.append(sf)
+    return m, a, torch.stack(out, 0)
+
+
+def surrogate_lif_unroll(
+    inputs: torch.Tensor,
+    m0: torch.Tensor,
+    tau: float,
+    threshold: float,
+    reset: float,
+    surrogate: str,
+    slope: float = 10.0,
+    hard_forward: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Surrogate-gradient LIF, differentiable by autograd (functional.py:115-146)."""
+
+    _check_tbn(inputs, m0)
+    d = decay_from_tau(tau)
+    m = m0
+    out = []
+    for x in inputs.unbind(0):
+        m = m * d + x
+        c = slope * (m - threshold)
+        s = hard_spike(surrogate, c) if hard_forward else surrogate_primitive(surrogate, c)
+        m = m * (1.0 - s) + reset * s
+        out.append(s)
+    return m, torch.stack(out, 0)
+
+
+def surrogate_alif_unroll(
+    inputs: torch.Tensor,
+    m0: torch.Tensor,
+    a0: torch.Tensor,
+    tau_mem: float,
+    tau_adaptation: float,
+    threshold: float,
+    reset: float,
+    beta: float,
+    surrogate: str,
+    slope: float = 10.0,
+    hard_forward: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Surrogate-gradient ALIF, differentiable by autograd (functional.py:149-189)."""
+
+    _check_tbn(inputs, m0, a0)
+    d = decay_from_tau(tau_mem)
+    rho = decay_from_tau(tau_adaptation)
+    m, a = m0, a0
+    out = []
+    for x in inputs.unbind(0):
+        m = m * d + x
+        th = threshold + beta * a
+        c = slope * (m - th)
+        s = hard_spike(surrogate, c) if hard_forward else surrogate_primitive(surrogate, c)
+        m = m * (1.0 - s) + reset * s
+        a = a * rho + s
+        out.append(s)
+    return m, a, torch.stack(out, 0)
+
+
+# ---------------------------------------------------------------------------
+# checkpoint policy  (checkpointing.py:13-60)
+# ---------------------------------------------------------------------------
+
+
+def recommended_checkpoint_size(timesteps: int, policy: str = "balanced") -> int:
+    """checkpointing.py:13-33."""
+
+    if timesteps <= 0:
+        raise ValueError("timesteps must be positive")
+    if policy == "memory":
+        c = math.ceil(math.sqrt(timesteps))
+    elif policy == "balanced":
+        c = math.ceil(timesteps / 4)
+    elif policy == "speed":
+        c = math.ceil(timesteps / 2)
+    else:
+        raise ValueError("policy must be 'memory', 'balanced', or 'speed'")
+    return max(1, min(timesteps, c))
+
+
+def resolve_checkpoint_size(timesteps: int, checkpoint_size: int | str) -> int:
+    """checkpointing.py:36-43."""
+
+    if isinstance(checkpoint_size, int):
+        if checkpoint_size <= 0:
+            raise ValueError("checkpoint_size must be positive")
+        return min(checkpoint_size, timesteps)
+    return recommended_checkpoint_size(timesteps, checkpoint_size)
+
+
+# ---------------------------------------------------------------------------
+# packing  (packing.py:14-162,165-273)
+# ---------------------------------------------------------------------------
+
+BITS = 32
+
+
+def packed_words(n: int) -> int:
+    """packing.py:36-42."""
+
+    if n < 0:
+        raise ValueError("size must be non-negative")
+    return (n + BITS - 1) // BITS
+
+
+def pack_spikes(spikes: torch.Tensor) -> tuple[torch.Tensor, tuple[int, ...]]:
+    """Nonzero -> bit, LSB-first along the last dim, int32 words (packing.py:45-71)."""
+
+    if spikes.ndim == 0:
+        raise ValueError("spikes must have at least one dimension")
+    n = spikes.shape[-1]
+    if n == 0:
+        raise ValueError("cannot pack an empty last dimension")
+    w = packed_words(n)
+    bits = (spikes != 0).to(torch.int64)
+    pad = w * BITS - n
+    if pad:
+        bits = torch.cat((bits, bits.new_zeros((*spikes.shape[:-1], pad))), dim=-1)
+    bits = bits.reshape(*spikes.shape[:-1], w, BITS)
+    weights = torch.ones(BITS, dtype=torch.int64) << torch.arange(BITS, dtype=torch.int64)
+    return (bits * weights).sum(-1).to(torch.int32), tuple(spikes.shape)
+
+
+def _check_packed(data: torch.Tensor, shape: tuple[int, ...]) -> None:
+    # packing.py:236-252
+    if data.dtype != torch.int32:
+        raise ValueError("packed.data must have dtype torch.int32")
+    if len(shape) == 0:
+        raise ValueError("packed.original_shape must have at least one dimension")
+    if shape[-1] <= 0:
+        raise ValueError("packed.original_shape must have non-empty last dimension")
+    if tuple(data.shape) != (*shape[:-1], packed_words(shape[-1])):
+        raise ValueError("packed.data shape does not match packed.original_shape")
+
+
+def unpack_spikes(
+    data: torch.Tensor, shape: tuple[int, ...], dtype: torch.dtype = torch.float32
+) -> torch.Tensor:
+    """packing.py:74-81."""
+
+    _check_packed(data, shape)
+    shifts = torch.arange(BITS, dtype=torch.int64)
+    bits = ((data.to(torch.int64).unsqueeze(-1) >> shifts) & 1).to(dtype)
+    return bits.reshape(*shape[:-1], -1)[..., : shape[-1]]
+
+
+def _norm_dims(dim: int | Sequence[int], ndim: int) -> tuple[int, ...]:
+    # packing.py:223-233
+    raw = (dim,) if isinstance(dim, int) else tuple(dim)
+    out: list[int] = []
+    for d in raw:
+        a = d + ndim if d < 0 else d
+        if a < 0 or a >= ndim:
+            raise IndexError(f"dimension out of range: {d}")
+        if a in out:
+            raise ValueError(f"duplicate reduction dimension: {d}")
+        out.append(a)
+    return tuple(out)
+
+
+def _row_counts(data: torch.Tensor, shape: tuple[int, ...]) -> torch.Tensor:
+    """Per-row popcount with padding bits masked (packing.py:164-205)."""
+
+    _check_packed(data, shape)
+    words = data.to(torch.int64) & 0xFFFFFFFF
+    rem = shape[-1] % BITS
+    if rem:
+        mask = torch.full((words.shape[-1],), 0xFFFFFFFF, dtype=torch.int64)
+        mask[-1] = (1 << rem) - 1
+        words = words & mask
+    shifts = torch.arange(BITS, dtype=torch.int64)
+    return ((words.unsqueeze(-1) >> shifts) & 1).sum(dim=(-1, -2), dtype=torch.int64)
+
+
+def packed_spike_counts(
+    data: torch.Tensor, shape: tuple[int, ...], dim: int | Sequence[int] | None = -1
+) -> torch.Tensor:
+    """Counts over dims that include the last one (packing.py:110-142)."""
+
+    rows = _row_counts(data, shape)
+    if dim is None:
+        return rows.sum()
+    dims = _norm_dims(dim, len(shape))
+    last = len(shape) - 1
+    if last not in dims:
+        raise ValueError(
+            "packed_spike_counts requires reducing the packed/original last dimension; "
+            "use packed_spike_count for dense-like reductions that keep that dimension"
+        )
+    rest = tuple(d for d in dims if d != last)
+    return rows if not rest else rows.sum(dim=rest)
+
+
+def packed_spike_count(
+    data: torch.Tensor, shape: tuple[int, ...], dim: int | Sequence[int] | None = None
+) -> torch.Tensor:
+    """Dense-like count reductions (packing.py:84-107,209-216)."""
+
+    if dim is None:
+        return packed_spike_counts(data, shape, None)
+    dims = _norm_dims(dim, len(shape))
+    last = len(shape) - 1
+    if last in dims:
+        return packed_spike_counts(data, shape, dims)
+    if dims == tuple(range(last)):
+        # every leading dim reduced: per-neuron counts from the bits
+        _check_packed(data, shape)
+        shifts = torch.arange(BITS, dtype=torch.int64)
+        bits = ((data.to(torch.int64) & 0xFFFFFFFF).unsqueeze(-1) >> shifts) & 1
+        lead = tuple(range(last))
+        per = bits.sum(dim=lead, dtype=torch.int64) if lead else bits.to(torch.int64)
+        return per.reshape(-1)[: shape[-1]]
+    dense = unpack_spikes(data, shape, torch.float32)
+    return dense.sum(dim=dims).to(torch.int64)
+
+
+def packed_spike_rate(
+    data: torch.Tensor,
+    shape: tuple[int, ...],
+    dim: int | Sequence[int] | None = None,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``count.to(dtype) / prod(reduced sizes)`` (packing.py:145-162)."""
+
+    counts = packed_spike_count(data, shape, dim)
+    dims = tuple(range(len(shape))) if dim is None else _norm_dims(dim, len(shape))
+    denom = 1
+    for d in dims:
+        denom *= shape[d]
+    return counts.to(dtype) / denom
+
+
+# ---------------------------------------------------------------------------
+# streamed synapse + surrogate LIF  (autograd.py:445-923)
+# ---------------------------------------------------------------------------
+
+
+class _StreamFn(torch.autograd.Function):
+    """Restates ``LinearSurrogateLIFStreamFunction`` (autograd.py:445-558)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, tau, threshold, reset, surrogate, slope):
+        ctx.set_materialize_grads(False)
+        d = decay_from_tau(tau)
+        m = torch.zeros((x.shape[1], w.shape[1]), dtype=x.dtype)
+        pres, spikes = [], []
+        for xt in x.unbind(0):
+            cur = torch.matmul(xt, w)
+            if b is not None:
+                cur = cur + b
+            m = m * d + cur
+            smooth = surrogate_primitive(surrogate, slope * (m - threshold))
+            s = (m >= threshold).to(x.dtype) + smooth - smooth.detach()
+            pres.append(m)
+            spikes.append(s)
+            m = m * (1.0 - s) + reset * s
+        ctx.meta = (tau, threshold, reset, surrogate, slope, b is not None)
+        ctx.save_for_backward(x, w, torch.stack(pres), torch.stack(spikes))
+        return m, torch.stack(spikes)
+
+    @staticmethod
+    def backward(ctx, g_final, g_spikes):
+        if g_final is None and g_spikes is None:
+            return (None,) * 8
+        x, w, pres, spikes = ctx.saved_tensors
+        tau, threshold, reset, surrogate, slope, has_b = ctx.meta
+        d_m = decay_from_tau(tau)
+        need_x, need_w, need_b = ctx.needs_input_grad[:3]
+        gm = torch.zeros_like(pres[0]) if g_final is None else g_final
+        gx = torch.empty_like(x) if need_x else None
+        gw = torch.zeros_like(w) if need_w else None
+        gb = torch.zeros((w.shape[1],), dtype=x.dtype) if (need_b and has_b) else None
+        for t in range(x.shape[0] - 1, -1, -1):
+            pre, s = pres[t], spikes[t]
+            d = slope * surrogate_derivative(surrogate, slope * (pre - threshold))
+            gp = gm * ((1.0 - s) + (reset - pre) * d)
+            if g_spikes is not None:
+                gp = gp + g_spikes[t] * d
+            if gx is not None:
+                gx[t] = torch.matmul(gp, w.t())
+            if gw is not None:
+                gw = gw + torch.matmul(x[t].t(), gp)
+            if gb is not None:
+                gb = gb + gp.sum(dim=0)
+            gm = gp * d_m
+        return gx, gw, gb, None, None, None, None, None
+
+
+def _recompute_chunk(x, w, b, m, t0, t1, d, threshold, reset):
+    pres, spikes = [], []
+    for t in range(t0, t1):
+        cur = torch.matmul(x[t], w)
+        if b is not None:
+            cur = cur + b
+        m = m * d + cur
+        s = (m >= threshold).to(x.dtype)
+        pres.append(m)
+        spikes.append(s)
+        m = m * (1.0 - s) + reset * s
+    return pres, spikes
+
+
+class _CheckpointFn(torch.autograd.Function):
+    """Restates ``LinearSurrogateLIFCheckpointFunction`` (autograd.py:588-717) and,
+    with ``rate=True``, ``LinearSurrogateLIFCheckpointRateFunction``
+    (autograd.py:753-885)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, tau, threshold, reset, surrogate, slope, chunk, rate):
+        ctx.set_materialize_grads(False)
+        d = decay_from_tau(tau)
+        m = torch.zeros((x.shape[1], w.shape[1]), dtype=x.dtype)
+        counts = torch.zeros_like(m) if rate else None
+        starts, spikes = [], []
+        for t, xt in enumerate(x.unbind(0)):
+            if t % chunk == 0:
+                starts.append(m)
+            cur = torch.matmul(xt, w)
+            if b is not None:
+                cur = cur + b
+            m = m * d + cur
+            s = (m >= threshold).to(x.dtype)
+            if rate:
+                counts = counts + s
+            else:
+                spikes.append(s)
+            m = m * (1.0 - s) + reset * s
+        ctx.meta = (tau, threshold, reset, surrogate, slope, chunk, rate)
+        bias = torch.empty(0, dtype=x.dtype) if b is None else b
+        ctx.has_b = b is not None
+        ctx.save_for_backward(x, w, bias, torch.stack(starts))
+        if rate:
+            return m, counts / x.shape[0]
+        return m, torch.stack(spikes)
+
+    @staticmethod
+    def backward(ctx, g_final, g_out):
+        if g_final is None and g_out is None:
+            return (None,) * 10
+        x, w, bias, starts = ctx.saved_tensors
+        b = bias if ctx.has_b else None
+        tau, threshold, reset, surrogate, slope, chunk, rate = ctx.meta
+        d_m = decay_from_tau(tau)
+        T = x.shape[0]
+        need_x, need_w, need_b = ctx.needs_input_grad[:3]
+        gm = torch.zeros((x.shape[1], w.shape[1]), dtype=x.dtype) if g_final is None else g_final
+        gx = torch.empty_like(x) if need_x else None
+        gw = torch.zeros_like(w) if need_w else None
+        gb = torch.zeros((w.shape[1],), dtype=x.dtype) if (need_b and ctx.has_b) else None
+        g_step = None
+        if rate and g_out is not None:
+            g_step = g_out / T
+        for k in range(starts.shape[0] - 1, -1, -1):
+            t0 = k * chunk
+            t1 = min(t0 + chunk, T)
+            pres, spikes = _recompute_chunk(x, w, b, starts[k], t0, t1, d_m, threshold, reset)
+            for j in range(t1 - t0 - 1, -1, -1):
+                t = t0 + j
+                pre, s = pres[j], spikes[j]
+                d = slope * surrogate_derivative(surrogate, slope * (pre - threshold))
+                gp = gm * ((1.0 - s) + (reset - pre) * d)
+                if rate:
+                    if g_step is not None:
+                        gp = gp + g_step * d
+                elif g_out is not None:
+                    gp = gp + g_out[t] * d
+                if gx is not None:
+                    gx[t] = torch.matmul(gp, w.t())
+                if gw is not None:
+                    gw = gw + torch.matmul(x[t].t(), gp)
+                if gb is not None:
+                    gb = gb + gp.sum(dim=0)
+                gm = gp * d_m
+        return gx, gw, gb, None, None, None, None, None, None, None
+
+
+def linear_surrogate_lif_stream(x, w, b, tau, threshold, reset, surrogate="atan", slope=10.0):
+    """``linear_surrogate_lif_stream_function`` (autograd.py:561-585)."""
+
+    return _StreamFn.apply(x, w, b, tau, threshold, reset, surrogate, slope)
+
+
+def linear_surrogate_lif_checkpoint(
+    x, w, b, tau, threshold, reset, surrogate="atan", slope=10.0, checkpoint_size=25
+):
+    """``linear_surrogate_lif_checkpoint_function`` (autograd.py:720-750)."""
+
+    if checkpoint_size <= 0:
+        raise ValueError("checkpoint_size must be positive")
+    return _CheckpointFn.apply(
+        x, w, b, tau, threshold, reset, surrogate, slope, checkpoint_size, False
+    )
+
+
+def linear_surrogate_lif_rate(
+    x,
+    w,
+    b,
+    tau,
+    threshold,
+    reset,
+    surrogate="atan",
+    slope=10.0,
+    checkpoint_size=25,
+    reduction="mean",
+):
+    """``linear_surrogate_lif_checkpoint_rate_function`` (autograd.py:888-923)."""
+
+    if checkpoint_size <= 0:
+        raise ValueError("checkpoint_size must be positive")
+    if reduction not in ("mean", "none"):
+        raise ValueError("reduction must be 'mean' or 'none'")
+    m, rates = _CheckpointFn.apply(
+        x, w, b, tau, threshold, reset, surrogate, slope, checkpoint_size, True
+    )
+    return m, (rates.mean() if reduction == "mean" else rates)

@@ -1,0 +1,84 @@
+"""The C-ABI library loads and exports every entry point the header declares;
+argument validation runs on the host (no GPU calls)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from myelin_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "myelin_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(myelin_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_entry_points():
+    names = declared_functions()
+    assert "myelin_last_error" in names and "myelin_abi_version" in names
+    assert set(_lib.SIGNATURES) <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.myelin_abi_version() == 1
+
+
+def test_validation_errors_are_reported_without_launching():
+    lib = _lib.load()
+    rc = lib.myelin_lif_fwd_f32(None, None, None, None, None, None, 0, 1, 1, 0.9, 1.0, 0.0, 10.0, 0, 16, None)
+    assert rc == _lib.EINVAL
+    assert b"positive" in lib.myelin_last_error()
+    with pytest.raises(ValueError, match="chunk must be 8, 16 or 32"):
+        _lib.call("myelin_lif_bwd_f32", 1, 1, None, None, 1, 1, 4, 4, 0.9, 1.0, 0.0, 10.0, 1, 12, None)
+    with pytest.raises(ValueError, match="unknown surrogate"):
+        _lib.call("myelin_alif_bwd_f32", 1, 1, 1, None, None, None, 1, 1, 1, 4, 4, 0.9, 0.9, 1.0, 1.8, 0.0,
+                  10.0, 42, 16, None)
+    with pytest.raises(ValueError, match="unsupported dtype"):
+        _lib.call("myelin_pack", 1, 99, 1, 4, 4, None)
+    with pytest.raises(ValueError, match="exactly one of spikes"):
+        _lib.call("myelin_lif_fwd_f32", 1, 1, 1, 1, 1, None, 4, 1, 1, 0.9, 1.0, 0.0, 10.0, 0, 16, None)
+    # empty problems are valid no-ops
+    assert lib.myelin_pack(None, 0, None, 0, 5, None) == 0
+
+
+def test_error_message_is_per_thread():
+    import threading
+
+    lib = _lib.load()
+    lib.myelin_pack(None, 0, None, -1, 5, None)
+    seen = {}
+
+    def worker():
+        seen["msg"] = lib.myelin_last_error()
+
+    th = threading.Thread(target=worker)
+    th.start()
+    th.join()
+    assert seen["msg"] == b""
+    assert b"rows" in lib.myelin_last_error()
+
+
+def test_ctypes_signatures_match_header_arity():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, argtypes in _lib.SIGNATURES.items():
+        m = re.search(rf"int {name}\((.*?)\);", text, flags=re.S)
+        assert m, name
+        assert len(m.group(1).split(",")) == len(argtypes), name
+
+
+def test_pointer_types_are_plain():
+    # the ABI takes void* / c types only: ctypes argtypes never name torch
+    for argtypes in _lib.SIGNATURES.values():
+        for a in argtypes:
+            assert a in (ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int, ctypes.c_uint32)
+    assert torch is not None
