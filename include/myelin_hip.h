@@ -98,7 +98,7 @@ int myelin_alif_fwd_f32(const float *x, const float *m0, const float *a0,
  * Reverse-time surrogate backward with chunked recompute: each chunk is
  * re-run forward from its checkpoint (x re-read once), staged in
  * registers, then walked backward.  grad_spikes / grad_m_final may be NULL.
- * chunk must be 8, 16 or 32 (the value the forward used for ckpt_m).
+ * chunk must be 8 or 16 (the value the forward used for ckpt_m).
  * surrogate_id MYELIN_SG_NONE recomputes with the threshold rule and
  * propagates only through the membrane (grad_spikes is then ignored).
  * Replaces: _surrogate_lif_backward_kernel + surrogate_lif_backward

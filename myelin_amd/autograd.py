@@ -21,9 +21,11 @@ import torch
 
 from myelin_amd import _lib
 
-# chunk length of the checkpointed backward (a compiled kernel parameter:
-# 8, 16 or 32)
-BWD_CHUNK = 16
+# chunk length of the checkpointed backward (a compiled kernel parameter,
+# 8 or 16).  8 keeps the backward at 122 VGPRs (4 waves/SIMD), so a
+# [T, 128, 4096] problem runs in one occupancy round; its extra checkpoint
+# traffic (1 B per neuron-step) costs less than the second round C=16 needs.
+BWD_CHUNK = 8
 
 
 def _chunks(T: int) -> int:

@@ -31,7 +31,7 @@
 #define MYELIN_FWD_UNROLL 8
 #endif
 #ifndef MYELIN_BWD_VEC
-#define MYELIN_BWD_VEC 1
+#define MYELIN_BWD_VEC 2
 #endif
 
 namespace {
@@ -141,9 +141,9 @@ __device__ __forceinline__ bool neuron_step(float &m, float &a, float x, const F
   return s;
 }
 
-// Dense-spike forward: lane owns neurons [V*gid, V*gid + V) of the flat BN axis.
+// Generic dense forward: any chunk length, every step guarded.
 template <bool ALIF, int RULE, int V, int U>
-__global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
+__global__ __launch_bounds__(256) void fwd_dense_generic(FwdArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t base = gid * V;
   if (base >= p.BN) return;
@@ -191,6 +191,90 @@ __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
         st_stream<V>(p.spikes + t * BN + base, sp);
       }
     }
+  }
+  st<V>(p.m_final + base, m);
+  if constexpr (ALIF) st<V>(p.a_final + base, a);
+}
+
+// U steps starting at t0, all inside [0, T): straight-line code.
+template <bool ALIF, int RULE, int V, int U>
+__device__ __forceinline__ void fwd_block(const FwdArgs &p, int64_t base, int64_t t0, const float (&cur)[U][V],
+                                          float (&m)[V], float (&a)[V]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float sp[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p) ? 1.0f : 0.0f;
+    st_stream<V>(p.spikes + (t0 + u) * p.BN + base, sp);
+  }
+}
+
+template <bool ALIF, int V>
+__device__ __forceinline__ void fwd_ckpt(const FwdArgs &p, int64_t base, int64_t k, const float (&m)[V],
+                                         const float (&a)[V]) {
+  st<V>(p.ckpt_m + k * p.BN + base, m);
+  if constexpr (ALIF) st<V>(p.ckpt_a + k * p.BN + base, a);
+}
+
+// Dense-spike forward, lane owns neurons [V*gid, V*gid + V) of the flat BN
+// axis.  Checkpoints (when requested) fall on block starts (chunk % U == 0,
+// checked by the host), so every full block of U steps is straight-line code:
+// the compiler keeps the next block's U loads in flight across the current
+// block with exact vmcnt waits.  The last T % U steps run in a guarded tail.
+template <bool ALIF, int RULE, int V, int U>
+__global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t base = gid * V;
+  if (base >= p.BN) return;
+  const int64_t T = p.T, BN = p.BN;
+  const bool ck = p.ckpt_m != nullptr;
+
+  float m[V], a[V];
+  ld<V>(m, p.m0 + base);
+  if constexpr (ALIF) {
+    ld<V>(a, p.a0 + base);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a[v] = 0.0f;
+  }
+
+  const int64_t Tm = (T / U) * U;
+  int64_t next_ck = 0, k = 0;  // next checkpoint step and its row
+  if (Tm > 0) {
+    float nxt[U][V];
+#pragma unroll
+    for (int u = 0; u < U; ++u) ld_stream<V>(nxt[u], p.x + u * BN + base);
+    int64_t t0 = 0;
+    for (; t0 + U < Tm; t0 += U) {
+      float cur[U][V];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int v = 0; v < V; ++v) cur[u][v] = nxt[u][v];
+#pragma unroll
+      for (int u = 0; u < U; ++u) ld_stream<V>(nxt[u], p.x + (t0 + U + u) * BN + base);
+      if (ck && t0 == next_ck) {
+        fwd_ckpt<ALIF, V>(p, base, k++, m, a);
+        next_ck += p.chunk;
+      }
+      fwd_block<ALIF, RULE, V, U>(p, base, t0, cur, m, a);
+    }
+    if (ck && t0 == next_ck) {
+      fwd_ckpt<ALIF, V>(p, base, k++, m, a);
+      next_ck += p.chunk;
+    }
+    fwd_block<ALIF, RULE, V, U>(p, base, t0, nxt, m, a);
+  }
+  for (int64_t t = Tm; t < T; ++t) {
+    if (ck && t == next_ck) {
+      fwd_ckpt<ALIF, V>(p, base, k++, m, a);
+      next_ck += p.chunk;
+    }
+    float xv[V], sp[V];
+    ld_stream<V>(xv, p.x + t * BN + base);
+#pragma unroll
+    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], xv[v], p) ? 1.0f : 0.0f;
+    st_stream<V>(p.spikes + t * BN + base, sp);
   }
   st<V>(p.m_final + base, m);
   if constexpr (ALIF) st<V>(p.a_final + base, a);
@@ -302,19 +386,105 @@ struct BwdArgs {
   float decay, rho, thr, beta, reset, slope;
 };
 
-// Reverse-time adjoint.  Per step, with gm = dL/dm_{t+1}, ga = dL/da_{t+1}:
+// Recompute one chunk forward from its checkpointed state: pre[j] = m'_t,
+// cv[j] = c_t = slope*(m'_t - th_t) (for SG_NONE: m'_t - th_t, so that
+// c >= 0 is the plain threshold test).  GUARD: only the first `len` steps.
+template <bool ALIF, int C, int SID, int V, bool GUARD>
+__device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const float (&xb)[C][V], float (&m)[V],
+                                              float (&a)[V], float (&pre)[C][V], float (&cv)[C][V]) {
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    if (GUARD && j >= len) break;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float mp = m[v] * p.decay;
+      mp = mp + xb[j][v];
+      float th = p.thr;
+      if constexpr (ALIF) {
+        float ba = p.beta * a[v];
+        th = p.thr + ba;
+      }
+      const float c = (SID == MYELIN_SG_NONE) ? mp - th : p.slope * (mp - th);
+      const bool s = c >= 0.0f;
+      pre[j][v] = mp;
+      cv[j][v] = c;
+      m[v] = s ? p.reset : mp;
+      if constexpr (ALIF) {
+        float ra = a[v] * p.rho;
+        a[v] = ra + (s ? 1.0f : 0.0f);
+      }
+    }
+  }
+}
+
+// Walk one chunk backwards, storing grad_x for t0 + j.  Per step, with
+// gm = dL/dm_{t+1}, ga = dL/da_{t+1}:
 //   q  = gm*(reset - m') + gs_t + ga
-//   gc = q * slope * sigma'(c),  c = slope*(m' - th)
-//   gp = gm*(1 - s) + gc         -> grad_x[t]
+//   gc = q * slope * sigma'(c)
+//   gp = gm*(1 - s) + gc          -> grad_x[t]
 //   ga = ga*rho - beta*gc ;  gm = gp*decay
-template <bool ALIF, int C, int SID, int V>
+template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD>
+__device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int64_t t0, int len,
+                                            const float (&gsb)[C][V], const float (&pre)[C][V],
+                                            const float (&cv)[C][V], float (&gm)[V], float (&ga)[V]) {
+#pragma unroll
+  for (int j = C - 1; j >= 0; --j) {
+    if (GUARD && j >= len) continue;
+    float g[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float c = cv[j][v];
+      const float s = c >= 0.0f ? 1.0f : 0.0f;
+      if constexpr (SID == MYELIN_SG_NONE) {
+        // where(s, reset, m') passes gradient to m' only where s == 0
+        const float gp = s != 0.0f ? 0.0f : gm[v];
+        g[v] = gp;
+        if constexpr (ALIF) ga[v] = ga[v] * p.rho;
+        gm[v] = gp * p.decay;
+      } else {
+        const float dsdm = p.slope * sg_deriv<SID>(c);
+        float q = gm[v] * (p.reset - pre[j][v]);
+        if constexpr (GS) q = q + gsb[j][v];
+        if constexpr (ALIF) q = q + ga[v];
+        const float gc = q * dsdm;
+        const float gp = gm[v] * (1.0f - s) + gc;
+        g[v] = gp;
+        if constexpr (ALIF) {
+          float r = ga[v] * p.rho;
+          ga[v] = r - p.beta * gc;
+        }
+        gm[v] = gp * p.decay;
+      }
+    }
+    st_stream<V>(p.gx + (t0 + j) * p.BN + base, g);
+  }
+}
+
+template <bool ALIF, int V>
+__device__ __forceinline__ void bwd_load_ckpt(const BwdArgs &p, int64_t k, int64_t base, float (&m)[V],
+                                              float (&a)[V]) {
+  ld<V>(m, p.ckpt_m + k * p.BN + base);
+  if constexpr (ALIF) {
+    ld<V>(a, p.ckpt_a + k * p.BN + base);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a[v] = 0.0f;
+  }
+}
+
+// Reverse-time adjoint over chunks of C steps, lane owns V neurons.
+// The partial last chunk (T % C steps) is handled first with guards; the
+// full chunks then run as straight-line code, software-pipelined: the
+// checkpoint and x of chunk k-1 are loaded while chunk k is walked
+// backwards, and grad_spikes of chunk k while chunk k is recomputed.
+template <bool ALIF, int C, int SID, int V, bool GS>
 __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t base = gid * V;
   if (base >= p.BN) return;
   const int64_t T = p.T, BN = p.BN;
-  const int64_t K = (T + C - 1) / C;
-  const bool has_gs = (SID != MYELIN_SG_NONE) && p.gs != nullptr;
+  const int64_t Kf = T / C;
+  const int rem = static_cast<int>(T - Kf * C);
 
   float gm[V], ga[V];
   if (p.gmT != nullptr) {
@@ -330,97 +500,51 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
     for (int v = 0; v < V; ++v) ga[v] = 0.0f;
   }
 
-  float xb[C][V];
-  {
-    const int64_t t0 = (K - 1) * C;
+  float xb[C][V], gsb[C][V], pre[C][V], cv[C][V], m[V], a[V];
+  if (rem > 0) {
+    const int64_t t0 = Kf * C;
+    bwd_load_ckpt<ALIF, V>(p, Kf, base, m, a);
 #pragma unroll
     for (int j = 0; j < C; ++j)
-      if (t0 + j < T) ld_stream<V>(xb[j], p.x + (t0 + j) * BN + base);
-  }
-
-  for (int64_t k = K - 1; k >= 0; --k) {
-    const int64_t t0 = k * C;
-    float gsb[C][V];
-    if (has_gs) {
+      if (j < rem) ld_stream<V>(xb[j], p.x + (t0 + j) * BN + base);
+    if constexpr (GS) {
 #pragma unroll
       for (int j = 0; j < C; ++j)
-        if (t0 + j < T) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+        if (j < rem) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
     }
-    float m[V], a[V];
-    ld<V>(m, p.ckpt_m + k * BN + base);
-    if constexpr (ALIF) {
-      ld<V>(a, p.ckpt_a + k * BN + base);
-    } else {
+    bwd_recompute<ALIF, C, SID, V, true>(p, rem, xb, m, a, pre, cv);
+    bwd_reverse<ALIF, C, SID, V, GS, true>(p, base, t0, rem, gsb, pre, cv, gm, ga);
+  }
+  if (Kf > 0) {
+    int64_t k = Kf - 1;
+    bwd_load_ckpt<ALIF, V>(p, k, base, m, a);
 #pragma unroll
-      for (int v = 0; v < V; ++v) a[v] = 0.0f;
-    }
-
-    // recompute the chunk forward
-    float pre[C][V], cv[C][V];
+    for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (k * C + j) * BN + base);
+    for (; k > 0; --k) {
+      const int64_t t0 = k * C;
+      if constexpr (GS) {
 #pragma unroll
-    for (int j = 0; j < C; ++j) {
-      if (t0 + j < T) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          float mp = m[v] * p.decay;
-          mp = mp + xb[j][v];
-          float th = p.thr;
-          if constexpr (ALIF) {
-            float ba = p.beta * a[v];
-            th = p.thr + ba;
-          }
-          // the plain unrolls spike on m' >= th; store c so that c >= 0 is that test
-          const float c = (SID == MYELIN_SG_NONE) ? mp - th : p.slope * (mp - th);
-          const bool s = (SID == MYELIN_SG_NONE) ? (mp >= th) : (c >= 0.0f);
-          pre[j][v] = mp;
-          cv[j][v] = c;
-          m[v] = s ? p.reset : mp;
-          if constexpr (ALIF) {
-            float ra = a[v] * p.rho;
-            a[v] = ra + (s ? 1.0f : 0.0f);
-          }
-        }
+        for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
       }
-    }
-
-    // inputs of the previous chunk (always a full chunk) go in flight now
-    if (k > 0) {
+      // keep the issue order: grad_spikes(k) | recompute(k) | ckpt, x(k-1) |
+      // reverse(k), so the reverse phase waits only for grad_spikes(k) while
+      // the loads of chunk k-1 stay in flight
+      __builtin_amdgcn_sched_barrier(0);
+      bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+      __builtin_amdgcn_sched_barrier(0);
+      bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
 #pragma unroll
       for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
+      __builtin_amdgcn_sched_barrier(0);
+      bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, t0, C, gsb, pre, cv, gm, ga);
+      __builtin_amdgcn_sched_barrier(0);
     }
-
+    if constexpr (GS) {
 #pragma unroll
-    for (int j = C - 1; j >= 0; --j) {
-      if (t0 + j < T) {
-        float g[V];
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          const float c = cv[j][v];
-          const float s = c >= 0.0f ? 1.0f : 0.0f;
-          if constexpr (SID == MYELIN_SG_NONE) {
-            // where(s, reset, m') passes gradient to m' only where s == 0
-            const float gp = s != 0.0f ? 0.0f : gm[v];
-            g[v] = gp;
-            if constexpr (ALIF) ga[v] = ga[v] * p.rho;
-            gm[v] = gp * p.decay;
-          } else {
-            const float dsdm = p.slope * sg_deriv<SID>(c);
-            float q = gm[v] * (p.reset - pre[j][v]);
-            if (has_gs) q = q + gsb[j][v];
-            if constexpr (ALIF) q = q + ga[v];
-            const float gc = q * dsdm;
-            const float gp = gm[v] * (1.0f - s) + gc;
-            g[v] = gp;
-            if constexpr (ALIF) {
-              float r = ga[v] * p.rho;
-              ga[v] = r - p.beta * gc;
-            }
-            gm[v] = gp * p.decay;
-          }
-        }
-        st_stream<V>(p.gx + (t0 + j) * BN + base, g);
-      }
+      for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + j * BN + base);
     }
+    bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+    bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, 0, C, gsb, pre, cv, gm, ga);
   }
   st<V>(p.gm0 + base, gm);
   if constexpr (ALIF) st<V>(p.ga0 + base, ga);
@@ -452,12 +576,22 @@ int launch_fwd(const FwdArgs &a, hipStream_t stream) {
   }
   const int64_t lanes = (a.BN + v - 1) / v;
   const dim3 grid(blocks_for(lanes));
+  constexpr int U = MYELIN_FWD_UNROLL;
+  if (a.ckpt_m != nullptr && a.chunk % U != 0) {
+    if (v == 4)
+      fwd_dense_generic<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
+    else if (v == 2)
+      fwd_dense_generic<ALIF, RULE, 2, U><<<grid, dim3(256), 0, stream>>>(a);
+    else
+      fwd_dense_generic<ALIF, RULE, 1, U><<<grid, dim3(256), 0, stream>>>(a);
+    return myelin::launched("fwd_dense_generic");
+  }
   if (v == 4)
-    fwd_dense<ALIF, RULE, 4, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+    fwd_dense<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
   else if (v == 2)
-    fwd_dense<ALIF, RULE, 2, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+    fwd_dense<ALIF, RULE, 2, U><<<grid, dim3(256), 0, stream>>>(a);
   else
-    fwd_dense<ALIF, RULE, 1, MYELIN_FWD_UNROLL><<<grid, dim3(256), 0, stream>>>(a);
+    fwd_dense<ALIF, RULE, 1, U><<<grid, dim3(256), 0, stream>>>(a);
   return myelin::launched("fwd_dense");
 }
 
@@ -493,10 +627,18 @@ int launch_bwd_sid(const BwdArgs &a, hipStream_t stream) {
     v >>= 1;
   }
   const dim3 grid(blocks_for((a.BN + v - 1) / v));
-  if (v == 2)
-    bwd_chunked<ALIF, C, SID, 2><<<grid, dim3(256), 0, stream>>>(a);
-  else
-    bwd_chunked<ALIF, C, SID, 1><<<grid, dim3(256), 0, stream>>>(a);
+  const bool gs = (SID != MYELIN_SG_NONE) && a.gs != nullptr;
+  if (v == 2) {
+    if (gs)
+      bwd_chunked<ALIF, C, SID, 2, (SID != MYELIN_SG_NONE)><<<grid, dim3(256), 0, stream>>>(a);
+    else
+      bwd_chunked<ALIF, C, SID, 2, false><<<grid, dim3(256), 0, stream>>>(a);
+  } else {
+    if (gs)
+      bwd_chunked<ALIF, C, SID, 1, (SID != MYELIN_SG_NONE)><<<grid, dim3(256), 0, stream>>>(a);
+    else
+      bwd_chunked<ALIF, C, SID, 1, false><<<grid, dim3(256), 0, stream>>>(a);
+  }
   return myelin::launched("bwd_chunked");
 }
 
@@ -524,8 +666,7 @@ int bwd_entry(const BwdArgs &a, int sid, int64_t chunk, hipStream_t stream) {
   switch (chunk) {
     case 8: return launch_bwd_c<ALIF, 8>(a, sid, stream);
     case 16: return launch_bwd_c<ALIF, 16>(a, sid, stream);
-    case 32: return launch_bwd_c<ALIF, 32>(a, sid, stream);
-    default: return myelin::invalid("backward chunk must be 8, 16 or 32; got %lld", (long long)chunk);
+    default: return myelin::invalid("backward chunk must be 8 or 16; got %lld", (long long)chunk);
   }
 }
 

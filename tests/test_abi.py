@@ -38,7 +38,7 @@ def test_validation_errors_are_reported_without_launching():
     rc = lib.myelin_lif_fwd_f32(None, None, None, None, None, None, 0, 1, 1, 0.9, 1.0, 0.0, 10.0, 0, 16, None)
     assert rc == _lib.EINVAL
     assert b"positive" in lib.myelin_last_error()
-    with pytest.raises(ValueError, match="chunk must be 8, 16 or 32"):
+    with pytest.raises(ValueError, match="chunk must be 8 or 16"):
         _lib.call("myelin_lif_bwd_f32", 1, 1, None, None, 1, 1, 4, 4, 0.9, 1.0, 0.0, 10.0, 1, 12, None)
     with pytest.raises(ValueError, match="unknown surrogate"):
         _lib.call("myelin_alif_bwd_f32", 1, 1, 1, None, None, None, 1, 1, 1, 4, 4, 0.9, 0.9, 1.0, 1.8, 0.0,
