@@ -49,6 +49,10 @@ typedef struct ihipStream_t *myelin_stream_t;
  * carry no gradient, functional.py:21-78) */
 #define MYELIN_SG_NONE 6
 
+/* GEMM input precision (accumulation is always fp32) */
+#define MYELIN_PREC_F32 0
+#define MYELIN_PREC_BF16 1 /* inputs rounded to bf16 (nearest even) */
+
 /* element type codes for pack / unpack */
 #define MYELIN_DT_F32 0
 #define MYELIN_DT_F16 1
@@ -174,6 +178,72 @@ int myelin_packed_counts_keep_last(const int32_t *words, int64_t R, int64_t K,
 int myelin_counts_to_rate(const int64_t *counts, void *out, int dtype,
                           int64_t numel, int64_t denominator,
                           myelin_stream_t stream);
+
+/*
+ * C[M,N] = (accumulate ? C : 0) + A(m,k) B(k,n) (+ bias[n]) on MFMA tiles,
+ * fp32 out; bias may be NULL.
+ *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]
+ *   B(k,n) = trans_b ? B[n*ldb + k] : B[k*ldb + n]
+ * precision MYELIN_PREC_F32 or MYELIN_PREC_BF16.  Each output element is
+ * summed by one lane in a fixed k order (deterministic, no atomics).
+ * Replaces: the per-step matmuls of LinearSynapse / the stream functions
+ *   (modules.py:129-133, autograd.py:477-556) and the Triton backward GEMMs
+ *   _linear_surrogate_lif_backward_inputs_kernel / _weight_kernel
+ *   (triton/lif.py:1136-1228).
+ */
+int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C,
+                    int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                    int64_t ldc, int trans_a, int trans_b, int accumulate,
+                    int precision, myelin_stream_t stream);
+
+/*
+ * Streamed synapse fused ahead of the LIF update, over steps
+ * [t_begin, t_end) of x [T, B, F] with W [F, N] (+ bias [N]):
+ *   I_t = x_t @ W + bias ; m' = m*decay + I_t ; s = rule(m') ; m = s ? reset : m'
+ * m0 NULL means a zero initial membrane (the reference's linear paths start
+ * at 0, autograd.py:470-474).  Optional outputs (NULL to skip):
+ *   spikes [T,B,N] fp32 and packed [T,B,ceil(N/32)] at absolute t;
+ *   pre [t_end-t_begin,B,N] pre-reset membranes at relative t;
+ *   rates [B,N] = spike count / T;  ckpt rows every ckpt_every steps from
+ *   t_begin (row 0 = m0);  m_final [B,N].
+ * Replaces: _linear_surrogate_lif_forward_kernel, the checkpoint / packed /
+ *   rate forward kernels and their launchers (triton/lif.py:554-1133), and
+ *   the recompute-chunk kernel (triton/lif.py:1746-1810).
+ */
+int myelin_linear_lif_fwd(const float *x, const float *w, const float *bias,
+                          const float *m0, float *m_final, float *spikes,
+                          float *pre, int32_t *packed, float *rates,
+                          float *ckpt, int64_t T, int64_t B, int64_t F,
+                          int64_t N, int64_t t_begin, int64_t t_end,
+                          int64_t ckpt_every, float decay, float threshold,
+                          float reset, float slope, int rule, int precision,
+                          myelin_stream_t stream);
+
+/*
+ * Reverse recurrence over C steps of a saved pre-reset trace [C, BN]:
+ *   d = slope*sigma'(slope*(pre - thr)); gp = gm*((1-s) + (reset-pre)*d)
+ *   + g_spike*d; G[j] = gp; gm = gp*decay   (grad_m is in/out)
+ * g_spike = grad_spikes[j] (may be NULL) plus grad_rates/T_total (may be
+ * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.
+ * Replaces: the reverse loops of the torch stream / checkpoint / rate
+ *   Functions (autograd.py:540-556,694-715,857-883) and
+ *   _linear_surrogate_lif_checkpoint_backward_chunk_packed_spikes_kernel
+ *   (triton/lif.py:1934-2067).
+ */
+int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
+                          const float *grad_rates, float *grad_m, float *G,
+                          float *gbias_acc, int64_t C, int64_t BN,
+                          int64_t T_total, float decay, float threshold,
+                          float reset, float slope, int surrogate_id, int rule,
+                          myelin_stream_t stream);
+
+/*
+ * out[n] = (accumulate ? out[n] : 0) + sum_r in[r, n], fixed order per
+ * column.  Replaces: _linear_surrogate_lif_backward_bias_kernel
+ *   (triton/lif.py:1231-1258) without its atomics.
+ */
+int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int64_t cols,
+                       int accumulate, myelin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -211,3 +211,111 @@ def _resolve(inputs: torch.Tensor, checkpoint_size: CheckpointSize | None) -> in
     if checkpoint_size is None:
         return None
     return resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
+
+
+def linear_surrogate_lif_forward(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    params: LIFParams,
+    *,
+    surrogate: SurrogateName = "atan",
+    surrogate_slope: float = 10.0,
+    hard_forward: bool = True,
+    backend: Backend = "auto",
+    checkpoint_size: CheckpointSize | None = None,
+    block_b: int = 16,
+    block_n: int = 32,
+    block_f: int = 32,
+    synapse_precision: Literal["fp32", "bf16"] = "fp32",
+) -> tuple[LIFState, torch.Tensor]:
+    """Dense projection streamed through surrogate LIF (kernels.py:395-562).
+
+    ``inputs [T, B, F] @ weight [F, N] (+ bias)`` is computed on MFMA tiles
+    fused ahead of the neuron update; the membrane starts at zero.
+    ``checkpoint_size=None`` saves the pre-reset trace for the backward;
+    an int or policy saves chunk-start membranes and recomputes chunks.
+    ``synapse_precision="bf16"`` rounds the GEMM inputs to bf16 (fp32
+    accumulate); the default keeps the reference's fp32 matmul.
+    """
+
+    from myelin_amd.linear import linear_forward
+
+    sid = surrogate_id(surrogate)
+    _check_backend(backend)
+    if not hard_forward:
+        raise ValueError("HIP linear surrogate LIF currently supports only hard_forward=True")
+    ck = _resolve(inputs, checkpoint_size)
+    m, spikes = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, False, synapse_precision)
+    return LIFState(membrane=m), spikes
+
+
+def linear_surrogate_lif_rate_forward(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    params: LIFParams,
+    *,
+    surrogate: SurrogateName = "atan",
+    surrogate_slope: float = 10.0,
+    hard_forward: bool = True,
+    backend: Backend = "auto",
+    checkpoint_size: CheckpointSize = 25,
+    block_b: int = 16,
+    block_n: int = 32,
+    block_f: int = 32,
+    reduction: Literal["mean", "none"] = "mean",
+    synapse_precision: Literal["fp32", "bf16"] = "fp32",
+) -> tuple[LIFState, torch.Tensor]:
+    """Dense projection + surrogate LIF returning spike rates (kernels.py:565-702).
+
+    The forward keeps spike counts in registers and writes only ``[B, N]``
+    rates and chunk-start membranes: no ``[T, B, N]`` tensor is written.
+    The backward injects ``grad_rates / T`` at every step.
+    """
+
+    from myelin_amd.linear import linear_forward
+
+    sid = surrogate_id(surrogate)
+    _check_backend(backend)
+    if not hard_forward:
+        raise ValueError("HIP spike-rate LIF currently supports only hard_forward=True")
+    if reduction not in ("mean", "none"):
+        raise ValueError("reduction must be 'mean' or 'none'")
+    ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
+    m, rates = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, True, synapse_precision)
+    if reduction == "mean":
+        return LIFState(membrane=m), rates.mean()
+    return LIFState(membrane=m), rates
+
+
+def linear_surrogate_lif_packed_forward(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    params: LIFParams,
+    *,
+    surrogate: SurrogateName = "atan",
+    surrogate_slope: float = 10.0,
+    hard_forward: bool = True,
+    backend: Backend = "auto",
+    checkpoint_size: CheckpointSize = 25,
+    block_b: int = 16,
+    block_f: int = 32,
+    synapse_precision: Literal["fp32", "bf16"] = "fp32",
+) -> tuple[LIFState, PackedSpikes]:
+    """Dense projection + LIF writing bitpacked spikes only (kernels.py:705-776).
+
+    Forward-only, like the reference: a wave ballot packs 64 neurons per step
+    straight from the fused kernel, so dense spikes are never written.
+    """
+
+    from myelin_amd.linear import linear_packed_forward
+
+    surrogate_id(surrogate)
+    _check_backend(backend)
+    if not hard_forward:
+        raise ValueError("HIP packed surrogate LIF currently supports only hard_forward=True")
+    ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
+    m, packed = linear_packed_forward(inputs, weight, bias, params, ck, synapse_precision)
+    return LIFState(membrane=m), packed

@@ -1,0 +1,242 @@
+"""Autograd boundary of the streamed-synapse LIF path (``x_t @ W`` fused ahead
+of the neuron update).
+
+Forward: one launch of ``myelin_linear_lif_fwd`` computes every step's
+current tile on MFMA and runs the recurrence in the same workgroup.
+
+Saved state:
+* ``checkpoint_size=None`` (the reference's stream Function,
+  autograd.py:445-558): the pre-reset membranes ``[T, B, N]`` -- one tensor
+  where the reference keeps pre-reset membranes and spikes;
+* ``checkpoint_size=C`` (autograd.py:588-717) and the rate readout
+  (autograd.py:753-885): chunk-start membranes every C steps only.
+
+Backward, per chunk in reverse time: recompute the chunk's pre-reset trace
+(fused kernel from the chunk-start membrane; skipped for the stream path),
+reverse recurrence -> G = dL/dI ``[C, B, N]`` plus per-(b, n) bias partials,
+then ``dX[t] = G_t @ W^T`` and ``dW += X_t^T G_t`` on MFMA GEMMs,
+``db = sum_b`` of the bias partials.  Every reduction has a fixed order, so
+gradients are run-to-run deterministic (the reference's Triton path uses
+fp32 atomics, triton/lif.py:1336-1348).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from myelin_amd import _lib
+
+
+def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None):
+    _lib.call("myelin_gemm_f32", _lib.ptr(A), _lib.ptr(B), _lib.ptr(bias), _lib.ptr(C), M, N, K, lda, ldb, ldc,
+              int(trans_a), int(trans_b), int(accumulate), prec, stream)
+
+
+class HipLinearFunction(torch.autograd.Function):
+    """``inputs @ weight + bias`` on the MFMA GEMM (LinearSynapse, modules.py:112-133).
+
+    Backward: ``dX = dY W^T``, ``dW = X^T dY``, ``db = sum over rows of dY``.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, x, w, b, prec):
+        F, N = w.shape
+        x2 = x.reshape(-1, F)
+        M = x2.shape[0]
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+        _gemm(x2, w, out, M, N, F, F, N, N, False, False, False, prec, _lib.stream(x.device), bias=b)
+        ctx.prec = prec
+        ctx.has_b = b is not None
+        ctx.save_for_backward(x2, w)
+        ctx.in_shape = x.shape
+        return out.reshape(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx: Any, gy):
+        x2, w = ctx.saved_tensors
+        F, N = w.shape
+        M = x2.shape[0]
+        gy2 = gy.float().reshape(M, N).contiguous()
+        dev = x2.device
+        gx = gw = gb = None
+        with torch.cuda.device(dev):
+            stream = _lib.stream(dev)
+            if ctx.needs_input_grad[0]:
+                gx = torch.empty((M, F), dtype=x2.dtype, device=dev)
+                _gemm(gy2, w, gx, M, F, N, N, N, F, False, True, False, ctx.prec, stream)
+                gx = gx.reshape(ctx.in_shape)
+            if ctx.needs_input_grad[1]:
+                gw = torch.empty_like(w)
+                _gemm(x2, gy2, gw, F, N, M, F, N, N, True, False, False, ctx.prec, stream)
+            if ctx.has_b and ctx.needs_input_grad[2]:
+                gb = torch.empty((N,), dtype=x2.dtype, device=dev)
+                _lib.call("myelin_col_sum_f32", _lib.ptr(gy2), _lib.ptr(gb), M, N, 0, stream)
+        return gx, gw, gb, None
+
+
+def linear(x, w, b, precision: str = "fp32"):
+    """Differentiable ``x @ w + b`` for ``x [..., F]``, ``w [F, N]`` on the HIP GEMM."""
+
+    _lib.require_device(x, "inputs")
+    if x.dtype != torch.float32 or w.dtype != torch.float32:
+        raise ValueError("inputs and weight must be float32 for the HIP path")
+    if x.shape[-1] != w.shape[0]:
+        raise ValueError("inputs.shape[-1] must match weight.shape[0]")
+    with torch.cuda.device(x.device):
+        return HipLinearFunction.apply(x.contiguous(), w.contiguous(), None if b is None else b.contiguous(),
+                                       _lib.PREC[precision])
+
+
+class HipLinearLIFFunction(torch.autograd.Function):
+    """Outputs ``(final_membrane, spikes)`` or, with ``rate=True``,
+    ``(final_membrane, rates)`` where ``rates = spike_count / T``."""
+
+    @staticmethod
+    def forward(ctx: Any, x, w, b, decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule):
+        T, B, F = x.shape
+        N = w.shape[1]
+        dev = x.device
+        stream = _lib.stream(dev)
+        need = any(ctx.needs_input_grad[:3])
+        m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
+        out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
+        pre = ckpt = None
+        if need:
+            if checkpoint is None:
+                pre = torch.empty((T, B, N), dtype=x.dtype, device=dev)
+            else:
+                ckpt = torch.empty((math.ceil(T / checkpoint), B, N), dtype=x.dtype, device=dev)
+        _lib.call(
+            "myelin_linear_lif_fwd",
+            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), None, _lib.ptr(m_final),
+            None if rate else _lib.ptr(out), _lib.ptr(pre), None, _lib.ptr(out) if rate else None, _lib.ptr(ckpt),
+            T, B, F, N, 0, T, checkpoint or 1, decay, threshold, reset, slope, rule, prec, stream,
+        )
+        ctx.set_materialize_grads(False)
+        ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
+        if need:
+            ctx.save_for_backward(x, w, b, pre, ckpt)
+        return m_final, out
+
+    @staticmethod
+    def backward(ctx: Any, g_m, g_out):
+        none = (None,) * 12
+        if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
+            return none
+        decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
+        x, w, b, pre, ckpt = ctx.saved_tensors
+        T, B, F = x.shape
+        N = w.shape[1]
+        BN = B * N
+        dev = x.device
+        need_x, need_w, need_b = ctx.needs_input_grad[:3]
+        with torch.cuda.device(dev):
+            stream = _lib.stream(dev)
+            gm = g_m.float().contiguous().clone() if g_m is not None else torch.zeros((B, N), device=dev)
+            g_out = None if g_out is None else g_out.float().contiguous()
+            g_spikes = None if rate else g_out
+            g_rates = g_out if rate else None
+            gx = torch.empty_like(x) if need_x else None
+            gw = torch.zeros_like(w) if need_w else None
+            gb_acc = torch.zeros((B, N), device=dev) if (need_b and has_b) else None
+            chunk = T if checkpoint is None else checkpoint
+            G = torch.empty((min(chunk, T), B, N), device=dev)
+            scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
+            n_chunks = math.ceil(T / chunk)
+            for k in range(n_chunks - 1, -1, -1):
+                t0 = k * chunk
+                t1 = min(t0 + chunk, T)
+                C = t1 - t0
+                if checkpoint is None:
+                    pre_k = pre
+                else:
+                    _lib.call(
+                        "myelin_linear_lif_fwd",
+                        _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(ckpt[k]), None, None,
+                        _lib.ptr(scratch), None, None, None,
+                        T, B, F, N, t0, t1, 1, decay, threshold, reset, slope, rule, prec, stream,
+                    )
+                    pre_k = scratch
+                _lib.call(
+                    "myelin_linear_pre_bwd",
+                    _lib.ptr(pre_k), _lib.ptr(g_spikes[t0:t1]) if g_spikes is not None else None,
+                    _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.ptr(gb_acc),
+                    C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
+                )
+                rows = C * B
+                if gx is not None:
+                    # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
+                    _gemm(G, w, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
+                if gw is not None:
+                    # dW += X[t0:t1]^T @ G : [F, rows] x [rows, N]
+                    _gemm(x[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
+            gb = None
+            if gb_acc is not None:
+                gb = torch.empty((N,), device=dev)
+                _lib.call("myelin_col_sum_f32", _lib.ptr(gb_acc), _lib.ptr(gb), B, N, 0, stream)
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None
+
+
+def linear_forward(x, w, b, params, surrogate_id: int, slope: float, checkpoint, rate: bool, precision: str,
+                   rule: int = _lib.RULE_THRESHOLD):
+    """Validate and run the fused streamed-synapse LIF (shared by the public
+    entry points in myelin_amd.kernels)."""
+
+    if x.ndim != 3:
+        raise ValueError(f"inputs must be shaped [T, B, F]; got {tuple(x.shape)}")
+    if w.ndim != 2:
+        raise ValueError(f"weight must be shaped [F, N]; got {tuple(w.shape)}")
+    _lib.require_device(x, "inputs")
+    if w.device != x.device or w.dtype != x.dtype:
+        raise ValueError("weight must have the same device and dtype as inputs")
+    if x.shape[2] != w.shape[0]:
+        raise ValueError("inputs.shape[2] must match weight.shape[0]")
+    if b is not None:
+        if b.shape != (w.shape[1],):
+            raise ValueError("bias must be shaped [N]")
+        if b.device != x.device or b.dtype != x.dtype:
+            raise ValueError("bias must have the same device and dtype as inputs")
+    if x.dtype != torch.float32:
+        raise ValueError(f"inputs must be float32 for the HIP path; got {x.dtype}")
+    if x.shape[0] == 0:
+        raise ValueError("inputs must have at least one timestep")
+    if precision not in _lib.PREC:
+        raise ValueError("synapse_precision must be 'fp32' or 'bf16'")
+    with torch.cuda.device(x.device):
+        return HipLinearLIFFunction.apply(
+            x.contiguous(), w.contiguous(), None if b is None else b.contiguous(), float(params.decay),
+            float(params.threshold), float(params.reset), surrogate_id, float(slope), checkpoint, rate,
+            _lib.PREC[precision], rule,
+        )
+
+
+def linear_packed_forward(x, w, b, params, checkpoint: int, precision: str):
+    """Forward-only packed-spike output (no dense [T, B, N] spikes)."""
+
+    from myelin_amd.packing import PackedSpikes, packed_last_dim_size
+
+    if x.ndim != 3:
+        raise ValueError(f"inputs must be shaped [T, B, F]; got {tuple(x.shape)}")
+    _lib.require_device(x, "inputs")
+    if x.shape[2] != w.shape[0]:
+        raise ValueError("inputs.shape[2] must match weight.shape[0]")
+    if x.dtype != torch.float32 or w.dtype != torch.float32:
+        raise ValueError("inputs and weight must be float32 for the HIP path")
+    x = x.contiguous()
+    w = w.contiguous()
+    b = None if b is None else b.contiguous()
+    T, B, F = x.shape
+    N = w.shape[1]
+    m_final = torch.empty((B, N), device=x.device)
+    words = torch.empty((T, B, packed_last_dim_size(N)), dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call(
+            "myelin_linear_lif_fwd",
+            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), None, _lib.ptr(m_final), None, None, _lib.ptr(words), None, None,
+            T, B, F, N, 0, T, checkpoint, float(params.decay), float(params.threshold), float(params.reset), 10.0,
+            _lib.RULE_THRESHOLD, _lib.PREC[precision], _lib.stream(x.device),
+        )
+    return m_final, PackedSpikes(data=words, original_shape=(T, B, N))
