@@ -8,6 +8,20 @@ dL/ds ~ N(0, 1).  One step = the public-API forward
 in HBM.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+
+``--workload`` selects one of the other synthetic configurations instead of
+the headline (each prints its own JSON line with its own roofline):
+  lif_fwd         LIF forward [100, 64, 1024], tau 10, hard reset (8 input
+                  buffers rotated so the 52 MB working set is not served from
+                  the 256 MB Infinity Cache)
+  linear_bf16     one training step: LinearSurrogateLIF(784 -> 2048,
+                  stream_synapse, atan, bf16 GEMM) + LinearSurrogateLIFRate
+                  (2048 -> 10, atan, C=25), CE on spike counts, [50, 256, 784]
+  long_rate       one training step: LinearSurrogateLIF(1024 -> 4096,
+                  checkpoint "memory", superspike, fp32) + rate readout
+                  (4096 -> 20), CE, [2000, 32, 1024]; reports peak HBM bytes
+  bitpack         pack [512, 64, 8192] spikes, unpack, per-neuron counts over
+                  T, per-sample rates
 """
 
 from __future__ import annotations
@@ -36,6 +50,8 @@ def _args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--workload", default="alif_headline",
+                    choices=["alif_headline", "lif_fwd", "linear_bf16", "long_rate", "bitpack"])
     ap.add_argument("--cpu-sample-batch", type=int, default=128)
     ap.add_argument("--cpu-min-seconds", type=float, default=10.0)
     ap.add_argument(
@@ -125,6 +141,159 @@ def _cpu_baseline(torch, sample_b: int, min_seconds: float):
     }
 
 
+def _timed(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _line(metric, value, unit, ms, args, config, **extra):
+    out = {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic", "config": config,
+    }
+    out.update(extra)
+    return out
+
+
+def _workload_lif_fwd(torch, myelin, args):
+    Tl, Bl, Nl = 100, 64, 1024
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    xs = [(0.3 + 0.5 * torch.randn(Tl, Bl, Nl, generator=g)).to(dev) for _ in range(8)]
+    m0 = myelin.LIFState(torch.zeros(Bl, Nl, device=dev))
+    p = myelin.LIFParams(10.0, 1.0, 0.0)
+    it = [0]
+
+    def step():
+        myelin.lif_forward(xs[it[0] % 8], m0, p)
+        it[0] += 1
+
+    ms = _timed(torch, step, args.steps, args.warmup)
+    E = Tl * Bl * Nl
+    gbps = 8 * E / (ms * 1e-3) / 1e9
+    return _line("neuron-steps/sec LIF forward", E / (ms * 1e-3), "neuron-steps/s", ms, args,
+                 {"workload": "lif_forward, hard reset", "T": Tl, "B": Bl, "N": Nl, "tau_mem": 10.0,
+                  "x": "N(0.3, 0.5)", "rotated_input_buffers": 8},
+                 roofline={"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                           "frac": gbps / HBM_PEAK_GBPS, "traffic": None,
+                           "note": "step time includes the Python launch path (52 MB per step)"})
+
+
+def _workload_linear_bf16(torch, myelin, args):
+    Tl, Bl, F, H, O = 50, 256, 784, 2048, 10
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    rate_f = torch.rand(F, generator=g) * 0.2
+    x = (torch.rand(Tl, Bl, F, generator=g) < rate_f).float().to(dev)
+    labels = torch.randint(0, O, (Bl,), generator=g).to(dev)
+    torch.manual_seed(3)
+    hidden = myelin.LinearSurrogateLIF(F, H, surrogate=myelin.atan_surrogate, stream_synapse=True,
+                                       synapse_precision="bf16")
+    readout = myelin.LinearSurrogateLIFRate(H, O, surrogate=myelin.atan_surrogate, checkpoint_size=25,
+                                            synapse_precision="bf16")
+    for mod, fan in ((hidden, F), (readout, H)):
+        wt = torch.empty(mod.synapse.weight.shape[1], fan)
+        torch.nn.init.kaiming_uniform_(wt)  # a=0: bound sqrt(6 / fan_in)
+        with torch.no_grad():
+            mod.synapse.weight.copy_(wt.t())
+    hidden.to(dev)
+    readout.to(dev)
+    params = list(hidden.parameters()) + list(readout.parameters())
+
+    def step():
+        for q in params:
+            q.grad = None
+        rates = readout(hidden(x))
+        loss = torch.nn.functional.cross_entropy(rates * Tl, labels)
+        loss.backward()
+
+    ms = _timed(torch, step, args.steps, args.warmup)
+    flops = 2 * Tl * Bl * F * H * 2 + 4 * 2 * Tl * Bl * H * O
+    tflops = flops / (ms * 1e-3) / 1e12
+    E = Tl * Bl * H
+    return _line("neuron-steps/sec, streamed-synapse training step", E / (ms * 1e-3), "neuron-steps/s", ms, args,
+                 {"workload": "LinearSurrogateLIF(784->2048, stream_synapse, atan, bf16) + "
+                              "LinearSurrogateLIFRate(2048->10, atan, C=25) + CE, fwd+bwd",
+                  "T": Tl, "B": Bl, "F": F, "N": H, "readout": O, "gflop_per_step": flops / 1e9},
+                 roofline={"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
+                           "frac": tflops / 2500.0, "traffic": None,
+                           "note": "whole training step (all kernels) against dense bf16 MFMA peak"},
+                 dtype="bf16")
+
+
+def _workload_long_rate(torch, myelin, args):
+    Tl, Bl, F, H, O = 2000, 32, 1024, 4096, 20
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(4)
+    x = (torch.rand(Tl, Bl, F, generator=g) < 0.05).float().to(dev)
+    labels = torch.randint(0, O, (Bl,), generator=g).to(dev)
+    torch.manual_seed(4)
+    hidden = myelin.LinearSurrogateLIF(F, H, surrogate=myelin.superspike_surrogate, stream_synapse=True,
+                                       checkpoint_size="memory").to(dev)
+    readout = myelin.LinearSurrogateLIFRate(H, O, surrogate=myelin.superspike_surrogate,
+                                            checkpoint_size="memory").to(dev)
+    params = list(hidden.parameters()) + list(readout.parameters())
+
+    def step():
+        for q in params:
+            q.grad = None
+        rates = readout(hidden(x))
+        torch.nn.functional.cross_entropy(rates * Tl, labels).backward()
+
+    step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    ms = _timed(torch, step, max(1, args.steps // 5), 1)
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    flops = 3 * 2 * Tl * Bl * F * H + 4 * 2 * Tl * Bl * H * O
+    tflops = flops / (ms * 1e-3) / 1e12
+    E = Tl * Bl * H
+    return _line("neuron-steps/sec, long-horizon checkpointed rate training step", E / (ms * 1e-3),
+                 "neuron-steps/s", ms, args,
+                 {"workload": "LinearSurrogateLIF(1024->4096, stream_synapse, checkpoint 'memory'=45, superspike, "
+                              "fp32) + LinearSurrogateLIFRate(4096->20, 'memory') + CE, fwd+bwd",
+                  "T": Tl, "B": Bl, "F": F, "N": H, "readout": O, "gflop_per_step": flops / 1e9},
+                 roofline={"bound": "mfma", "achieved": tflops, "peak": 157.3, "unit": "TFLOP/s",
+                           "frac": tflops / 157.3, "traffic": None,
+                           "note": "whole training step against dense fp32 MFMA peak"},
+                 peak_step_bytes=peak, dense_hidden_spike_bytes=Tl * Bl * H * 4)
+
+
+def _workload_bitpack(torch, myelin, args):
+    Tl, Bl, Nl = 512, 64, 8192
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    rate = torch.exp(-3.0 + torch.randn(Nl, generator=g)).clamp(0.0, 1.0)
+    gd = torch.Generator(device=dev).manual_seed(5)
+    s = (torch.rand((Tl, Bl, Nl), generator=gd, device=dev) < rate.to(dev)).float()
+    pk = myelin.pack_spikes(s)
+    E = Tl * Bl * Nl
+    times = {}
+    for name, fn in (("pack", lambda: myelin.pack_spikes(s)), ("unpack", lambda: myelin.unpack_spikes(pk)),
+                     ("count_dim0", lambda: myelin.packed_spike_count(pk, dim=0)),
+                     ("rate_dim0_last", lambda: myelin.packed_spike_rate(pk, dim=(0, -1)))):
+        times[name] = _timed(torch, fn, args.steps, args.warmup)
+    ms = sum(times.values())
+    byte_model = {"pack": 4.125 * E, "unpack": 4.125 * E, "count_dim0": E / 8 + Bl * Nl * 8,
+                  "rate_dim0_last": E / 8}
+    gbps = {k: byte_model[k] / (times[k] * 1e-3) / 1e9 for k in times}
+    return _line("spikes/sec, pack + unpack + counts + rates", E / (ms * 1e-3), "spikes/s", ms, args,
+                 {"workload": "bitpack [512, 64, 8192], Bernoulli(LogNormal(-3, 1) clipped)", "T": Tl, "B": Bl,
+                  "N": Nl},
+                 roofline={"bound": "hbm", "achieved": gbps["pack"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                           "frac": gbps["pack"] / HBM_PEAK_GBPS, "traffic": None, "kernel": "pack"},
+                 kernels={f"{k}_ms": v for k, v in times.items()} | {f"{k}_GBps": v for k, v in gbps.items()},
+                 dtype="u8")
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -140,6 +309,11 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    others = {"lif_fwd": _workload_lif_fwd, "linear_bf16": _workload_linear_bf16, "long_rate": _workload_long_rate,
+              "bitpack": _workload_bitpack}
+    if args.workload in others:
+        print(json.dumps(others[args.workload](torch, myelin, args)), flush=True)
+        return 0
     g = torch.Generator().manual_seed(2)
     x = (0.25 + 0.6 * torch.randn(T, B, N, generator=g)).to(dev)
     gs = torch.randn(T, B, N, generator=g).to(dev)

@@ -185,7 +185,10 @@ int myelin_counts_to_rate(const int64_t *counts, void *out, int dtype,
  *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]
  *   B(k,n) = trans_b ? B[n*ldb + k] : B[k*ldb + n]
  * precision MYELIN_PREC_F32 or MYELIN_PREC_BF16.  Each output element is
- * summed by one lane in a fixed k order (deterministic, no atomics).
+ * summed by one lane in a fixed k order (deterministic, no atomics).  When
+ * the output has few 64x64 tiles and K is long, K is split across
+ * workgroups: partial tiles go to `workspace` (workspace_elems floats; 0 or
+ * NULL disables splitting) and are added in split order.
  * Replaces: the per-step matmuls of LinearSynapse / the stream functions
  *   (modules.py:129-133, autograd.py:477-556) and the Triton backward GEMMs
  *   _linear_surrogate_lif_backward_inputs_kernel / _weight_kernel
@@ -194,7 +197,8 @@ int myelin_counts_to_rate(const int64_t *counts, void *out, int dtype,
 int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C,
                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, int trans_a, int trans_b, int accumulate,
-                    int precision, myelin_stream_t stream);
+                    int precision, float *workspace, int64_t workspace_elems,
+                    myelin_stream_t stream);
 
 /*
  * Streamed synapse fused ahead of the LIF update, over steps

@@ -49,7 +49,7 @@ SIGNATURES: dict[str, list] = {
     "myelin_packed_counts": [_P, _INT, _P, ctypes.c_uint32, _I64, _P, _P],
     "myelin_packed_counts_keep_last": [_P, _I64, _I64, _I64, _P, _P],
     "myelin_counts_to_rate": [_P, _P, _INT, _I64, _I64, _P],
-    "myelin_gemm_f32": [_P, _P, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P],
+    "myelin_gemm_f32": [_P, _P, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P],
     "myelin_linear_lif_fwd": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_linear_pre_bwd": [_P] * 6 + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],

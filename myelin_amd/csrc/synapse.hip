@@ -28,31 +28,30 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTile = 64;  // output tile edge
-constexpr int kChunk = 8;  // timesteps per fused chunk
-constexpr int kBt = 8;     // batch rows per fused workgroup (kChunk * kBt == kTile)
 
 template <int PREC>
 struct Prec;
 template <>
 struct Prec<0> {  // fp32 MFMA
   using T = float;
-  static constexpr int KS = 16;  // k per LDS stage
+  static constexpr int KS = 32;  // k per LDS stage
   static constexpr int KV = 1;   // k per lane per MFMA
   static constexpr int KM = 2;   // k per MFMA
+  static constexpr int PAD = 1;
 };
 template <>
 struct Prec<1> {  // bf16 MFMA, fp32 accumulate
   using T = __bf16;
-  static constexpr int KS = 32;
+  static constexpr int KS = 64;
   static constexpr int KV = 8;
   static constexpr int KM = 16;
+  static constexpr int PAD = 8;
 };
 
 template <int PREC>
 struct Stage {
   using T = typename Prec<PREC>::T;
-  static constexpr int KS = Prec<PREC>::KS;
-  static constexpr int LD = KS + (PREC == 1 ? 8 : 1);  // padded row length (elements)
+  static constexpr int LD = Prec<PREC>::KS + Prec<PREC>::PAD;  // padded row length (elements)
   alignas(16) T a[kTile][LD];
   alignas(16) T b[kTile][LD];
 };
@@ -85,80 +84,215 @@ __device__ __forceinline__ void mfma_stage(const Stage<PREC> &st, int wm, int wn
 // row index (within the wave's 32 x 32 quarter) of accumulator register r
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Stages one operand tile (64 rows x KS k) from global memory through
+// registers into LDS.  Each thread owns NV float4 pieces.
+//  KCONTIG: rows are k-contiguous in memory (base[e] = start of the row, or
+//           null for a padding row); piece e covers k = koff[e] .. +3 of LDS
+//           row roff[e].
+//  otherwise: the 64 rows are contiguous along memory for a fixed k (stride
+//           ld between k); piece e covers rows roff[e] .. +3 at k = koff[e];
+//           nvalid[e] of those rows exist.
+// VEC: 16-byte aligned pieces may be loaded as one float4.
+template <int PREC, bool KCONTIG, bool VEC>
+struct TileLoader {
+  static constexpr int KS = Prec<PREC>::KS;
+  static constexpr int NV = KS * kTile / 1024;
+  const float *base[NV];
+  int koff[NV], roff[NV], nvalid[NV];
+  int64_t ld;
+  float v[NV][4];
+
+  // KCONTIG piece mapping for thread tid; the caller fills base[e] from row r = roff[e]
+  __device__ __forceinline__ void map_kcontig(int tid) {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int idx = e * 256 + tid;
+      roff[e] = idx / (KS / 4);
+      koff[e] = 4 * (idx % (KS / 4));
+      nvalid[e] = 4;
+    }
+  }
+  // row-contiguous mapping: rows [row0, row0 + 64) of a [K x rows] array
+  __device__ __forceinline__ void map_rowcontig(int tid, const float *ptr, int64_t row0, int64_t rows, int64_t ld_) {
+    ld = ld_;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int idx = e * 256 + tid;
+      koff[e] = idx / 16;
+      roff[e] = 4 * (idx % 16);
+      const int64_t left = rows - (row0 + roff[e]);
+      nvalid[e] = left <= 0 ? 0 : (left >= 4 ? 4 : static_cast<int>(left));
+      base[e] = ptr + row0 + roff[e];
+    }
+  }
+
+  __device__ __forceinline__ void load(int64_t k0, int64_t kend) {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      v[e][0] = v[e][1] = v[e][2] = v[e][3] = 0.0f;
+      if constexpr (KCONTIG) {
+        const int64_t k = k0 + koff[e];
+        if (base[e] != nullptr && k < kend) {
+          const float *q = base[e] + k;
+          if (VEC && k + 3 < kend) {
+            const f4 t = *reinterpret_cast<const f4 *>(q);
+            v[e][0] = t.x;
+            v[e][1] = t.y;
+            v[e][2] = t.z;
+            v[e][3] = t.w;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k + i < kend) v[e][i] = q[i];
+          }
+        }
+      } else {
+        const int64_t k = k0 + koff[e];
+        if (k < kend && nvalid[e] > 0) {
+          const float *q = base[e] + k * ld;
+          if (VEC && nvalid[e] == 4) {
+            const f4 t = *reinterpret_cast<const f4 *>(q);
+            v[e][0] = t.x;
+            v[e][1] = t.y;
+            v[e][2] = t.z;
+            v[e][3] = t.w;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (i < nvalid[e]) v[e][i] = q[i];
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[Stage<PREC>::LD]) const {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (KCONTIG)
+          dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
+        else
+          dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+      }
+    }
+  }
+};
+
+// acc += A[64 x (kb..ke)] B[(kb..ke) x 64], software-pipelined: the next
+// stage's global loads are in flight while the current stage runs on MFMA
+// from the other LDS buffer (one barrier per stage).
+template <int PREC, class LA, class LB>
+__device__ __forceinline__ void tile_mma(LA &la, LB &lb, int64_t kb, int64_t ke, Stage<PREC> (&st)[2], int wm,
+                                         int wn, int lane, f32x16 &acc) {
+  constexpr int KS = Prec<PREC>::KS;
+  if (kb >= ke) return;
+  la.load(kb, ke);
+  lb.load(kb, ke);
+  la.store(st[0].a);
+  lb.store(st[0].b);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t k0 = kb; k0 < ke; k0 += KS) {
+    const bool more = k0 + KS < ke;
+    if (more) {
+      la.load(k0 + KS, ke);
+      lb.load(k0 + KS, ke);
+    }
+    mfma_stage<PREC>(st[buf], wm, wn, lane, acc);
+    if (more) {
+      la.store(st[buf ^ 1].a);
+      lb.store(st[buf ^ 1].b);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Plain GEMM: C[M,N] (+)= A(m,k) B(k,n), fp32 in and out.
+// Plain GEMM: C[M,N] (+)= A(m,k) B(k,n) (+ bias[n]), fp32 in and out.
 //   A(m,k) = TA ? A[k*lda + m] : A[m*lda + k]
 //   B(k,n) = TB ? B[n*ldb + k] : B[k*ldb + n]
+// gridDim.z > 1 splits K: each split writes its partial tile to the
+// workspace and splitk_reduce adds them in split order (deterministic).
 // ---------------------------------------------------------------------------
 struct GemmArgs {
   const float *A;
   const float *B;
   const float *bias;  // [N] added in the epilogue, or null
   float *C;
-  int64_t M, N, K, lda, ldb, ldc;
-  int accumulate;
+  float *ws;          // [splits, M, N] when split
+  int64_t M, N, K, lda, ldb, ldc, kchunk;
+  int accumulate, splits;
 };
 
-template <int PREC, bool TA, bool TB>
+template <int PREC, bool TA, bool TB, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  constexpr int KS = Prec<PREC>::KS;
-  __shared__ Stage<PREC> st;
+  __shared__ Stage<PREC> st[2];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTile, n0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int64_t kb = static_cast<int64_t>(blockIdx.z) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+
+  TileLoader<PREC, !TA, VEC> la;
+  if constexpr (TA) {
+    la.map_rowcontig(tid, g.A, m0, g.M, g.lda);
+  } else {
+    la.map_kcontig(tid);
+#pragma unroll
+    for (int e = 0; e < TileLoader<PREC, true, VEC>::NV; ++e) {
+      const int64_t m = m0 + la.roff[e];
+      la.base[e] = m < g.M ? g.A + m * g.lda : nullptr;
+    }
+  }
+  TileLoader<PREC, TB, VEC> lb;
+  if constexpr (TB) {
+    lb.map_kcontig(tid);
+#pragma unroll
+    for (int e = 0; e < TileLoader<PREC, true, VEC>::NV; ++e) {
+      const int64_t n = n0 + lb.roff[e];
+      lb.base[e] = n < g.N ? g.B + n * g.ldb : nullptr;
+    }
+  } else {
+    lb.map_rowcontig(tid, g.B, n0, g.N, g.ldb);
+  }
+
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  tile_mma<PREC>(la, lb, kb, ke, st, wm, wn, lane, acc);
 
-  for (int64_t k0 = 0; k0 < g.K; k0 += KS) {
-    // stage A and B (kTile * KS elements each, KS*kTile/256 per thread)
-#pragma unroll
-    for (int e = 0; e < kTile * KS / 256; ++e) {
-      const int idx = e * 256 + tid;
-      int row, kk;
-      if constexpr (TA) {  // memory is k-major: consecutive threads take consecutive m
-        kk = idx / kTile;
-        row = idx % kTile;
-      } else {
-        row = idx / KS;
-        kk = idx % KS;
-      }
-      const int64_t m = m0 + row, k = k0 + kk;
-      float v = 0.0f;
-      if (m < g.M && k < g.K) v = TA ? g.A[k * g.lda + m] : g.A[m * g.lda + k];
-      st.a[row][kk] = cvt<PREC>(v);
-    }
-#pragma unroll
-    for (int e = 0; e < kTile * KS / 256; ++e) {
-      const int idx = e * 256 + tid;
-      int col, kk;
-      if constexpr (TB) {  // memory is n-major with k contiguous
-        col = idx / KS;
-        kk = idx % KS;
-      } else {
-        kk = idx / kTile;
-        col = idx % kTile;
-      }
-      const int64_t n = n0 + col, k = k0 + kk;
-      float v = 0.0f;
-      if (n < g.N && k < g.K) v = TB ? g.B[n * g.ldb + k] : g.B[k * g.ldb + n];
-      st.b[col][kk] = cvt<PREC>(v);
-    }
-    __syncthreads();
-    mfma_stage<PREC>(st, wm, wn, lane, acc);
-    __syncthreads();
-  }
   const int64_t col = n0 + 32 * wn + (lane & 31);
   if (col >= g.N) return;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t row = m0 + 32 * wm + acc_row(r, lane);
-    if (row < g.M) {
+    if (row >= g.M) continue;
+    if (g.splits > 1) {
+      g.ws[(static_cast<int64_t>(blockIdx.z) * g.M + row) * g.N + col] = acc[r];
+    } else {
       float *dst = g.C + row * g.ldc + col;
       float v = g.accumulate ? *dst + acc[r] : acc[r];
       if (g.bias != nullptr) v = v + g.bias[col];
       *dst = v;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= g.M * g.N) return;
+  const int64_t row = i / g.N, col = i - row * g.N;
+  float *dst = g.C + row * g.ldc + col;
+  float v = g.accumulate ? *dst : 0.0f;
+  float part = 0.0f;
+  for (int z = 0; z < g.splits; ++z) part = part + g.ws[static_cast<int64_t>(z) * g.M * g.N + i];
+  v = v + part;
+  if (g.bias != nullptr) v = v + g.bias[col];
+  *dst = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -180,28 +314,26 @@ struct LinArgs {
   int rule;
 };
 
-template <int PREC>
-struct FusedSmem {
-  Stage<PREC> st;
-  alignas(16) float cur[kTile][kTile + 1];  // currents [row = j*kBt + bb][col]
-};
-
-template <int PREC>
+// BT batch rows x 64 neurons per workgroup, 64/BT timesteps per chunk
+// (GEMM rows r = j*BT + bb).  Wave w owns batch rows bb = w*Q .. w*Q+Q-1
+// (Q = BT/4) of the recurrence; lane = neuron.
+template <int PREC, int BT, bool VEC>
 __global__ __launch_bounds__(256) void linear_lif_fwd(LinArgs p) {
-  constexpr int KS = Prec<PREC>::KS;
-  __shared__ FusedSmem<PREC> sm;
+  constexpr int CH = kTile / BT;
+  constexpr int Q = BT / 4;
+  __shared__ Stage<PREC> st[2];
+  __shared__ float cur[kTile][kTile + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kBt, n0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * BT, n0 = static_cast<int64_t>(blockIdx.x) * kTile;
   const int64_t BN = p.B * p.N;
 
-  // recurrence ownership: wave w owns batch rows bb = 2w, 2w+1; lane = neuron
   const int64_t n = n0 + lane;
-  float m[2], cnt[2];
-  bool act[2];
-  int64_t flat[2];
+  float m[Q], cnt[Q];
+  bool act[Q];
+  int64_t flat[Q];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int64_t b = b0 + 2 * w + q;
+  for (int q = 0; q < Q; ++q) {
+    const int64_t b = b0 + Q * w + q;
     act[q] = (b < p.B) && (n < p.N);
     flat[q] = b * p.N + n;
     m[q] = (act[q] && p.m0 != nullptr) ? p.m0[flat[q]] : 0.0f;
@@ -210,56 +342,44 @@ __global__ __launch_bounds__(256) void linear_lif_fwd(LinArgs p) {
   const float bias_n = (p.bias != nullptr && n < p.N) ? p.bias[n] : 0.0f;
   int64_t next_ck = p.t_begin, ck_row = 0;
 
-  for (int64_t t0 = p.t_begin; t0 < p.t_end; t0 += kChunk) {
+  TileLoader<PREC, false, VEC> lb;  // W [F, N]: rows of the B tile are neurons, contiguous for a fixed k
+  lb.map_rowcontig(tid, p.w, n0, p.N, p.N);
+  TileLoader<PREC, true, VEC> la;
+  la.map_kcontig(tid);
+
+  for (int64_t t0 = p.t_begin; t0 < p.t_end; t0 += CH) {
+#pragma unroll
+    for (int e = 0; e < TileLoader<PREC, true, VEC>::NV; ++e) {
+      const int r = la.roff[e];
+      const int64_t t = t0 + r / BT, b = b0 + r % BT;
+      la.base[e] = (t < p.t_end && b < p.B) ? p.x + (t * p.B + b) * p.F : nullptr;
+    }
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    for (int64_t k0 = 0; k0 < p.F; k0 += KS) {
-      // A rows: r = j*kBt + bb  ->  x[t0 + j, b0 + bb, k]
+    tile_mma<PREC>(la, lb, 0, p.F, st, wm, wn, lane, acc);
 #pragma unroll
-      for (int e = 0; e < kTile * KS / 256; ++e) {
-        const int idx = e * 256 + tid;
-        const int row = idx / KS, kk = idx % KS;
-        const int64_t t = t0 + row / kBt, b = b0 + row % kBt, k = k0 + kk;
-        float v = 0.0f;
-        if (t < p.t_end && b < p.B && k < p.F) v = p.x[(t * p.B + b) * p.F + k];
-        sm.st.a[row][kk] = cvt<PREC>(v);
-      }
-#pragma unroll
-      for (int e = 0; e < kTile * KS / 256; ++e) {
-        const int idx = e * 256 + tid;
-        const int kk = idx / kTile, col = idx % kTile;
-        const int64_t k = k0 + kk, nn = n0 + col;
-        float v = 0.0f;
-        if (k < p.F && nn < p.N) v = p.w[k * p.N + nn];
-        sm.st.b[col][kk] = cvt<PREC>(v);
-      }
-      __syncthreads();
-      mfma_stage<PREC>(sm.st, wm, wn, lane, acc);
-      __syncthreads();
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sm.cur[32 * wm + acc_row(r, lane)][32 * wn + (lane & 31)] = acc[r];
+    for (int r = 0; r < 16; ++r) cur[32 * wm + acc_row(r, lane)][32 * wn + (lane & 31)] = acc[r];
     __syncthreads();
 
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
+    for (int j = 0; j < CH; ++j) {
       const int64_t t = t0 + j;
       if (t >= p.t_end) break;  // uniform
       if (p.ckpt != nullptr && t == next_ck) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < Q; ++q)
           if (act[q]) p.ckpt[ck_row * BN + flat[q]] = m[q];
         ++ck_row;
         next_ck += p.ckpt_every;
       }
-      bool s[2];
+      bool s[Q];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < Q; ++q) {
         // input_current = x_t @ W + bias ; m' = m*decay + input_current
-        const float cur = sm.cur[j * kBt + 2 * w + q][lane] + bias_n;
+        const float c_in = cur[j * BT + Q * w + q][lane] + bias_n;
         float mp = m[q] * p.decay;
-        mp = mp + cur;
+        mp = mp + c_in;
         bool sp;
         if (p.rule == MYELIN_RULE_THRESHOLD) {
           sp = mp >= p.thr;
@@ -277,9 +397,9 @@ __global__ __launch_bounds__(256) void linear_lif_fwd(LinArgs p) {
       }
       if (p.packed != nullptr) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < Q; ++q) {
           const uint64_t bits = __ballot(s[q]);
-          const int64_t b = b0 + 2 * w + q;
+          const int64_t b = b0 + Q * w + q;
           const int64_t word = n0 / 32 + (lane >> 5);
           if ((lane & 31) == 0 && b < p.B && word < p.W)
             p.packed[(t * p.B + b) * p.W + word] = static_cast<int32_t>(lane ? (bits >> 32) : (bits & 0xffffffffu));
@@ -289,7 +409,7 @@ __global__ __launch_bounds__(256) void linear_lif_fwd(LinArgs p) {
     __syncthreads();
   }
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < Q; ++q) {
     if (!act[q]) continue;
     if (p.m_final != nullptr) p.m_final[flat[q]] = m[q];
     if (p.rates != nullptr) p.rates[flat[q]] = cnt[q] / p.rate_denominator;
@@ -379,35 +499,74 @@ __global__ __launch_bounds__(256) void col_sum(const float *__restrict__ in, flo
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-template <int PREC>
-int launch_gemm(const GemmArgs &g, int ta, int tb, hipStream_t s) {
-  const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile));
-  if (grid.y > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
+bool al16(const void *q) { return q == nullptr || myelin::aligned(q, 16); }
+
+template <int PREC, bool VEC>
+void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
   if (!ta && !tb)
-    gemm_kernel<PREC, false, false><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, false, VEC><<<grid, dim3(256), 0, s>>>(g);
   else if (!ta && tb)
-    gemm_kernel<PREC, false, true><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, true, VEC><<<grid, dim3(256), 0, s>>>(g);
   else if (ta && !tb)
-    gemm_kernel<PREC, true, false><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, true, false, VEC><<<grid, dim3(256), 0, s>>>(g);
   else
-    gemm_kernel<PREC, true, true><<<grid, dim3(256), 0, s>>>(g);
-  return myelin::launched("gemm");
+    gemm_kernel<PREC, true, true, VEC><<<grid, dim3(256), 0, s>>>(g);
+}
+
+template <int PREC>
+int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
+  constexpr int KS = Prec<PREC>::KS;
+  const int64_t tiles = cdiv(g.N, kTile) * cdiv(g.M, kTile);
+  if (cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
+  // split K when the output alone gives under ~2 workgroups per CU and K is long
+  int64_t splits = 1;
+  if (g.ws != nullptr && tiles < 512 && g.K >= 8 * KS) {
+    splits = cdiv(512, tiles);
+    const int64_t max_by_k = g.K / (4 * KS);
+    if (splits > max_by_k) splits = max_by_k;
+    if (splits > 64) splits = 64;
+    while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
+    if (splits < 1) splits = 1;
+  }
+  g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
+  splits = cdiv(g.K, g.kchunk);
+  if (splits < 1) splits = 1;
+  g.splits = static_cast<int>(splits);
+  const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
+  const bool vec = al16(g.A) && al16(g.B) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
+  if (vec)
+    launch_gemm_v<PREC, true>(g, ta, tb, grid, s);
+  else
+    launch_gemm_v<PREC, false>(g, ta, tb, grid, s);
+  if (int rc = myelin::launched("gemm")) return rc;
+  if (splits > 1) {
+    splitk_reduce<<<dim3(cdiv(g.M * g.N, 256)), dim3(256), 0, s>>>(g);
+    return myelin::launched("gemm split-k reduce");
+  }
+  return MYELIN_OK;
 }
 
 }  // namespace
 
 extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
                                int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b,
-                               int accumulate, int precision, myelin_stream_t stream) {
+                               int accumulate, int precision, float *workspace, int64_t workspace_elems,
+                               myelin_stream_t stream) {
   if (M < 0 || N < 0 || K < 0) return myelin::invalid("gemm: negative size");
   if (M == 0 || N == 0) return MYELIN_OK;
   if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm: null pointer");
   if (ldc < N) return myelin::invalid("gemm: ldc < N");
   if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N)) return myelin::invalid("gemm: bad leading dim");
-  GemmArgs g{A, B, bias, C, M, N, K, lda, ldb, ldc, accumulate};
+  if (workspace_elems < 0) return myelin::invalid("gemm: negative workspace size");
+  GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
+  if (K == 0) {  // C = (accumulate ? C : 0) + bias
+    g.splits = 0;
+    splitk_reduce<<<dim3(cdiv(M * N, 256)), dim3(256), 0, myelin::as_hip(stream)>>>(g);
+    return myelin::launched("gemm (K = 0)");
+  }
   hipStream_t s = myelin::as_hip(stream);
-  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, s);
-  if (precision == MYELIN_PREC_F32) return launch_gemm<0>(g, trans_a, trans_b, s);
+  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, workspace_elems, s);
+  if (precision == MYELIN_PREC_F32) return launch_gemm<0>(g, trans_a, trans_b, workspace_elems, s);
   return myelin::invalid("gemm: unknown precision %d", precision);
 }
 
@@ -447,15 +606,34 @@ extern "C" int myelin_linear_lif_fwd(const float *x, const float *w, const float
   a.slope = slope;
   a.rate_denominator = static_cast<float>(T);
   a.rule = rule;
-  const dim3 grid(cdiv(N, kTile), cdiv(B, kBt));
-  if (grid.y > 65535) return myelin::invalid("linear_lif_fwd: B too large");
-  hipStream_t s = myelin::as_hip(stream);
-  if (precision == MYELIN_PREC_BF16)
-    linear_lif_fwd<1><<<grid, dim3(256), 0, s>>>(a);
-  else if (precision == MYELIN_PREC_F32)
-    linear_lif_fwd<0><<<grid, dim3(256), 0, s>>>(a);
-  else
+  if (precision != MYELIN_PREC_BF16 && precision != MYELIN_PREC_F32)
     return myelin::invalid("linear_lif_fwd: unknown precision %d", precision);
+  // 8 batch rows x 8 steps per tile, or 4 x 16 when that leaves the chip
+  // under ~2 workgroups per CU
+  const int bt = (cdiv(N, kTile) * cdiv(B, 8) >= 512) ? 8 : 4;
+  const dim3 grid(cdiv(N, kTile), cdiv(B, bt));
+  if (grid.y > 65535) return myelin::invalid("linear_lif_fwd: B too large");
+  const bool vec = al16(x) && al16(w) && (F % 4 == 0) && (N % 4 == 0);
+  hipStream_t s = myelin::as_hip(stream);
+#define MYELIN_LAUNCH_FUSED(P, BT)                                                     \
+  do {                                                                                 \
+    if (vec)                                                                           \
+      linear_lif_fwd<P, BT, true><<<grid, dim3(256), 0, s>>>(a);                       \
+    else                                                                               \
+      linear_lif_fwd<P, BT, false><<<grid, dim3(256), 0, s>>>(a);                      \
+  } while (0)
+  if (precision == MYELIN_PREC_BF16) {
+    if (bt == 8)
+      MYELIN_LAUNCH_FUSED(1, 8);
+    else
+      MYELIN_LAUNCH_FUSED(1, 4);
+  } else {
+    if (bt == 8)
+      MYELIN_LAUNCH_FUSED(0, 8);
+    else
+      MYELIN_LAUNCH_FUSED(0, 4);
+  }
+#undef MYELIN_LAUNCH_FUSED
   return myelin::launched("linear_lif_fwd");
 }
 
