@@ -249,6 +249,23 @@ int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
 int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int64_t cols,
                        int accumulate, myelin_stream_t stream);
 
+/*
+ * The LIF recurrence of myelin_linear_lif_fwd over precomputed currents
+ * [t_end - t_begin, B, N] (x_t @ W + bias from myelin_gemm_f32), same
+ * optional outputs and indexing.  Used when N is too narrow for the fused
+ * kernel to fill the chip (e.g. 10- or 20-neuron rate readouts).
+ * Replaces: the recurrence half of _linear_surrogate_lif_checkpoint_rate_
+ *   forward_kernel / _linear_surrogate_lif_forward_kernel
+ *   (triton/lif.py:554-612,823-889).
+ */
+int myelin_lif_currents_fwd(const float *currents, const float *m0,
+                            float *m_final, float *spikes, float *pre,
+                            int32_t *packed, float *rates, float *ckpt,
+                            int64_t T, int64_t B, int64_t N, int64_t t_begin,
+                            int64_t t_end, int64_t ckpt_every, float decay,
+                            float threshold, float reset, float slope, int rule,
+                            myelin_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -487,14 +487,85 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   if (p.gbias_acc != nullptr) p.gbias_acc[i] = p.gbias_acc[i] + gb;
 }
 
-// out[n] (+)= sum_b in[b, n]  (fixed order per column: deterministic)
-__global__ __launch_bounds__(256) void col_sum(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
-                                               int64_t cols, int accumulate) {
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (n >= cols) return;
+// out[n] (+)= sum_r in[r, n].  A block of 16 waves takes 64 columns; wave
+// q sums rows q, q+16, ... of its column, then wave 0 adds the 16 partials
+// in wave order (fixed order: deterministic).
+__global__ __launch_bounds__(1024) void col_sum(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
+                                                int64_t cols, int accumulate) {
+  __shared__ float part[16][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + lane;
   float s = 0.0f;
-  for (int64_t r = 0; r < rows; ++r) s = s + in[r * cols + n];
-  out[n] = accumulate ? out[n] + s : s;
+  if (n < cols)
+    for (int64_t r = q; r < rows; r += 16) s = s + in[r * cols + n];
+  part[q][lane] = s;
+  __syncthreads();
+  if (q == 0 && n < cols) {
+    float t = 0.0f;
+    for (int i = 0; i < 16; ++i) t = t + part[i][lane];
+    out[n] = accumulate ? out[n] + t : t;
+  }
+}
+
+// LIF recurrence over precomputed currents cur [t_end - t_begin, B, N]
+// (bias already added by the GEMM epilogue), for outputs too narrow to
+// fill the chip with the fused kernel.  Lanes map to (b, word, bit) so a
+// half-wave owns one packed word.
+struct CurArgs {
+  const float *cur;
+  const float *m0;
+  float *m_final, *spikes, *pre, *rates, *ckpt;
+  int32_t *packed;
+  int64_t T, B, N, W, t_begin, t_end, ckpt_every;
+  float decay, thr, reset, slope, rate_denominator;
+  int rule;
+};
+
+__global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t g = gid >> 5;
+  const int bit = static_cast<int>(gid & 31);
+  const int64_t b = g / p.W;
+  const int64_t n = (g - b * p.W) * 32 + bit;
+  const bool act = (b < p.B) && (n < p.N);
+  const int64_t flat = b * p.N + n, BN = p.B * p.N;
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  float m = (act && p.m0 != nullptr) ? p.m0[flat] : 0.0f;
+  float cnt = 0.0f;
+  int64_t next_ck = p.t_begin, ck_row = 0;
+  for (int64_t t = p.t_begin; t < p.t_end; ++t) {
+    if (p.ckpt != nullptr && t == next_ck) {
+      if (act) p.ckpt[ck_row * BN + flat] = m;
+      ++ck_row;
+      next_ck += p.ckpt_every;
+    }
+    bool sp = false;
+    if (act) {
+      float mp = m * p.decay;
+      mp = mp + p.cur[(t - p.t_begin) * BN + flat];
+      if (p.rule == MYELIN_RULE_THRESHOLD) {
+        sp = mp >= p.thr;
+      } else {
+        const float c = p.slope * (mp - p.thr);
+        sp = c >= 0.0f;
+      }
+      if (p.pre != nullptr) p.pre[(t - p.t_begin) * BN + flat] = mp;
+      if (p.spikes != nullptr) p.spikes[t * BN + flat] = sp ? 1.0f : 0.0f;
+      m = sp ? p.reset : mp;
+      cnt = cnt + (sp ? 1.0f : 0.0f);
+    }
+    if (p.packed != nullptr) {
+      const uint64_t bits = __ballot(sp);
+      const int64_t gw = (gid - lane) >> 5;  // the wave's first word
+      int32_t *row = p.packed + t * p.B * p.W;
+      if (lane == 0 && gw < p.B * p.W) row[gw] = static_cast<int32_t>(bits & 0xffffffffu);
+      if (lane == 32 && gw + 1 < p.B * p.W) row[gw + 1] = static_cast<int32_t>(bits >> 32);
+    }
+  }
+  if (act) {
+    if (p.m_final != nullptr) p.m_final[flat] = m;
+    if (p.rates != nullptr) p.rates[flat] = cnt / p.rate_denominator;
+  }
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -664,6 +735,43 @@ extern "C" int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int
   if (rows < 0 || cols < 0) return myelin::invalid("col_sum: negative size");
   if (cols == 0) return MYELIN_OK;
   if (out == nullptr || (rows > 0 && in == nullptr)) return myelin::invalid("col_sum: null pointer");
-  col_sum<<<dim3(cdiv(cols, 256)), dim3(256), 0, myelin::as_hip(stream)>>>(in, out, rows, cols, accumulate);
+  col_sum<<<dim3(cdiv(cols, 64)), dim3(1024), 0, myelin::as_hip(stream)>>>(in, out, rows, cols, accumulate);
   return myelin::launched("col_sum");
+}
+
+extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, float *m_final, float *spikes,
+                                       float *pre, int32_t *packed, float *rates, float *ckpt, int64_t T, int64_t B,
+                                       int64_t N, int64_t t_begin, int64_t t_end, int64_t ckpt_every, float decay,
+                                       float threshold, float reset, float slope, int rule, myelin_stream_t stream) {
+  if (T < 1 || B < 1 || N < 1) return myelin::invalid("lif_currents_fwd: T, B, N must be positive");
+  if (t_begin < 0 || t_end > T || t_begin >= t_end) return myelin::invalid("lif_currents_fwd: bad time range");
+  if (currents == nullptr) return myelin::invalid("lif_currents_fwd: currents are required");
+  if (ckpt != nullptr && ckpt_every < 1) return myelin::invalid("lif_currents_fwd: ckpt_every must be positive");
+  if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
+    return myelin::invalid("lif_currents_fwd: unknown rule %d", rule);
+  CurArgs a{};
+  a.cur = currents;
+  a.m0 = m0;
+  a.m_final = m_final;
+  a.spikes = spikes;
+  a.pre = pre;
+  a.rates = rates;
+  a.ckpt = ckpt;
+  a.packed = packed;
+  a.T = T;
+  a.B = B;
+  a.N = N;
+  a.W = (N + 31) / 32;
+  a.t_begin = t_begin;
+  a.t_end = t_end;
+  a.ckpt_every = ckpt_every < 1 ? 1 : ckpt_every;
+  a.decay = decay;
+  a.thr = threshold;
+  a.reset = reset;
+  a.slope = slope;
+  a.rate_denominator = static_cast<float>(T);
+  a.rule = rule;
+  const int64_t lanes = B * a.W * 32;
+  lif_currents_fwd<<<dim3(cdiv(lanes, 256)), dim3(256), 0, myelin::as_hip(stream)>>>(a);
+  return myelin::launched("lif_currents_fwd");
 }

@@ -2,7 +2,9 @@
 of the neuron update).
 
 Forward: one launch of ``myelin_linear_lif_fwd`` computes every step's
-current tile on MFMA and runs the recurrence in the same workgroup.
+current tile on MFMA and runs the recurrence in the same workgroup (layers
+narrower than 64 neurons use a split-K GEMM plus the recurrence kernel, see
+``_lif_fwd``).
 
 Saved state:
 * ``checkpoint_size=None`` (the reference's stream Function,
@@ -104,6 +106,36 @@ def linear(x, w, b, precision: str = "fp32"):
                                        _lib.PREC[precision])
 
 
+def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
+             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1):
+    """Synaptic currents + LIF recurrence over steps [t0, t1).
+
+    N >= 64: one fused launch (currents stay in LDS).  Narrower layers (the
+    10/20-neuron rate readouts) would leave the chip nearly idle in the fused
+    kernel, so they run a split-K GEMM into a [t1 - t0, B, N] current buffer
+    (bias added in its epilogue) and the recurrence kernel over it.
+    """
+
+    T, B, F = x.shape
+    N = w.shape[1]
+    if N >= 64:
+        _lib.call(
+            "myelin_linear_lif_fwd",
+            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre),
+            _lib.ptr(packed), _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold,
+            reset, slope, rule, prec, stream,
+        )
+        return
+    rows = (t1 - t0) * B
+    cur = torch.empty((t1 - t0, B, N), dtype=torch.float32, device=x.device)
+    _gemm(x[t0:t1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
+    _lib.call(
+        "myelin_lif_currents_fwd",
+        _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
+        _lib.ptr(rates), _lib.ptr(ckpt), T, B, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule, stream,
+    )
+
+
 class HipLinearLIFFunction(torch.autograd.Function):
     """Outputs ``(final_membrane, spikes)`` or, with ``rate=True``,
     ``(final_membrane, rates)`` where ``rates = spike_count / T``."""
@@ -123,12 +155,9 @@ class HipLinearLIFFunction(torch.autograd.Function):
                 pre = torch.empty((T, B, N), dtype=x.dtype, device=dev)
             else:
                 ckpt = torch.empty((math.ceil(T / checkpoint), B, N), dtype=x.dtype, device=dev)
-        _lib.call(
-            "myelin_linear_lif_fwd",
-            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), None, _lib.ptr(m_final),
-            None if rate else _lib.ptr(out), _lib.ptr(pre), None, _lib.ptr(out) if rate else None, _lib.ptr(ckpt),
-            T, B, F, N, 0, T, checkpoint or 1, decay, threshold, reset, slope, rule, prec, stream,
-        )
+        _lif_fwd(x, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
+                 spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
+                 ckpt_every=checkpoint or 1)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:
@@ -167,12 +196,8 @@ class HipLinearLIFFunction(torch.autograd.Function):
                 if checkpoint is None:
                     pre_k = pre
                 else:
-                    _lib.call(
-                        "myelin_linear_lif_fwd",
-                        _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(ckpt[k]), None, None,
-                        _lib.ptr(scratch), None, None, None,
-                        T, B, F, N, t0, t1, 1, decay, threshold, reset, slope, rule, prec, stream,
-                    )
+                    _lif_fwd(x, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
+                             pre=scratch)
                     pre_k = scratch
                 _lib.call(
                     "myelin_linear_pre_bwd",
@@ -247,10 +272,7 @@ def linear_packed_forward(x, w, b, params, checkpoint: int, precision: str):
     m_final = torch.empty((B, N), device=x.device)
     words = torch.empty((T, B, packed_last_dim_size(N)), dtype=torch.int32, device=x.device)
     with torch.cuda.device(x.device):
-        _lib.call(
-            "myelin_linear_lif_fwd",
-            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), None, _lib.ptr(m_final), None, None, _lib.ptr(words), None, None,
-            T, B, F, N, 0, T, checkpoint, float(params.decay), float(params.threshold), float(params.reset), 10.0,
-            _lib.RULE_THRESHOLD, _lib.PREC[precision], _lib.stream(x.device),
-        )
+        _lif_fwd(x, w, b, None, 0, T, float(params.decay), float(params.threshold), float(params.reset), 10.0,
+                 _lib.RULE_THRESHOLD, _lib.PREC[precision], _lib.stream(x.device), m_final=m_final, packed=words,
+                 ckpt_every=checkpoint)
     return m_final, PackedSpikes(data=words, original_shape=(T, B, N))
