@@ -251,18 +251,25 @@ int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int64_t cols,
 
 /*
  * The LIF recurrence of myelin_linear_lif_fwd over precomputed currents
- * [t_end - t_begin, B, N] (x_t @ W + bias from myelin_gemm_f32), same
- * optional outputs and indexing.  Used when N is too narrow for the fused
- * kernel to fill the chip (e.g. 10- or 20-neuron rate readouts).
+ * [t_end - t_begin, B, N] (x_t @ W + bias from myelin_gemm_f32), for steps
+ * [t_begin, t_end).  Long horizons run as several calls with the membrane
+ * (m0 -> m_final, may alias) and spike counts (`counts`, [B, N] in/out,
+ * may be NULL) carried across calls.  pre rows are t - pre_origin;
+ * checkpoint rows count from ck_origin (row k = state before step
+ * ck_origin + k*ckpt_every); spikes / packed use absolute t; rates =
+ * counts / T at the end of the call.  Used when the fused kernel would leave
+ * the chip under-filled: narrow layers (10/20-neuron readouts) and few
+ * batch x neuron tiles with long horizons.
  * Replaces: the recurrence half of _linear_surrogate_lif_checkpoint_rate_
  *   forward_kernel / _linear_surrogate_lif_forward_kernel
  *   (triton/lif.py:554-612,823-889).
  */
 int myelin_lif_currents_fwd(const float *currents, const float *m0,
                             float *m_final, float *spikes, float *pre,
-                            int32_t *packed, float *rates, float *ckpt,
-                            int64_t T, int64_t B, int64_t N, int64_t t_begin,
-                            int64_t t_end, int64_t ckpt_every, float decay,
+                            int32_t *packed, float *rates, float *counts,
+                            float *ckpt, int64_t T, int64_t B, int64_t N,
+                            int64_t t_begin, int64_t t_end, int64_t pre_origin,
+                            int64_t ck_origin, int64_t ckpt_every, float decay,
                             float threshold, float reset, float slope, int rule,
                             myelin_stream_t stream);
 

@@ -53,7 +53,7 @@ SIGNATURES: dict[str, list] = {
     "myelin_linear_lif_fwd": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_linear_pre_bwd": [_P] * 6 + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],
-    "myelin_lif_currents_fwd": [_P] * 8 + [_I64] * 6 + [_F] * 4 + [_INT, _P],
+    "myelin_lif_currents_fwd": [_P] * 9 + [_I64] * 8 + [_F] * 4 + [_INT, _P],
 }
 
 _lock = threading.Lock()

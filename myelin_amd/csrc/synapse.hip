@@ -514,9 +514,9 @@ __global__ __launch_bounds__(1024) void col_sum(const float *__restrict__ in, fl
 struct CurArgs {
   const float *cur;
   const float *m0;
-  float *m_final, *spikes, *pre, *rates, *ckpt;
+  float *m_final, *spikes, *pre, *rates, *ckpt, *counts;
   int32_t *packed;
-  int64_t T, B, N, W, t_begin, t_end, ckpt_every;
+  int64_t T, B, N, W, t_begin, t_end, ckpt_every, pre_origin, ck_origin;
   float decay, thr, reset, slope, rate_denominator;
   int rule;
 };
@@ -531,8 +531,11 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const int64_t flat = b * p.N + n, BN = p.B * p.N;
   const int lane = static_cast<int>(threadIdx.x & 63);
   float m = (act && p.m0 != nullptr) ? p.m0[flat] : 0.0f;
-  float cnt = 0.0f;
-  int64_t next_ck = p.t_begin, ck_row = 0;
+  float cnt = (act && p.counts != nullptr) ? p.counts[flat] : 0.0f;
+  // checkpoint rows are counted from ck_origin: row k holds the state before
+  // step ck_origin + k*ckpt_every
+  int64_t ck_row = (p.t_begin - p.ck_origin + p.ckpt_every - 1) / p.ckpt_every;
+  int64_t next_ck = p.ck_origin + ck_row * p.ckpt_every;
   for (int64_t t = p.t_begin; t < p.t_end; ++t) {
     if (p.ckpt != nullptr && t == next_ck) {
       if (act) p.ckpt[ck_row * BN + flat] = m;
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
         const float c = p.slope * (mp - p.thr);
         sp = c >= 0.0f;
       }
-      if (p.pre != nullptr) p.pre[(t - p.t_begin) * BN + flat] = mp;
+      if (p.pre != nullptr) p.pre[(t - p.pre_origin) * BN + flat] = mp;
       if (p.spikes != nullptr) p.spikes[t * BN + flat] = sp ? 1.0f : 0.0f;
       m = sp ? p.reset : mp;
       cnt = cnt + (sp ? 1.0f : 0.0f);
@@ -564,6 +567,7 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   }
   if (act) {
     if (p.m_final != nullptr) p.m_final[flat] = m;
+    if (p.counts != nullptr) p.counts[flat] = cnt;
     if (p.rates != nullptr) p.rates[flat] = cnt / p.rate_denominator;
   }
 }
@@ -740,11 +744,14 @@ extern "C" int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int
 }
 
 extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, float *m_final, float *spikes,
-                                       float *pre, int32_t *packed, float *rates, float *ckpt, int64_t T, int64_t B,
-                                       int64_t N, int64_t t_begin, int64_t t_end, int64_t ckpt_every, float decay,
-                                       float threshold, float reset, float slope, int rule, myelin_stream_t stream) {
+                                       float *pre, int32_t *packed, float *rates, float *counts, float *ckpt, int64_t T,
+                                       int64_t B, int64_t N, int64_t t_begin, int64_t t_end, int64_t pre_origin,
+                                       int64_t ck_origin, int64_t ckpt_every, float decay, float threshold,
+                                       float reset, float slope, int rule, myelin_stream_t stream) {
   if (T < 1 || B < 1 || N < 1) return myelin::invalid("lif_currents_fwd: T, B, N must be positive");
   if (t_begin < 0 || t_end > T || t_begin >= t_end) return myelin::invalid("lif_currents_fwd: bad time range");
+  if (pre_origin < 0 || pre_origin > t_begin || ck_origin < 0 || ck_origin > t_begin)
+    return myelin::invalid("lif_currents_fwd: origins must lie in [0, t_begin]");
   if (currents == nullptr) return myelin::invalid("lif_currents_fwd: currents are required");
   if (ckpt != nullptr && ckpt_every < 1) return myelin::invalid("lif_currents_fwd: ckpt_every must be positive");
   if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
@@ -757,6 +764,7 @@ extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, f
   a.pre = pre;
   a.rates = rates;
   a.ckpt = ckpt;
+  a.counts = counts;
   a.packed = packed;
   a.T = T;
   a.B = B;
@@ -764,6 +772,8 @@ extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, f
   a.W = (N + 31) / 32;
   a.t_begin = t_begin;
   a.t_end = t_end;
+  a.pre_origin = pre_origin;
+  a.ck_origin = ck_origin;
   a.ckpt_every = ckpt_every < 1 ? 1 : ckpt_every;
   a.decay = decay;
   a.thr = threshold;

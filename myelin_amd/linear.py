@@ -106,19 +106,33 @@ def linear(x, w, b, precision: str = "fp32"):
                                        _lib.PREC[precision])
 
 
+# currents buffer budget of the chunked path (floats)
+_CURRENT_CHUNK_ELEMS = 1 << 25
+
+
+def _fused_grid(B: int, N: int) -> int:
+    """Workgroups of the fused kernel (its 8- or 4-row batch tiles)."""
+
+    nt = -(-N // 64)
+    return nt * -(-B // 8) if nt * -(-B // 8) >= 512 else nt * -(-B // 4)
+
+
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
              spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
-    N >= 64: one fused launch (currents stay in LDS).  Narrower layers (the
-    10/20-neuron rate readouts) would leave the chip nearly idle in the fused
-    kernel, so they run a split-K GEMM into a [t1 - t0, B, N] current buffer
-    (bias added in its epilogue) and the recurrence kernel over it.
+    Fused (one launch, currents stay in LDS) when N >= 64 and the fused grid
+    has >= 1024 workgroups.  Otherwise each workgroup would walk many chunks
+    serially, so the steps are processed in chunks of up to 2**25 currents:
+    an MFMA GEMM (split-K when narrow) writes ``x_t @ W + b`` for the chunk,
+    then the recurrence kernel consumes it, carrying the membrane and the
+    spike counts across chunks.  ``pre`` is indexed from t0; checkpoint rows
+    from t0.
     """
 
     T, B, F = x.shape
     N = w.shape[1]
-    if N >= 64:
+    if N >= 64 and _fused_grid(B, N) >= 1024:
         _lib.call(
             "myelin_linear_lif_fwd",
             _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre),
@@ -126,14 +140,24 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
             reset, slope, rule, prec, stream,
         )
         return
-    rows = (t1 - t0) * B
-    cur = torch.empty((t1 - t0, B, N), dtype=torch.float32, device=x.device)
-    _gemm(x[t0:t1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
-    _lib.call(
-        "myelin_lif_currents_fwd",
-        _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
-        _lib.ptr(rates), _lib.ptr(ckpt), T, B, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule, stream,
-    )
+    dev = x.device
+    step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
+    cur = torch.empty((step, B, N), dtype=torch.float32, device=dev)
+    state = torch.zeros((B, N), dtype=torch.float32, device=dev) if m0 is None else m0.clone()
+    counts = torch.zeros((B, N), dtype=torch.float32, device=dev) if rates is not None else None
+    for c0 in range(t0, t1, step):
+        c1 = min(c0 + step, t1)
+        rows = (c1 - c0) * B
+        _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
+        last = c1 == t1
+        _lib.call(
+            "myelin_lif_currents_fwd",
+            _lib.ptr(cur), _lib.ptr(state), _lib.ptr(state), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
+            _lib.ptr(rates) if last else None, _lib.ptr(counts), _lib.ptr(ckpt), T, B, N, c0, c1, t0, t0,
+            ckpt_every, decay, threshold, reset, slope, rule, stream,
+        )
+    if m_final is not None:
+        m_final.copy_(state)
 
 
 class HipLinearLIFFunction(torch.autograd.Function):
