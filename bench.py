@@ -20,6 +20,10 @@ the headline (each prints its own JSON line with its own roofline):
   long_rate       one training step: LinearSurrogateLIF(1024 -> 4096,
                   checkpoint "memory", superspike, fp32) + rate readout
                   (4096 -> 20), CE, [2000, 32, 1024]; reports peak HBM bytes
+  long_rate_packed  the same network and step through
+                  two_layer_surrogate_lif_rate_packed_hidden_forward (the two
+                  layers interleaved per checkpoint chunk, hidden spikes kept
+                  bitpacked); reports peak HBM bytes
   bitpack         pack [512, 64, 8192] spikes, unpack, per-neuron counts over
                   T, per-sample rates
 """
@@ -51,7 +55,7 @@ def _args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--workload", default="alif_headline",
-                    choices=["alif_headline", "lif_fwd", "linear_bf16", "long_rate", "bitpack"])
+                    choices=["alif_headline", "lif_fwd", "linear_bf16", "long_rate", "long_rate_packed", "bitpack"])
     ap.add_argument("--cpu-sample-batch", type=int, default=128)
     ap.add_argument("--cpu-min-seconds", type=float, default=10.0)
     ap.add_argument(
@@ -228,7 +232,7 @@ def _workload_linear_bf16(torch, myelin, args):
                  dtype="bf16")
 
 
-def _workload_long_rate(torch, myelin, args):
+def _workload_long_rate(torch, myelin, args, packed_hidden=False):
     Tl, Bl, F, H, O = 2000, 32, 1024, 4096, 20
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(4)
@@ -240,11 +244,17 @@ def _workload_long_rate(torch, myelin, args):
     readout = myelin.LinearSurrogateLIFRate(H, O, surrogate=myelin.superspike_surrogate,
                                             checkpoint_size="memory").to(dev)
     params = list(hidden.parameters()) + list(readout.parameters())
+    wh, bh, wo, bo = hidden.synapse.weight, hidden.synapse.bias, readout.synapse.weight, readout.synapse.bias
 
     def step():
         for q in params:
             q.grad = None
-        rates = readout(hidden(x))
+        if packed_hidden:
+            rates = myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(
+                x, wh, bh, wo, bo, myelin.LIFParams(), surrogate="superspike", surrogate_slope=10.0,
+                checkpoint_size="memory")
+        else:
+            rates = readout(hidden(x))
         torch.nn.functional.cross_entropy(rates * Tl, labels).backward()
 
     step()
@@ -256,10 +266,13 @@ def _workload_long_rate(torch, myelin, args):
     flops = 3 * 2 * Tl * Bl * F * H + 4 * 2 * Tl * Bl * H * O
     tflops = flops / (ms * 1e-3) / 1e12
     E = Tl * Bl * H
+    name = ("two_layer_surrogate_lif_rate_packed_hidden_forward(1024->4096->20, checkpoint 'memory'=45, "
+            "superspike, fp32) + CE, fwd+bwd" if packed_hidden else
+            "LinearSurrogateLIF(1024->4096, stream_synapse, checkpoint 'memory'=45, superspike, "
+            "fp32) + LinearSurrogateLIFRate(4096->20, 'memory') + CE, fwd+bwd")
     return _line("neuron-steps/sec, long-horizon checkpointed rate training step", E / (ms * 1e-3),
                  "neuron-steps/s", ms, args,
-                 {"workload": "LinearSurrogateLIF(1024->4096, stream_synapse, checkpoint 'memory'=45, superspike, "
-                              "fp32) + LinearSurrogateLIFRate(4096->20, 'memory') + CE, fwd+bwd",
+                 {"workload": name,
                   "T": Tl, "B": Bl, "F": F, "N": H, "readout": O, "gflop_per_step": flops / 1e9},
                  roofline={"bound": "mfma", "achieved": tflops, "peak": 157.3, "unit": "TFLOP/s",
                            "frac": tflops / 157.3, "traffic": None,
@@ -310,6 +323,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     others = {"lif_fwd": _workload_lif_fwd, "linear_bf16": _workload_linear_bf16, "long_rate": _workload_long_rate,
+              "long_rate_packed": lambda t, m, a: _workload_long_rate(t, m, a, packed_hidden=True),
               "bitpack": _workload_bitpack}
     if args.workload in others:
         print(json.dumps(others[args.workload](torch, myelin, args)), flush=True)

@@ -319,3 +319,73 @@ def linear_surrogate_lif_packed_forward(
     ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
     m, packed = linear_packed_forward(inputs, weight, bias, params, ck, synapse_precision)
     return LIFState(membrane=m), packed
+
+
+def two_layer_surrogate_lif_rate_recompute_forward(
+    inputs: torch.Tensor,
+    hidden_weight: torch.Tensor,
+    hidden_bias: torch.Tensor | None,
+    output_weight: torch.Tensor,
+    output_bias: torch.Tensor | None,
+    params: LIFParams,
+    *,
+    surrogate: SurrogateName = "fast_sigmoid",
+    surrogate_slope: float = 5.0,
+    hard_forward: bool = True,
+    checkpoint_size: CheckpointSize = 25,
+    synapse_precision: Literal["fp32", "bf16"] = "fp32",
+) -> torch.Tensor:
+    """Two-layer LIF rate network, input -> hidden -> readout rates ``[B, O]``
+    (kernels.py:779-808; autograd.py:926-1126).
+
+    Only the inputs, weights and chunk-start membranes of both layers are
+    kept for the backward; the two layers run interleaved per checkpoint
+    chunk, so hidden spikes and their gradient exist one chunk at a time.
+    """
+
+    from myelin_amd.two_layer import two_layer_rate_forward
+
+    sid = surrogate_id(surrogate)
+    if not hard_forward:
+        raise ValueError("two-layer recompute currently supports only hard_forward=True")
+    ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
+    return two_layer_rate_forward(inputs, hidden_weight, hidden_bias, output_weight, output_bias, params, sid,
+                                  surrogate_slope, ck, synapse_precision, packed_hidden=False)
+
+
+def two_layer_surrogate_lif_rate_packed_hidden_forward(
+    inputs: torch.Tensor,
+    hidden_weight: torch.Tensor,
+    hidden_bias: torch.Tensor | None,
+    output_weight: torch.Tensor,
+    output_bias: torch.Tensor | None,
+    params: LIFParams,
+    *,
+    surrogate: SurrogateName = "fast_sigmoid",
+    surrogate_slope: float = 5.0,
+    hard_forward: bool = True,
+    checkpoint_size: CheckpointSize = 25,
+    block_b: int = 16,
+    block_n: int = 32,
+    block_f: int = 32,
+    synapse_precision: Literal["fp32", "bf16"] = "fp32",
+) -> torch.Tensor:
+    """Two-layer LIF rate network that keeps the hidden spikes bitpacked
+    (kernels.py:811-846; autograd.py:1129-1387).
+
+    The forward's hidden kernel ballots the spikes straight into
+    ``[T, B, ceil(H/32)]`` int32 words; the backward unpacks one checkpoint
+    chunk at a time as the readout's input (the reference unpacks all T).
+    Triton tile knobs are accepted and ignored.
+    """
+
+    from myelin_amd.two_layer import two_layer_rate_forward
+
+    sid = surrogate_id(surrogate)
+    if not hard_forward:
+        raise ValueError("packed-hidden two-layer rate training supports only hard_forward=True")
+    if not inputs.is_cuda:
+        raise ValueError("packed-hidden two-layer rate training requires CUDA tensors")
+    ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
+    return two_layer_rate_forward(inputs, hidden_weight, hidden_bias, output_weight, output_bias, params, sid,
+                                  surrogate_slope, ck, synapse_precision, packed_hidden=True)

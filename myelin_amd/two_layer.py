@@ -1,0 +1,209 @@
+"""Two-layer LIF rate network (input -> hidden LIF -> readout LIF rates) with
+the two layers interleaved per checkpoint chunk.
+
+Reference: ``TwoLayerSurrogateLIFRateRecomputeFunction`` and
+``TwoLayerSurrogateLIFRatePackedHiddenFunction`` (autograd.py:926-1387),
+entry points ``kernels.py:779-846``.  The reference runs each layer over all
+T steps in turn, so the hidden spikes ``[T, B, H]`` exist densely between
+them (in the packed variant they are unpacked to dense in both passes,
+autograd.py:1185,1284), and its backward produces a dense ``[T, B, H]``
+hidden-spike gradient.
+
+Here both passes walk time in chunks of C steps (the checkpoint size):
+
+* forward, chunk k: hidden ``x_t @ W_h`` + LIF from the carried hidden
+  membrane -> hidden spikes of the chunk ``[C, B, H]`` (and, packed variant,
+  their words ``[T, B, ceil(H/32)]``); readout ``s_t @ W_o`` + LIF from the
+  carried readout membrane and spike counts.  Chunk-start membranes of both
+  layers are kept ``[ceil(T/C), B, H + O]``.
+* backward, chunks in reverse: recompute the hidden chunk (pre-reset trace;
+  its spikes, or the unpacked words of the packed variant, feed the readout),
+  recompute the readout chunk, reverse the readout recurrence (adjoint
+  carried across chunks), ``dS = G_o @ W_o^T`` for the chunk only, then
+  reverse the hidden recurrence with ``dS`` as its spike gradient.
+
+So no tensor with T in its shape is written except the input gradient and,
+in the packed variant, the packed words.  The arithmetic of each step is
+that of the one-layer checkpointed path (same kernels), so rates and
+gradients equal those of composing the two one-layer functions.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from myelin_amd import _lib
+from myelin_amd.linear import _gemm, _lif_fwd
+
+
+def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
+                   slope, prec, stream):
+    """Readout currents ``hs @ W_o + b_o`` for steps [t0, t1) then the LIF
+    recurrence over them in absolute time (counts and rates over all T)."""
+
+    B, O = m0.shape
+    H = wo.shape[0]
+    L = t1 - t0
+    _gemm(hs, wo, cur, L * B, O, H, H, O, O, False, False, False, prec, stream, bias=bo)
+    _lib.call(
+        "myelin_lif_currents_fwd",
+        _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(m_final), None, _lib.ptr(pre), None, _lib.ptr(rates),
+        _lib.ptr(counts), _lib.ptr(ckpt), T, B, O, t0, t1, t0, 0, C, decay, threshold, reset, slope,
+        _lib.RULE_THRESHOLD, stream,
+    )
+
+
+class HipTwoLayerRateFunction(torch.autograd.Function):
+    """Returns readout rates ``[B, O]`` = readout spike count / T."""
+
+    @staticmethod
+    def forward(ctx: Any, x, wh, bh, wo, bo, decay, threshold, reset, sid, slope, C, prec, packed_hidden):
+        T, B, F = x.shape
+        H = wh.shape[1]
+        O = wo.shape[1]
+        dev = x.device
+        stream = _lib.stream(dev)
+        need = any(ctx.needs_input_grad[:5])
+        K = math.ceil(T / C)
+        L0 = min(C, T)
+        ck_h = torch.empty((K, B, H), device=dev) if need else None
+        ck_o = torch.empty((K, B, O), device=dev) if need else None
+        m_h = torch.zeros((B, H), device=dev)
+        m_o = torch.zeros((B, O), device=dev)
+        counts = torch.zeros((B, O), device=dev)
+        rates = torch.empty((B, O), device=dev)
+        hs = torch.empty((L0, B, H), device=dev)
+        cur = torch.empty((L0, B, O), device=dev)
+        words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
+        for k in range(K):
+            t0 = k * C
+            t1 = min(t0 + C, T)
+            L = t1 - t0
+            _lif_fwd(x[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
+                     m_final=m_h, spikes=hs[:L], packed=None if words is None else words[t0:t1],
+                     ckpt=None if ck_h is None else ck_h[k], ckpt_every=L)
+            _readout_chunk(cur[:L], hs[:L], wo, bo, m_o, m_o, None, counts, rates if t1 == T else None, ck_o, T,
+                           t0, t1, C, decay, threshold, reset, slope, prec, stream)
+        ctx.set_materialize_grads(False)
+        ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
+        if need:
+            ctx.save_for_backward(x, wh, bh, wo, bo, ck_h, ck_o, words)
+        return rates
+
+    @staticmethod
+    def backward(ctx: Any, g_rates):
+        none = (None,) * 13
+        if g_rates is None or not any(ctx.needs_input_grad[:5]):
+            return none
+        decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
+        x, wh, bh, wo, bo, ck_h, ck_o, words = ctx.saved_tensors
+        need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
+        need_hidden = need_x or need_wh or (need_bh and has_bh)
+        T, B, F = x.shape
+        H = wh.shape[1]
+        O = wo.shape[1]
+        dev = x.device
+        K = math.ceil(T / C)
+        L0 = min(C, T)
+        with torch.cuda.device(dev):
+            stream = _lib.stream(dev)
+            g_rates = g_rates.float().contiguous()
+            gm_o = torch.zeros((B, O), device=dev)
+            gm_h = torch.zeros((B, H), device=dev) if need_hidden else None
+            gx = torch.empty_like(x) if need_x else None
+            gwh = torch.zeros_like(wh) if need_wh else None
+            gwo = torch.zeros_like(wo) if need_wo else None
+            gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
+            gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
+            hs = torch.empty((L0, B, H), device=dev)
+            pre_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
+            cur = torch.empty((L0, B, O), device=dev)
+            pre_o = torch.empty((L0, B, O), device=dev)
+            G_o = torch.empty((L0, B, O), device=dev)
+            ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
+            G_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
+            for k in range(K - 1, -1, -1):
+                t0 = k * C
+                t1 = min(t0 + C, T)
+                L = t1 - t0
+                rows = L * B
+                if words is not None:
+                    _lib.call("myelin_unpack", _lib.ptr(words[t0:t1]), _lib.ptr(hs), _lib.DT[torch.float32],
+                              rows, H, stream)
+                    if need_hidden:
+                        _lif_fwd(x[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
+                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L])
+                else:
+                    _lif_fwd(x[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
+                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L])
+                _readout_chunk(cur[:L], hs[:L], wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
+                               decay, threshold, reset, slope, prec, stream)
+                _lib.call(
+                    "myelin_linear_pre_bwd",
+                    _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.ptr(gbo_acc),
+                    L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                )
+                if gwo is not None:
+                    # dW_o += S[t0:t1]^T @ G_o
+                    _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, True, prec, stream)
+                if not need_hidden:
+                    continue
+                # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this chunk
+                _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
+                _lib.call(
+                    "myelin_linear_pre_bwd",
+                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h), _lib.ptr(gbh_acc),
+                    L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                )
+                if gx is not None:
+                    _gemm(G_h, wh, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
+                if gwh is not None:
+                    _gemm(x[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, True, prec, stream)
+            gbh = gbo = None
+            if gbh_acc is not None:
+                gbh = torch.empty((H,), device=dev)
+                _lib.call("myelin_col_sum_f32", _lib.ptr(gbh_acc), _lib.ptr(gbh), B, H, 0, stream)
+            if gbo_acc is not None:
+                gbo = torch.empty((O,), device=dev)
+                _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
+        return gx, gwh, gbh, gwo, gbo, None, None, None, None, None, None, None, None
+
+
+def two_layer_rate_forward(x, wh, bh, wo, bo, params, surrogate_id: int, slope: float, checkpoint: int,
+                           precision: str, packed_hidden: bool):
+    """Validate and run the chunk-interleaved two-layer rate network."""
+
+    if checkpoint <= 0:
+        raise ValueError("checkpoint_size must be positive")
+    if x.ndim != 3:
+        raise ValueError(f"inputs must be shaped [T, B, F]; got {tuple(x.shape)}")
+    if wh.ndim != 2 or wo.ndim != 2:
+        raise ValueError("hidden_weight and output_weight must be 2-D")
+    _lib.require_device(x, "inputs")
+    for name, t in (("hidden_weight", wh), ("hidden_bias", bh), ("output_weight", wo), ("output_bias", bo)):
+        if t is not None and (t.device != x.device or t.dtype != x.dtype):
+            raise ValueError(f"{name} must have the same device and dtype as inputs")
+    if x.dtype != torch.float32:
+        raise ValueError(f"inputs must be float32 for the HIP path; got {x.dtype}")
+    if x.shape[0] == 0:
+        raise ValueError("inputs must have at least one timestep")
+    if x.shape[2] != wh.shape[0]:
+        raise ValueError("inputs.shape[2] must match hidden_weight.shape[0]")
+    if wh.shape[1] != wo.shape[0]:
+        raise ValueError("hidden_weight.shape[1] must match output_weight.shape[0]")
+    if bh is not None and bh.shape != (wh.shape[1],):
+        raise ValueError("hidden_bias must be shaped [H]")
+    if bo is not None and bo.shape != (wo.shape[1],):
+        raise ValueError("output_bias must be shaped [O]")
+    if precision not in _lib.PREC:
+        raise ValueError("synapse_precision must be 'fp32' or 'bf16'")
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    with torch.cuda.device(x.device):
+        return HipTwoLayerRateFunction.apply(
+            x.contiguous(), wh.contiguous(), c(bh), wo.contiguous(), c(bo), float(params.decay),
+            float(params.threshold), float(params.reset), surrogate_id, float(slope), int(checkpoint),
+            _lib.PREC[precision], packed_hidden,
+        )

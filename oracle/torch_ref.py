@@ -598,3 +598,17 @@ def linear_surrogate_lif_rate(
         x, w, b, tau, threshold, reset, surrogate, slope, checkpoint_size, True
     )
     return m, (rates.mean() if reduction == "mean" else rates)
+
+
+def two_layer_rate(x, wh, bh, wo, bo, tau, threshold, reset, surrogate="fast_sigmoid", slope=5.0,
+                   checkpoint_size=25):
+    """``two_layer_surrogate_lif_rate_recompute_function`` (autograd.py:926-1126):
+    the hidden checkpoint function feeding the readout checkpoint-rate function
+    with ``reduction="none"``; the reference's backward replays exactly this
+    composition under autograd, so the gradient is its autograd gradient."""
+
+    if checkpoint_size <= 0:
+        raise ValueError("checkpoint_size must be positive")
+    _m, hidden = _CheckpointFn.apply(x, wh, bh, tau, threshold, reset, surrogate, slope, checkpoint_size, False)
+    _m, rates = _CheckpointFn.apply(hidden, wo, bo, tau, threshold, reset, surrogate, slope, checkpoint_size, True)
+    return rates

@@ -9,7 +9,9 @@ on its own: the linear stream / checkpoint / checkpoint-rate autograd
 Functions (autograd.py:445-923) at chunk edges with and without bias and
 with both reductions, the surrogate LIF / ALIF unroll gradients for every
 surrogate (functional.py:115-189), and every dim variant of
-packed_spike_count / packed_spike_rate (packing.py:84-162).  The fixtures
+packed_spike_count / packed_spike_rate (packing.py:84-162), and the
+two-layer whole-model-recompute rate network (autograd.py:926-1126,
+kernels.py:779-808) at several checkpoint sizes.  The fixtures
 are plain arrays (inputs and the reference's outputs) in .npz files next to
 this script; nothing from the reference is copied.
 """
@@ -144,6 +146,40 @@ def main(ref_root: str) -> None:
                 if bias:
                     out[f"{tag}_gb"] = _np(br.grad)
     np.savez_compressed(HERE / "linear_paths.npz", **out)
+
+    # ------------------------------------------------------ two-layer rate
+    from myelin.kernels import two_layer_surrogate_lif_rate_recompute_forward
+
+    out = {}
+    g = torch.Generator().manual_seed(12)
+    T, B, F, H, O = 11, 3, 13, 37, 5
+    x = (torch.rand(T, B, F, generator=g) < 0.35).float()
+    wh = (torch.rand(F, H, generator=g) - 0.3) * 0.9
+    bh = torch.rand(H, generator=g) * 0.1
+    wo = (torch.rand(H, O, generator=g) - 0.45) * 0.6
+    bo = torch.rand(O, generator=g) * 0.1
+    grate = torch.randn(B, O, generator=g)
+    for k, v in dict(x=x, wh=wh, bh=bh, wo=wo, bo=bo, grate=grate).items():
+        out[k] = _np(v)
+    p = LIFParams(tau_mem=6.0, threshold=0.6, reset=-0.1)
+    for bias in (False, True):
+        for ck in (1, 4, 11):
+            for sg in ("fast_sigmoid", "superspike"):
+                xr, whr, wor = (t.clone().requires_grad_() for t in (x, wh, wo))
+                bhr = bh.clone().requires_grad_() if bias else None
+                bor = bo.clone().requires_grad_() if bias else None
+                r = two_layer_surrogate_lif_rate_recompute_forward(
+                    xr, whr, bhr, wor, bor, p, surrogate=sg, surrogate_slope=5.0, checkpoint_size=ck)
+                r.backward(grate)
+                tag = f"{'b' if bias else 'nob'}_c{ck}_{sg}"
+                out[f"{tag}_r"] = _np(r)
+                out[f"{tag}_gx"] = _np(xr.grad)
+                out[f"{tag}_gwh"] = _np(whr.grad)
+                out[f"{tag}_gwo"] = _np(wor.grad)
+                if bias:
+                    out[f"{tag}_gbh"] = _np(bhr.grad)
+                    out[f"{tag}_gbo"] = _np(bor.grad)
+    np.savez_compressed(HERE / "two_layer_rate.npz", **out)
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
 
 

@@ -91,3 +91,18 @@ def test_packing_host_validation():
 def test_every_backend_name_is_accepted():
     for b in ("auto", "torch", "hip", "triton", "triton_generated", "triton_compile"):
         kernels._check_backend(b)
+
+
+def test_two_layer_entry_points_validate_like_the_reference():
+    x, wh, wo = torch.zeros(4, 2, 3), torch.zeros(3, 5), torch.zeros(5, 2)
+    p = myelin.LIFParams()
+    with pytest.raises(ValueError, match="ROCm device"):
+        myelin.two_layer_surrogate_lif_rate_recompute_forward(x, wh, None, wo, None, p)
+    with pytest.raises(ValueError, match="requires CUDA tensors"):
+        myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(x, wh, None, wo, None, p)
+    with pytest.raises(ValueError, match="only hard_forward=True"):
+        myelin.two_layer_surrogate_lif_rate_recompute_forward(x, wh, None, wo, None, p, hard_forward=False)
+    with pytest.raises(ValueError, match="only hard_forward=True"):
+        myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(x, wh, None, wo, None, p, hard_forward=False)
+    with pytest.raises(ValueError, match="unknown surrogate"):
+        myelin.two_layer_surrogate_lif_rate_recompute_forward(x, wh, None, wo, None, p, surrogate="relu")

@@ -23,6 +23,7 @@ def _load(name):
 PACK = _load("packing_counts.npz")
 UNR = _load("surrogate_unrolls.npz")
 LIN = _load("linear_paths.npz")
+TWO = _load("two_layer_rate.npz")
 
 
 @pytest.mark.parametrize("i", [0, 1, 2])
@@ -104,3 +105,22 @@ def test_linear_rate_paths_bitwise(bias, ck, red):
     assert np.array_equal(wr.grad.numpy(), LIN[f"{tag}_gw"])
     if bias:
         assert np.array_equal(br.grad.numpy(), LIN[f"{tag}_gb"])
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("ck", [1, 4, 11])
+@pytest.mark.parametrize("sg", ["fast_sigmoid", "superspike"])
+def test_two_layer_rate_bitwise(bias, ck, sg):
+    x, wh, bh, wo, bo, grate = (torch.from_numpy(TWO[k]) for k in ("x", "wh", "bh", "wo", "bo", "grate"))
+    xr, whr, wor = (t.clone().requires_grad_() for t in (x, wh, wo))
+    bhr = bh.clone().requires_grad_() if bias else None
+    bor = bo.clone().requires_grad_() if bias else None
+    r = R.two_layer_rate(xr, whr, bhr, wor, bor, 6.0, 0.6, -0.1, sg, 5.0, ck)
+    r.backward(grate)
+    tag = f"{'b' if bias else 'nob'}_c{ck}_{sg}"
+    assert np.array_equal(r.detach().numpy(), TWO[f"{tag}_r"])
+    for k, v in dict(gx=xr.grad, gwh=whr.grad, gwo=wor.grad).items():
+        assert np.array_equal(v.numpy(), TWO[f"{tag}_{k}"]), k
+    if bias:
+        assert np.array_equal(bhr.grad.numpy(), TWO[f"{tag}_gbh"])
+        assert np.array_equal(bor.grad.numpy(), TWO[f"{tag}_gbo"])
