@@ -184,11 +184,14 @@ int myelin_counts_to_rate(const int64_t *counts, void *out, int dtype,
  * fp32 out; bias may be NULL.
  *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]
  *   B(k,n) = trans_b ? B[n*ldb + k] : B[k*ldb + n]
- * precision MYELIN_PREC_F32 or MYELIN_PREC_BF16.  Each output element is
- * summed by one lane in a fixed k order (deterministic, no atomics).  When
- * the output has few 64x64 tiles and K is long, K is split across
- * workgroups: partial tiles go to `workspace` (workspace_elems floats; 0 or
- * NULL disables splitting) and are added in split order.
+ * precision MYELIN_PREC_F32 or MYELIN_PREC_BF16.  Outputs of at least
+ * 128 x 128 with 16-byte-aligned operands (lda, ldb multiples of 4) run on
+ * 128 x 128 tiles, others on 64 x 64 tiles; both sum each output element in
+ * the same fixed k order (deterministic, no atomics).  When the output has
+ * few tiles and K is long, K is split across workgroups: partial tiles go
+ * to `workspace` (workspace_elems floats; 0 or NULL disables splitting;
+ * myelin_gemm_workspace_elems gives the size that allows every split) and
+ * are added in split order.
  * Replaces: the per-step matmuls of LinearSynapse / the stream functions
  *   (modules.py:129-133, autograd.py:477-556) and the Triton backward GEMMs
  *   _linear_surrogate_lif_backward_inputs_kernel / _weight_kernel
@@ -234,6 +237,15 @@ int myelin_linear_lif_fwd(const float *x, const float *w, const float *bias,
  *   _linear_surrogate_lif_checkpoint_backward_chunk_packed_spikes_kernel
  *   (triton/lif.py:1934-2067).
  */
+/*
+ * Workspace (floats) with which myelin_gemm_f32 can use its full K split
+ * for an M x N x K product at `precision`; 0 when it would not split.
+ * No counterpart in the reference (its Triton GEMMs accumulate with fp32
+ * atomics instead of split-K partials).
+ */
+int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
+                                    int precision);
+
 int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
                           const float *grad_rates, float *grad_m, float *G,
                           float *gbias_acc, int64_t C, int64_t BN,

@@ -80,6 +80,8 @@ def load() -> ctypes.CDLL:
             lib = ctypes.CDLL(str(LIB_PATH))
             lib.myelin_last_error.restype = ctypes.c_char_p
             lib.myelin_abi_version.restype = ctypes.c_int
+            lib.myelin_gemm_workspace_elems.argtypes = [_I64, _I64, _I64, _INT]
+            lib.myelin_gemm_workspace_elems.restype = ctypes.c_int64
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes

@@ -296,6 +296,240 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-tile GEMM for long operands.  A workgroup of 4 waves computes a
+// 128 x 128 output tile; each wave owns a 64 x 64 quarter as 2 x 2 MFMA
+// blocks, so every LDS fragment read feeds two MFMAs and a stage carries
+// twice the flops per loaded byte of the 64 x 64 tile.  Operands are read as
+// fp32 in either layout and land in LDS k-contiguous in the MFMA input type,
+// always as 16-byte writes: an mn-contiguous operand is transposed in
+// registers (a thread loads a 4 (mn) x KQ (k) block as KQ float4 rows and
+// writes four k-vectors).  The k order of the MFMA chain is that of the
+// 64 x 64 kernel, so both produce identical sums.
+// ---------------------------------------------------------------------------
+constexpr int kBig = 128;
+
+template <int PREC>
+struct BigStage {
+  using T = typename Prec<PREC>::T;
+  static constexpr int KS = Prec<PREC>::KS;                         // 128 bytes of k per row
+  static constexpr int LD = KS + 16 / static_cast<int>(sizeof(T));  // + 16-byte pad
+  alignas(16) T a[kBig][LD];
+  alignas(16) T b[kBig][LD];
+};
+
+template <int PREC>
+__device__ __forceinline__ void store_kvec(typename Prec<PREC>::T *dst, const float *x) {
+  if constexpr (PREC == 1) {
+    bf16x8 t;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = static_cast<__bf16>(x[j]);
+    *reinterpret_cast<bf16x8 *>(dst) = t;
+  } else {
+    *reinterpret_cast<f4 *>(dst) = f4{x[0], x[1], x[2], x[3]};
+  }
+}
+
+// One operand's stage: 128 (mn) x KS (k) from fp32 global memory.
+//  KC: element (mn, k) at base[mn * ld + k];  MN: at base[k * ld + mn].
+// Requires 16-byte aligned base and ld % 4 == 0.
+template <int PREC, bool KC>
+struct BigLoader {
+  static constexpr int KS = Prec<PREC>::KS;
+  static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));  // k per LDS vector
+  static constexpr int NP = KC ? kBig * KS / KQ / 256 : 1;                          // pieces per thread (4 | 1)
+  float v[4 * KQ];
+  const float *p;
+  int64_t ld, mn_lim;
+  int mn[NP], kk[NP];
+
+  __device__ __forceinline__ void init(int tid, const float *base, int64_t mn0, int64_t mn_total, int64_t ld_) {
+    ld = ld_;
+    mn_lim = mn_total - mn0;
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const int idx = e * 256 + tid;
+        mn[e] = idx / (KS / KQ);
+        kk[e] = (idx % (KS / KQ)) * KQ;
+      }
+      p = base + mn0 * ld;
+    } else {
+      mn[0] = (tid & 31) * 4;
+      kk[0] = (tid >> 5) * KQ;
+      p = base + mn0;
+    }
+  }
+
+  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const int64_t k = k0 + kk[e];
+        const float *q = p + mn[e] * ld + k;
+        if (mn[e] < mn_lim && k + KQ <= ke) {
+#pragma unroll
+          for (int h = 0; h < KQ; h += 4) {
+            const f4 t = *reinterpret_cast<const f4 *>(q + h);
+            v[e * KQ + h] = t.x;
+            v[e * KQ + h + 1] = t.y;
+            v[e * KQ + h + 2] = t.z;
+            v[e * KQ + h + 3] = t.w;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < KQ; ++i) v[e * KQ + i] = (mn[e] < mn_lim && k + i < ke) ? q[i] : 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KQ; ++j) {
+        const int64_t k = k0 + kk[0] + j;
+        const float *q = p + k * ld + mn[0];
+        if (k < ke && mn[0] + 3 < mn_lim) {
+          const f4 t = *reinterpret_cast<const f4 *>(q);
+          v[4 * j] = t.x;
+          v[4 * j + 1] = t.y;
+          v[4 * j + 2] = t.z;
+          v[4 * j + 3] = t.w;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[4 * j + i] = (k < ke && mn[0] + i < mn_lim) ? q[i] : 0.0f;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) store_kvec<PREC>(&dst[mn[e]][kk[e]], &v[e * KQ]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x[KQ];
+#pragma unroll
+        for (int j = 0; j < KQ; ++j) x[j] = v[4 * j + i];
+        store_kvec<PREC>(&dst[mn[0] + i][kk[0]], x);
+      }
+    }
+  }
+};
+
+template <int PREC>
+__device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
+  constexpr int KS = Prec<PREC>::KS, KM = Prec<PREC>::KM, KV = Prec<PREC>::KV;
+  const int r = 64 * wm + (lane & 31), c = 64 * wn + (lane & 31), kq = (lane >> 5) * KV;
+#pragma unroll
+  for (int kk = 0; kk < KS; kk += KM) {
+    if constexpr (PREC == 1) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(&st.a[r][kk + kq]);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(&st.a[r + 32][kk + kq]);
+      const bf16x8 b0 = *reinterpret_cast<const bf16x8 *>(&st.b[c][kk + kq]);
+      const bf16x8 b1 = *reinterpret_cast<const bf16x8 *>(&st.b[c + 32][kk + kq]);
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+    } else {
+      const float a0 = st.a[r][kk + kq], a1 = st.a[r + 32][kk + kq];
+      const float b0 = st.b[c][kk + kq], b1 = st.b[c + 32][kk + kq];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    }
+  }
+}
+
+// Workgroup -> output tile.  Consecutive workgroup ids go round-robin to the
+// 8 XCDs (each with its own L2), so when the grid is a multiple of 8 each
+// XCD is handed a contiguous run of logical tiles; logical tiles walk groups
+// of 8 tile rows column by column, so a run shares A rows and B columns.
+__device__ __forceinline__ void big_tile(int64_t bid, int64_t nblk, int64_t tiles_m, int64_t tiles_n, int64_t &tm,
+                                         int64_t &tn) {
+  int64_t t = bid;
+  if (nblk % 8 == 0) t = (bid % 8) * (nblk / 8) + bid / 8;
+  constexpr int64_t G = 8;
+  const int64_t per_group = G * tiles_n;
+  const int64_t group = t / per_group, first = group * G;
+  const int64_t gs = (tiles_m - first < G) ? tiles_m - first : G;
+  const int64_t in = t - group * per_group;
+  tm = first + in % gs;
+  tn = in / gs;
+}
+
+template <int PREC, bool TA, bool TB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
+  __shared__ BigStage<PREC> st[2];
+  constexpr int KS = Prec<PREC>::KS;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+  const int64_t tiles_m = (g.M + kBig - 1) / kBig, tiles_n = (g.N + kBig - 1) / kBig;
+  int64_t tm, tn;
+  big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * kBig, n0 = tn * kBig;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+
+  BigLoader<PREC, !TA> la;
+  la.init(tid, g.A, m0, g.M, g.lda);
+  BigLoader<PREC, TB> lb;
+  lb.init(tid, g.B, n0, g.N, g.ldb);
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if (kb < ke) {
+    la.load(kb, ke);
+    lb.load(kb, ke);
+    la.store(st[0].a);
+    lb.store(st[0].b);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t k0 = kb; k0 < ke; k0 += KS) {
+      const bool more = k0 + KS < ke;
+      if (more) {
+        la.load(k0 + KS, ke);
+        lb.load(k0 + KS, ke);
+      }
+      big_mfma<PREC>(st[buf], wm, wn, lane, acc);
+      if (more) {
+        la.store(st[buf ^ 1].a);
+        lb.store(st[buf ^ 1].b);
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = n0 + 64 * wn + 32 * j + (lane & 31);
+    if (col >= g.N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + 64 * wm + 32 * i + acc_row(r, lane);
+        if (row >= g.M) continue;
+        if (g.splits > 1) {
+          g.ws[(static_cast<int64_t>(blockIdx.y) * g.M + row) * g.N + col] = acc[i][j][r];
+        } else {
+          float *dst = g.C + row * g.ldc + col;
+          float v = g.accumulate ? *dst + acc[i][j][r] : acc[i][j][r];
+          if (g.bias != nullptr) v = v + g.bias[col];
+          *dst = v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused current GEMM + LIF recurrence.
 // ---------------------------------------------------------------------------
 struct LinArgs {
@@ -463,25 +697,85 @@ struct PreBwdArgs {
   int rule;
 };
 
-template <int SID>
+// Serial time loops over [L] steps stream their operands in blocks of kPipe
+// steps, the next block's loads issued before the current block computes.
+// Block 0 holds the first f = L - (nblk - 1) * kPipe steps (1..kPipe), the
+// rest are full, so the steady state is straight-line code with a fixed
+// number of loads in flight; every load address is clamped into range, so
+// no load is predicated.
+constexpr int kPipe = 16;
+
+template <int SID, bool GS>
+__device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, float pre, float gsv,
+                                             float gstep, float &gm, float &gb) {
+  const float c = p.slope * (pre - p.thr);
+  const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (pre >= p.thr) : (c >= 0.0f);
+  const float s = sp ? 1.0f : 0.0f;
+  const float d = p.slope * sg_deriv<SID>(c);
+  float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
+  if constexpr (GS) gp = gp + gsv * d;
+  if (p.grate != nullptr) gp = gp + gstep * d;
+  p.G[j * p.BN + i] = gp;
+  gb = gb + gp;
+  gm = gp * p.decay;
+}
+
+// reverse time: relative index r = C - 1 - j
+template <int SID, bool GS>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= p.BN) return;
+  const int64_t C = p.C;
   float gm = p.gm[i];
   const float gstep = p.grate != nullptr ? p.grate[i] / p.rate_denominator : 0.0f;
   float gb = 0.0f;
-  for (int64_t j = p.C - 1; j >= 0; --j) {
-    const float pre = p.pre[j * p.BN + i];
-    const float c = p.slope * (pre - p.thr);
-    const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (pre >= p.thr) : (c >= 0.0f);
-    const float s = sp ? 1.0f : 0.0f;
-    const float d = p.slope * sg_deriv<SID>(c);
-    float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
-    if (p.gs != nullptr) gp = gp + p.gs[j * p.BN + i] * d;
-    if (p.grate != nullptr) gp = gp + gstep * d;
-    p.G[j * p.BN + i] = gp;
-    gb = gb + gp;
-    gm = gp * p.decay;
+  const float *pre = p.pre + i;
+  const float *gs = GS ? p.gs + i : nullptr;
+  const int64_t nblk = (C + kPipe - 1) / kPipe;
+  const int64_t f = C - (nblk - 1) * kPipe;
+  float pv[kPipe], gv[kPipe];
+#pragma unroll
+  for (int u = 0; u < kPipe; ++u) {
+    const int64_t j = C - 1 - (u < f ? u : f - 1);
+    pv[u] = pre[j * p.BN];
+    if constexpr (GS) gv[u] = gs[j * p.BN];
+  }
+  // block 0 (f steps), prefetching block 1 (or re-reading block 0 when alone)
+  {
+    const int64_t r0 = nblk > 1 ? f : 0;
+    float np[kPipe], ng[kPipe];
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) {
+      const int64_t r = r0 + u < C ? r0 + u : C - 1;
+      np[u] = pre[(C - 1 - r) * p.BN];
+      if constexpr (GS) ng[u] = gs[(C - 1 - r) * p.BN];
+    }
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u)
+      if (u < f) pre_bwd_step<SID, GS>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) {
+      pv[u] = np[u];
+      if constexpr (GS) gv[u] = ng[u];
+    }
+  }
+  for (int64_t r0 = f; r0 < C; r0 += kPipe) {
+    const int64_t rn = r0 + kPipe < C ? r0 + kPipe : r0;
+    float np[kPipe], ng[kPipe];
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) {
+      np[u] = pre[(C - 1 - rn - u) * p.BN];
+      if constexpr (GS) ng[u] = gs[(C - 1 - rn - u) * p.BN];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u)
+      pre_bwd_step<SID, GS>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) {
+      pv[u] = np[u];
+      if constexpr (GS) gv[u] = ng[u];
+    }
   }
   p.gm[i] = gm;
   if (p.gbias_acc != nullptr) p.gbias_acc[i] = p.gbias_acc[i] + gb;
@@ -521,6 +815,37 @@ struct CurArgs {
   int rule;
 };
 
+// One step of the currents recurrence for lane (b, n); output stores are
+// chosen at compile time (PRE: pre-reset membrane, SPK: dense spikes, PK:
+// ballot-packed words), checkpoints and counts at run time.
+template <bool PRE, bool SPK, bool PK>
+__device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, bool act, int64_t flat, int64_t BN,
+                                         int64_t gid, int lane, float &m, float &cnt, int64_t &ck_row,
+                                         int64_t &next_ck) {
+  if (p.ckpt != nullptr && t == next_ck) {
+    if (act) p.ckpt[ck_row * BN + flat] = m;
+    ++ck_row;
+    next_ck += p.ckpt_every;
+  }
+  float mp = m * p.decay;
+  mp = mp + c;
+  const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (mp >= p.thr) : (p.slope * (mp - p.thr) >= 0.0f);
+  if (act) {
+    if constexpr (PRE) p.pre[(t - p.pre_origin) * BN + flat] = mp;
+    if constexpr (SPK) p.spikes[t * BN + flat] = sp ? 1.0f : 0.0f;
+  }
+  m = sp ? p.reset : mp;
+  cnt = cnt + (sp ? 1.0f : 0.0f);
+  if constexpr (PK) {
+    const uint64_t bits = __ballot(act && sp);
+    const int64_t gw = (gid - lane) >> 5;  // the wave's first word
+    int32_t *row = p.packed + t * p.B * p.W;
+    if (lane == 0 && gw < p.B * p.W) row[gw] = static_cast<int32_t>(bits & 0xffffffffu);
+    if (lane == 32 && gw + 1 < p.B * p.W) row[gw + 1] = static_cast<int32_t>(bits >> 32);
+  }
+}
+
+template <bool PRE, bool SPK, bool PK>
 __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t g = gid >> 5;
@@ -536,34 +861,37 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   // step ck_origin + k*ckpt_every
   int64_t ck_row = (p.t_begin - p.ck_origin + p.ckpt_every - 1) / p.ckpt_every;
   int64_t next_ck = p.ck_origin + ck_row * p.ckpt_every;
-  for (int64_t t = p.t_begin; t < p.t_end; ++t) {
-    if (p.ckpt != nullptr && t == next_ck) {
-      if (act) p.ckpt[ck_row * BN + flat] = m;
-      ++ck_row;
-      next_ck += p.ckpt_every;
-    }
-    bool sp = false;
-    if (act) {
-      float mp = m * p.decay;
-      mp = mp + p.cur[(t - p.t_begin) * BN + flat];
-      if (p.rule == MYELIN_RULE_THRESHOLD) {
-        sp = mp >= p.thr;
-      } else {
-        const float c = p.slope * (mp - p.thr);
-        sp = c >= 0.0f;
-      }
-      if (p.pre != nullptr) p.pre[(t - p.pre_origin) * BN + flat] = mp;
-      if (p.spikes != nullptr) p.spikes[t * BN + flat] = sp ? 1.0f : 0.0f;
-      m = sp ? p.reset : mp;
-      cnt = cnt + (sp ? 1.0f : 0.0f);
-    }
-    if (p.packed != nullptr) {
-      const uint64_t bits = __ballot(sp);
-      const int64_t gw = (gid - lane) >> 5;  // the wave's first word
-      int32_t *row = p.packed + t * p.B * p.W;
-      if (lane == 0 && gw < p.B * p.W) row[gw] = static_cast<int32_t>(bits & 0xffffffffu);
-      if (lane == 32 && gw + 1 < p.B * p.W) row[gw + 1] = static_cast<int32_t>(bits >> 32);
-    }
+  // inactive lanes read element 0 and store nothing
+  const float *cur = p.cur + (act ? flat : 0);
+  const int64_t L = p.t_end - p.t_begin;
+  const int64_t nblk = (L + kPipe - 1) / kPipe;
+  const int64_t f = L - (nblk - 1) * kPipe;
+  float cv[kPipe];
+#pragma unroll
+  for (int u = 0; u < kPipe; ++u) cv[u] = cur[(u < f ? u : f - 1) * BN];
+  {
+    const int64_t r0 = nblk > 1 ? f : 0;
+    float nc[kPipe];
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) nc[u] = cur[(r0 + u < L ? r0 + u : L - 1) * BN];
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u)
+      if (u < f)
+        cur_step<PRE, SPK, PK>(p, p.t_begin + u, cv[u], act, flat, BN, gid, lane, m, cnt, ck_row, next_ck);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) cv[u] = nc[u];
+  }
+  for (int64_t r0 = f; r0 < L; r0 += kPipe) {
+    const int64_t rn = r0 + kPipe < L ? r0 + kPipe : r0;
+    float nc[kPipe];
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) nc[u] = cur[(rn + u) * BN];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u)
+      cur_step<PRE, SPK, PK>(p, p.t_begin + r0 + u, cv[u], act, flat, BN, gid, lane, m, cnt, ck_row, next_ck);
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) cv[u] = nc[u];
   }
   if (act) {
     if (p.m_final != nullptr) p.m_final[flat] = m;
@@ -588,31 +916,63 @@ void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) 
     gemm_kernel<PREC, true, true, VEC><<<grid, dim3(256), 0, s>>>(g);
 }
 
+// K splits for an output of `tiles` workgroups: split when the output alone
+// gives under ~2 workgroups per CU (load latency stays exposed with one) and
+// K is long.
+template <int PREC>
+int64_t plan_splits(int64_t tiles, int64_t K, bool big) {
+  constexpr int KS = Prec<PREC>::KS;
+  const int64_t want = 512;
+  if (tiles >= want || K < 8 * KS) return 1;
+  int64_t splits = cdiv(want, tiles);
+  const int64_t max_by_k = K / (4 * KS);
+  if (splits > max_by_k) splits = max_by_k;
+  if (splits > 64) splits = 64;
+  return splits < 1 ? 1 : splits;
+}
+
+// the 128 x 128 kernel takes outputs of at least one full tile per side
+// whose operands allow 16-byte loads
+bool use_big(const GemmArgs &g) {
+  return g.M >= kBig && g.N >= kBig && al16(g.A) && al16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0;
+}
+
+template <int PREC, bool TA, bool TB>
+void launch_big(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  gemm_big<PREC, TA, TB><<<grid, dim3(256), 0, s>>>(g);
+}
+
 template <int PREC>
 int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
   constexpr int KS = Prec<PREC>::KS;
-  const int64_t tiles = cdiv(g.N, kTile) * cdiv(g.M, kTile);
-  if (cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
-  // split K when the output alone gives under ~2 workgroups per CU and K is long
-  int64_t splits = 1;
-  if (g.ws != nullptr && tiles < 512 && g.K >= 8 * KS) {
-    splits = cdiv(512, tiles);
-    const int64_t max_by_k = g.K / (4 * KS);
-    if (splits > max_by_k) splits = max_by_k;
-    if (splits > 64) splits = 64;
-    while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
-    if (splits < 1) splits = 1;
-  }
+  const bool big = use_big(g);
+  const int64_t edge = big ? kBig : kTile;
+  const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
+  if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
+  int64_t splits = g.ws != nullptr ? plan_splits<PREC>(tiles, g.K, big) : 1;
+  while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
   g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
   splits = cdiv(g.K, g.kchunk);
   if (splits < 1) splits = 1;
   g.splits = static_cast<int>(splits);
-  const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
-  const bool vec = al16(g.A) && al16(g.B) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
-  if (vec)
-    launch_gemm_v<PREC, true>(g, ta, tb, grid, s);
-  else
-    launch_gemm_v<PREC, false>(g, ta, tb, grid, s);
+  if (big) {
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
+    if (!ta && !tb)
+      launch_big<PREC, false, false>(g, grid, s);
+    else if (!ta && tb)
+      launch_big<PREC, false, true>(g, grid, s);
+    else if (ta && !tb)
+      launch_big<PREC, true, false>(g, grid, s);
+    else
+      launch_big<PREC, true, true>(g, grid, s);
+  } else {
+    const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
+    const bool vec = al16(g.A) && al16(g.B) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
+    if (vec)
+      launch_gemm_v<PREC, true>(g, ta, tb, grid, s);
+    else
+      launch_gemm_v<PREC, false>(g, ta, tb, grid, s);
+  }
   if (int rc = myelin::launched("gemm")) return rc;
   if (splits > 1) {
     splitk_reduce<<<dim3(cdiv(g.M * g.N, 256)), dim3(256), 0, s>>>(g);
@@ -621,7 +981,47 @@ int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
   return MYELIN_OK;
 }
 
+template <int SID>
+void launch_pre_bwd(const PreBwdArgs &a, bool gs, dim3 grid, hipStream_t s) {
+  if (gs)
+    linear_pre_bwd<SID, true><<<grid, dim3(256), 0, s>>>(a);
+  else
+    linear_pre_bwd<SID, false><<<grid, dim3(256), 0, s>>>(a);
+}
+
+template <bool PRE, bool SPK>
+void launch_cur_pk(const CurArgs &a, bool pk, dim3 grid, hipStream_t s) {
+  if (pk)
+    lif_currents_fwd<PRE, SPK, true><<<grid, dim3(256), 0, s>>>(a);
+  else
+    lif_currents_fwd<PRE, SPK, false><<<grid, dim3(256), 0, s>>>(a);
+}
+
+void launch_currents(const CurArgs &a, dim3 grid, hipStream_t s) {
+  const bool pre = a.pre != nullptr, spk = a.spikes != nullptr, pk = a.packed != nullptr;
+  if (pre && spk)
+    launch_cur_pk<true, true>(a, pk, grid, s);
+  else if (pre)
+    launch_cur_pk<true, false>(a, pk, grid, s);
+  else if (spk)
+    launch_cur_pk<false, true>(a, pk, grid, s);
+  else
+    launch_cur_pk<false, false>(a, pk, grid, s);
+}
+
 }  // namespace
+
+extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, int precision) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  int64_t most = 1;
+  for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
+    const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
+    const bool big = edge == kBig;
+    const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, big) : plan_splits<0>(tiles, K, big);
+    if (s > most) most = s;
+  }
+  return most > 1 ? most * M * N : 0;
+}
 
 extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
                                int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b,
@@ -722,13 +1122,14 @@ extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
                static_cast<float>(T_total), rule};
   const dim3 grid(cdiv(BN, 256));
   hipStream_t s = myelin::as_hip(stream);
+  const bool gs = grad_spikes != nullptr;
   switch (surrogate_id) {
-    case MYELIN_SG_SIGMOID: linear_pre_bwd<MYELIN_SG_SIGMOID><<<grid, dim3(256), 0, s>>>(a); break;
-    case MYELIN_SG_FAST_SIGMOID: linear_pre_bwd<MYELIN_SG_FAST_SIGMOID><<<grid, dim3(256), 0, s>>>(a); break;
-    case MYELIN_SG_ATAN: linear_pre_bwd<MYELIN_SG_ATAN><<<grid, dim3(256), 0, s>>>(a); break;
-    case MYELIN_SG_TRIANGULAR: linear_pre_bwd<MYELIN_SG_TRIANGULAR><<<grid, dim3(256), 0, s>>>(a); break;
-    case MYELIN_SG_SUPERSPIKE: linear_pre_bwd<MYELIN_SG_SUPERSPIKE><<<grid, dim3(256), 0, s>>>(a); break;
-    case MYELIN_SG_MULTI_GAUSSIAN: linear_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN><<<grid, dim3(256), 0, s>>>(a); break;
+    case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, grid, s); break;
+    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, grid, s); break;
+    case MYELIN_SG_ATAN: launch_pre_bwd<MYELIN_SG_ATAN>(a, gs, grid, s); break;
+    case MYELIN_SG_TRIANGULAR: launch_pre_bwd<MYELIN_SG_TRIANGULAR>(a, gs, grid, s); break;
+    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd<MYELIN_SG_SUPERSPIKE>(a, gs, grid, s); break;
+    case MYELIN_SG_MULTI_GAUSSIAN: launch_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN>(a, gs, grid, s); break;
     default: return myelin::invalid("linear_pre_bwd: unknown surrogate id %d", surrogate_id);
   }
   return myelin::launched("linear_pre_bwd");
@@ -782,6 +1183,6 @@ extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, f
   a.rate_denominator = static_cast<float>(T);
   a.rule = rule;
   const int64_t lanes = B * a.W * 32;
-  lif_currents_fwd<<<dim3(cdiv(lanes, 256)), dim3(256), 0, myelin::as_hip(stream)>>>(a);
+  launch_currents(a, dim3(cdiv(lanes, 256)), myelin::as_hip(stream));
   return myelin::launched("lif_currents_fwd");
 }

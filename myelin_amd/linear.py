@@ -32,23 +32,11 @@ import torch
 from myelin_amd import _lib
 
 
-def _split_k(M: int, N: int, K: int, prec: int) -> int:
-    """Number of K splits the GEMM will use for an output this size (the
-    same rule as launch_gemm in csrc/synapse.hip)."""
-
-    ks = 64 if prec == _lib.PREC["bf16"] else 32
-    tiles = -(-M // 64) * -(-N // 64)
-    if tiles >= 512 or K < 8 * ks:
-        return 1
-    return max(1, min(-(-512 // tiles), K // (4 * ks), 64))
-
-
 def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None):
-    splits = _split_k(M, N, K, prec)
-    ws = torch.empty(splits * M * N, dtype=torch.float32, device=C.device) if splits > 1 else None
+    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec)
+    ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
     _lib.call("myelin_gemm_f32", _lib.ptr(A), _lib.ptr(B), _lib.ptr(bias), _lib.ptr(C), M, N, K, lda, ldb, ldc,
-              int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws), 0 if ws is None else ws.numel(),
-              stream)
+              int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws), n_ws, stream)
 
 
 class HipLinearFunction(torch.autograd.Function):

@@ -82,3 +82,13 @@ def test_pointer_types_are_plain():
         for a in argtypes:
             assert a in (ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int, ctypes.c_uint32)
     assert torch is not None
+
+
+def test_gemm_workspace_size_is_host_only_and_covers_the_split():
+    lib = _lib.load()
+    # 784 x 2048 output over K = 12800: 112 tiles of 128 x 128 -> split 5 ways
+    assert lib.myelin_gemm_workspace_elems(784, 2048, 12800, _lib.PREC["bf16"]) == 5 * 784 * 2048
+    # enough tiles, or a short K: no split, no workspace
+    assert lib.myelin_gemm_workspace_elems(12800, 2048, 784, _lib.PREC["bf16"]) == 0
+    assert lib.myelin_gemm_workspace_elems(784, 2048, 100, _lib.PREC["fp32"]) == 0
+    assert lib.myelin_gemm_workspace_elems(0, 5, 5, 0) == 0

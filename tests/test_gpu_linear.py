@@ -42,7 +42,8 @@ def _bf16(t):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (64, 64, 64), (70, 33, 100), (300, 17, 784), (5, 200, 10),
-                                   (129, 65, 31)])
+                                   (129, 65, 31), (128, 128, 64), (300, 260, 1000), (256, 384, 3000),
+                                   (520, 132, 200), (129, 130, 64)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
 def test_gemm(M, N, K, ta, tb, prec):
@@ -66,6 +67,30 @@ def test_gemm(M, N, K, ta, tb, prec):
     Cacc = C0.to(DEV)
     _gemm(Ad, Bd, Cacc, M, N, K, A.shape[1], B.shape[1], N, ta, tb, True, _lib.PREC[prec], stream, bias=bias.to(DEV))
     assert_norm_close(Cacc.cpu().double(), C0.double() + ref + bias.double(), 1e-5, "C accumulate + bias")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_gemm_tile_sizes_sum_identically(ta, tb, prec):
+    """The 128 x 128 kernel (16-byte-aligned operands) and the 64 x 64 kernel
+    (same operands one float off alignment) run the same k order per output
+    element, so with no K split both give bit-identical products."""
+
+    _print_case(test="gemm_tiles", ta=ta, tb=tb, prec=prec)
+    M, N, K = 260, 200, 300
+    g = seeded(99)
+    A = torch.randn((K, M) if ta else (M, K), generator=g)
+    B = torch.randn((N, K) if tb else (K, N), generator=g)
+    stream = _lib.stream(torch.device(DEV))
+    out = []
+    for shift in (0, 1):
+        Ab = torch.zeros(A.numel() + 4, device=DEV)
+        Ab[shift:shift + A.numel()] = A.reshape(-1).to(DEV)
+        Ad = Ab[shift:shift + A.numel()].view(A.shape)
+        C = torch.empty(M, N, device=DEV)
+        _gemm(Ad, B.to(DEV), C, M, N, K, A.shape[1], B.shape[1], N, ta, tb, False, _lib.PREC[prec], stream)
+        out.append(C.cpu())
+    assert torch.equal(out[0], out[1])
 
 
 def test_linear_synapse_function_grads():
