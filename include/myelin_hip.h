@@ -204,6 +204,30 @@ int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C,
                     myelin_stream_t stream);
 
 /*
+ * myelin_gemm_f32 with operand types: a_dtype = b_dtype = MYELIN_DT_F32, or
+ * MYELIN_DT_BF16 (bf16 values in memory, precision MYELIN_PREC_BF16 only,
+ * always on 128 x 128 tiles; k-contiguous operand rows 16-byte aligned,
+ * mn-contiguous ones 8-byte aligned).  bf16 operands give bit-identical
+ * results to fp32 operands holding the same values, at half the bytes.
+ * Replaces: as myelin_gemm_f32.
+ */
+int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype,
+                const float *bias, float *C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, int trans_a,
+                int trans_b, int accumulate, int precision, float *workspace,
+                int64_t workspace_elems, myelin_stream_t stream);
+
+/*
+ * Workspace (floats) with which myelin_gemm_f32 can use its full K split
+ * for an M x N x K product at `precision`; 0 when it would not split.
+ * No counterpart in the reference (its Triton GEMMs accumulate with fp32
+ * atomics instead of split-K partials).
+ */
+int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
+                                    int precision);
+
+
+/*
  * Streamed synapse fused ahead of the LIF update, over steps
  * [t_begin, t_end) of x [T, B, F] with W [F, N] (+ bias [N]):
  *   I_t = x_t @ W + bias ; m' = m*decay + I_t ; s = rule(m') ; m = s ? reset : m'
@@ -227,28 +251,49 @@ int myelin_linear_lif_fwd(const float *x, const float *w, const float *bias,
                           myelin_stream_t stream);
 
 /*
+ * myelin_linear_lif_fwd for the bf16 synapse from bf16 operands in memory:
+ * x [T, B, F] and the transposed weight wt [N, F] (both bf16, 16-byte
+ * aligned rows, F % 8 == 0), on 128 x 128 tiles.  Bit-identical to
+ * myelin_linear_lif_fwd(precision = MYELIN_PREC_BF16) on the same values.
+ * Replaces: as myelin_linear_lif_fwd.
+ */
+int myelin_linear_lif_fwd_bf16(const uint16_t *x, const uint16_t *wt,
+                               const float *bias, const float *m0,
+                               float *m_final, float *spikes, float *pre,
+                               int32_t *packed, float *rates, float *ckpt,
+                               int64_t T, int64_t B, int64_t F, int64_t N,
+                               int64_t t_begin, int64_t t_end,
+                               int64_t ckpt_every, float decay,
+                               float threshold, float reset, float slope,
+                               int rule, myelin_stream_t stream);
+
+/*
+ * bf16 operand copies (round to nearest even, as the bf16 GEMMs round fp32
+ * operands): dst[i] = bf16(src[i]) (both 16-byte aligned), and the
+ * transposed copy dst[c*rows + r] = bf16(src[r*cols + c]).  No counterpart
+ * in the reference (its tl.dot consumes fp32 operands).
+ */
+int myelin_cast_bf16(const float *src, uint16_t *dst, int64_t n,
+                     myelin_stream_t stream);
+int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows,
+                          int64_t cols, myelin_stream_t stream);
+
+/*
  * Reverse recurrence over C steps of a saved pre-reset trace [C, BN]:
  *   d = slope*sigma'(slope*(pre - thr)); gp = gm*((1-s) + (reset-pre)*d)
  *   + g_spike*d; G[j] = gp; gm = gp*decay   (grad_m is in/out)
  * g_spike = grad_spikes[j] (may be NULL) plus grad_rates/T_total (may be
- * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.
+ * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.  G is written
+ * as g_dtype MYELIN_DT_F32, or MYELIN_DT_BF16 (round to nearest even, the
+ * rounding the bf16 GEMMs apply) when only bf16 GEMMs read it.
  * Replaces: the reverse loops of the torch stream / checkpoint / rate
  *   Functions (autograd.py:540-556,694-715,857-883) and
  *   _linear_surrogate_lif_checkpoint_backward_chunk_packed_spikes_kernel
  *   (triton/lif.py:1934-2067).
  */
-/*
- * Workspace (floats) with which myelin_gemm_f32 can use its full K split
- * for an M x N x K product at `precision`; 0 when it would not split.
- * No counterpart in the reference (its Triton GEMMs accumulate with fp32
- * atomics instead of split-K partials).
- */
-int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
-                                    int precision);
-
 int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
-                          const float *grad_rates, float *grad_m, float *G,
-                          float *gbias_acc, int64_t C, int64_t BN,
+                          const float *grad_rates, float *grad_m, void *G,
+                          int g_dtype, float *gbias_acc, int64_t C, int64_t BN,
                           int64_t T_total, float decay, float threshold,
                           float reset, float slope, int surrogate_id, int rule,
                           myelin_stream_t stream);

@@ -50,8 +50,12 @@ SIGNATURES: dict[str, list] = {
     "myelin_packed_counts_keep_last": [_P, _I64, _I64, _I64, _P, _P],
     "myelin_counts_to_rate": [_P, _P, _INT, _I64, _I64, _P],
     "myelin_gemm_f32": [_P, _P, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P],
+    "myelin_gemm": [_P, _INT, _P, _INT, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P],
     "myelin_linear_lif_fwd": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _INT, _P],
-    "myelin_linear_pre_bwd": [_P] * 6 + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
+    "myelin_linear_lif_fwd_bf16": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _P],
+    "myelin_cast_bf16": [_P, _P, _I64, _P],
+    "myelin_transpose_bf16": [_P, _P, _I64, _I64, _P],
+    "myelin_linear_pre_bwd": [_P] * 5 + [_INT, _P] + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],
     "myelin_lif_currents_fwd": [_P] * 9 + [_I64] * 8 + [_F] * 4 + [_INT, _P],
 }

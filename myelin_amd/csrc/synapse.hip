@@ -18,6 +18,8 @@
 // membrane (and spike counts) stay in registers across chunks, so currents
 // never go to HBM.
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -220,8 +222,8 @@ __device__ __forceinline__ void tile_mma(LA &la, LB &lb, int64_t kb, int64_t ke,
 // workspace and splitk_reduce adds them in split order (deterministic).
 // ---------------------------------------------------------------------------
 struct GemmArgs {
-  const float *A;
-  const float *B;
+  const void *A;  // float, or bf16 bits (uint16_t) for the 128 x 128 kernel's bf16 operands
+  const void *B;
   const float *bias;  // [N] added in the epilogue, or null
   float *C;
   float *ws;          // [splits, M, N] when split
@@ -229,7 +231,7 @@ struct GemmArgs {
   int accumulate, splits;
 };
 
-template <int PREC, bool TA, bool TB, bool VEC>
+template <int PREC, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   __shared__ Stage<PREC> st[2];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
@@ -237,27 +239,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int64_t kb = static_cast<int64_t>(blockIdx.z) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
-  TileLoader<PREC, !TA, VEC> la;
+  TileLoader<PREC, !TA, VA> la;
   if constexpr (TA) {
-    la.map_rowcontig(tid, g.A, m0, g.M, g.lda);
+    la.map_rowcontig(tid, static_cast<const float *>(g.A), m0, g.M, g.lda);
   } else {
     la.map_kcontig(tid);
 #pragma unroll
-    for (int e = 0; e < TileLoader<PREC, true, VEC>::NV; ++e) {
+    for (int e = 0; e < TileLoader<PREC, true, VA>::NV; ++e) {
       const int64_t m = m0 + la.roff[e];
-      la.base[e] = m < g.M ? g.A + m * g.lda : nullptr;
+      la.base[e] = m < g.M ? static_cast<const float *>(g.A) + m * g.lda : nullptr;
     }
   }
-  TileLoader<PREC, TB, VEC> lb;
+  TileLoader<PREC, TB, VB> lb;
   if constexpr (TB) {
     lb.map_kcontig(tid);
 #pragma unroll
-    for (int e = 0; e < TileLoader<PREC, true, VEC>::NV; ++e) {
+    for (int e = 0; e < TileLoader<PREC, true, VB>::NV; ++e) {
       const int64_t n = n0 + lb.roff[e];
-      lb.base[e] = n < g.N ? g.B + n * g.ldb : nullptr;
+      lb.base[e] = n < g.N ? static_cast<const float *>(g.B) + n * g.ldb : nullptr;
     }
   } else {
-    lb.map_rowcontig(tid, g.B, n0, g.N, g.ldb);
+    lb.map_rowcontig(tid, static_cast<const float *>(g.B), n0, g.N, g.ldb);
   }
 
   f32x16 acc;
@@ -341,10 +343,13 @@ struct BigLoader {
   const float *p;
   int64_t ld, mn_lim;
   int mn[NP], kk[NP];
+  bool full;  // all 128 mn of the tile exist (uniform)
 
-  __device__ __forceinline__ void init(int tid, const float *base, int64_t mn0, int64_t mn_total, int64_t ld_) {
+  __device__ __forceinline__ void init(int tid, const void *base_, int64_t mn0, int64_t mn_total, int64_t ld_) {
+    const float *base = static_cast<const float *>(base_);
     ld = ld_;
     mn_lim = mn_total - mn0;
+    full = mn_lim >= kBig;
     if constexpr (KC) {
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
@@ -360,7 +365,41 @@ struct BigLoader {
     }
   }
 
+  // interior stages: straight-line 16-byte loads, no guards
+  __device__ __forceinline__ void fast(int64_t k0) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const float *q = p + mn[e] * ld + k0 + kk[e];
+#pragma unroll
+        for (int h = 0; h < KQ; h += 4) {
+          const f4 t = *reinterpret_cast<const f4 *>(q + h);
+          v[e * KQ + h] = t.x;
+          v[e * KQ + h + 1] = t.y;
+          v[e * KQ + h + 2] = t.z;
+          v[e * KQ + h + 3] = t.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KQ; ++j) {
+        const f4 t = *reinterpret_cast<const f4 *>(p + (k0 + kk[0] + j) * ld + mn[0]);
+        v[4 * j] = t.x;
+        v[4 * j + 1] = t.y;
+        v[4 * j + 2] = t.z;
+        v[4 * j + 3] = t.w;
+      }
+    }
+  }
+
   __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
+    if (full && k0 + KS <= ke)
+      fast(k0);
+    else
+      slow(k0, ke);
+  }
+
+  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
     if constexpr (KC) {
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
@@ -415,6 +454,130 @@ struct BigLoader {
   }
 };
 
+// The same stage from bf16 operands in memory (raw 16-bit values; bf16 MFMA
+// only).  KC: one 16-byte load of 8 k per piece, copied to LDS as is.  MN: a
+// thread loads a 4 (mn) x 8 (k) block as eight 8-byte rows and regroups the
+// halves into four 8-k vectors.  Requires 16-byte (KC) / 8-byte (MN)
+// aligned rows: base aligned and ld % 8 == 0 (KC) / ld % 4 == 0 (MN).
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+template <bool KC>
+struct BigLoaderH {
+  static constexpr int KS = Prec<1>::KS;  // 64
+  static constexpr int NP = KC ? 4 : 1;
+  u4 v4[KC ? 4 : 1];
+  u2 v2[KC ? 1 : 8];
+  const uint16_t *p;
+  int64_t ld, mn_lim;
+  int mn[NP], kk[NP];
+  bool full;  // all 128 mn of the tile exist (uniform)
+
+  __device__ __forceinline__ void init(int tid, const void *base_, int64_t mn0, int64_t mn_total, int64_t ld_) {
+    const uint16_t *base = static_cast<const uint16_t *>(base_);
+    ld = ld_;
+    mn_lim = mn_total - mn0;
+    full = mn_lim >= kBig;
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const int idx = e * 256 + tid;
+        mn[e] = idx / 8;
+        kk[e] = (idx % 8) * 8;
+      }
+      p = base + mn0 * ld;
+    } else {
+      mn[0] = (tid & 31) * 4;
+      kk[0] = (tid >> 5) * 8;
+      p = base + mn0;
+    }
+  }
+
+  __device__ __forceinline__ void fast(int64_t k0) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) v4[e] = *reinterpret_cast<const u4 *>(p + mn[e] * ld + k0 + kk[e]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v2[j] = *reinterpret_cast<const u2 *>(p + (k0 + kk[0] + j) * ld + mn[0]);
+    }
+  }
+
+  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
+    if (full && k0 + KS <= ke)
+      fast(k0);
+    else
+      slow(k0, ke);
+  }
+
+  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const int64_t k = k0 + kk[e];
+        const uint16_t *q = p + mn[e] * ld + k;
+        if (mn[e] < mn_lim && k + 8 <= ke) {
+          v4[e] = *reinterpret_cast<const u4 *>(q);
+        } else {
+          unsigned int w[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const unsigned int lo = (mn[e] < mn_lim && k + 2 * i < ke) ? q[2 * i] : 0u;
+            const unsigned int hi = (mn[e] < mn_lim && k + 2 * i + 1 < ke) ? q[2 * i + 1] : 0u;
+            w[i] = lo | (hi << 16);
+          }
+          v4[e] = u4{w[0], w[1], w[2], w[3]};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t k = k0 + kk[0] + j;
+        const uint16_t *q = p + k * ld + mn[0];
+        if (k < ke && mn[0] + 3 < mn_lim) {
+          v2[j] = *reinterpret_cast<const u2 *>(q);
+        } else {
+          unsigned int e4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e4[i] = (k < ke && mn[0] + i < mn_lim) ? q[i] : 0u;
+          v2[j] = u2{e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(__bf16 (*dst)[BigStage<1>::LD]) const {
+    if constexpr (KC) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) *reinterpret_cast<u4 *>(&dst[mn[e]][kk[e]]) = v4[e];
+    } else {
+      // v2[j] = {mn0 | mn1 << 16, mn2 | mn3 << 16} at k = j; vector for mn i
+      // packs k = 2d, 2d + 1 into word d
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        unsigned int w[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const unsigned int a = (i < 2) ? v2[2 * d].x : v2[2 * d].y;
+          const unsigned int b = (i < 2) ? v2[2 * d + 1].x : v2[2 * d + 1].y;
+          w[d] = (i & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+        }
+        *reinterpret_cast<u4 *>(&dst[mn[0] + i][kk[0]]) = u4{w[0], w[1], w[2], w[3]};
+      }
+    }
+  }
+};
+
+// loader for operand source type S (float, or uint16_t = bf16 bits)
+template <int PREC, bool KC, typename S>
+struct PickLoader {
+  using type = BigLoader<PREC, KC>;
+};
+template <bool KC>
+struct PickLoader<1, KC, uint16_t> {
+  using type = BigLoaderH<KC>;
+};
+
 template <int PREC>
 __device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
   constexpr int KS = Prec<PREC>::KS, KM = Prec<PREC>::KM, KV = Prec<PREC>::KV;
@@ -458,11 +621,12 @@ __device__ __forceinline__ void big_tile(int64_t bid, int64_t nblk, int64_t tile
   tn = in / gs;
 }
 
-template <int PREC, bool TA, bool TB>
+template <int PREC, bool TA, bool TB, typename S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
   __shared__ BigStage<PREC> st[2];
   constexpr int KS = Prec<PREC>::KS;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
   const int64_t tiles_m = (g.M + kBig - 1) / kBig, tiles_n = (g.N + kBig - 1) / kBig;
   int64_t tm, tn;
   big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
@@ -470,9 +634,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
-  BigLoader<PREC, !TA> la;
+  typename PickLoader<PREC, !TA, S>::type la;
   la.init(tid, g.A, m0, g.M, g.lda);
-  BigLoader<PREC, TB> lb;
+  typename PickLoader<PREC, TB, S>::type lb;
   lb.init(tid, g.B, n0, g.N, g.ldb);
 
   f32x16 acc[2][2];
@@ -535,6 +699,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 struct LinArgs {
   const float *x;     // [T, B, F]
   const float *w;     // [F, N]
+  const uint16_t *xh; // bf16 operands instead of x / w: [T, B, F] and
+  const uint16_t *wt; //   the transposed weight [N, F]
   const float *bias;  // [N] or null
   const float *m0;    // [B, N] or null (zeros)
   float *m_final;     // [B, N] or null
@@ -685,12 +851,277 @@ __device__ __forceinline__ float sg_deriv(float c) {
   }
 }
 
+// Fused current GEMM + LIF on the 128 x 128 engine.  The workgroup owns BT
+// batch rows x 128 neurons and walks time in chunks of CH = 128 / BT steps:
+// the chunk's 128 x 128 current tile (GEMM rows j*BT + bb) is computed over
+// the full input width, parked in LDS over the (then idle) staging buffers,
+// and consumed by the recurrence, wave w taking neurons 64*(w & 1) + lane
+// of batch rows (w >> 1)*Q .. +Q-1 (Q = BT / 2).  Same arithmetic per step
+// as linear_lif_fwd: m' = m*decay + (x_t W + bias).
+template <int PREC>
+struct BigRowLoader {  // A operand: 128 rows given by pointer (null = zero row), k-contiguous
+  static constexpr int KS = Prec<PREC>::KS;
+  static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));
+  static constexpr int NP = kBig * KS / KQ / 256;
+  float v[NP * KQ];
+  const float *row[NP];
+  int mn[NP], kk[NP];
+  bool full;  // every row pointer is set (uniform; set by the caller)
+
+  __device__ __forceinline__ void init(int tid) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int idx = e * 256 + tid;
+      mn[e] = idx / (KS / KQ);
+      kk[e] = (idx % (KS / KQ)) * KQ;
+    }
+  }
+  __device__ __forceinline__ void fast(int64_t k0) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+#pragma unroll
+      for (int h = 0; h < KQ; h += 4) {
+        const f4 t = *reinterpret_cast<const f4 *>(row[e] + k0 + kk[e] + h);
+        v[e * KQ + h] = t.x;
+        v[e * KQ + h + 1] = t.y;
+        v[e * KQ + h + 2] = t.z;
+        v[e * KQ + h + 3] = t.w;
+      }
+    }
+  }
+  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
+    if (full && k0 + KS <= ke)
+      fast(k0);
+    else
+      slow(k0, ke);
+  }
+  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int64_t k = k0 + kk[e];
+      if (row[e] != nullptr && k + KQ <= ke) {
+#pragma unroll
+        for (int h = 0; h < KQ; h += 4) {
+          const f4 t = *reinterpret_cast<const f4 *>(row[e] + k + h);
+          v[e * KQ + h] = t.x;
+          v[e * KQ + h + 1] = t.y;
+          v[e * KQ + h + 2] = t.z;
+          v[e * KQ + h + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < KQ; ++i) v[e * KQ + i] = (row[e] != nullptr && k + i < ke) ? row[e][k + i] : 0.0f;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) store_kvec<PREC>(&dst[mn[e]][kk[e]], &v[e * KQ]);
+  }
+};
+
+// A operand rows from bf16 inputs: one 16-byte load of 8 k per piece
+struct BigRowLoaderH {
+  static constexpr int KS = Prec<1>::KS;
+  static constexpr int NP = 4;
+  u4 v4[NP];
+  const uint16_t *row[NP];
+  int mn[NP], kk[NP];
+  bool full;  // every row pointer is set (uniform; set by the caller)
+
+  __device__ __forceinline__ void init(int tid) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int idx = e * 256 + tid;
+      mn[e] = idx / 8;
+      kk[e] = (idx % 8) * 8;
+    }
+  }
+  __device__ __forceinline__ void fast(int64_t k0) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) v4[e] = *reinterpret_cast<const u4 *>(row[e] + k0 + kk[e]);
+  }
+  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
+    if (full && k0 + KS <= ke)
+      fast(k0);
+    else
+      slow(k0, ke);
+  }
+  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int64_t k = k0 + kk[e];
+      if (row[e] != nullptr && k + 8 <= ke) {
+        v4[e] = *reinterpret_cast<const u4 *>(row[e] + k);
+      } else {
+        unsigned int w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const unsigned int lo = (row[e] != nullptr && k + 2 * i < ke) ? row[e][k + 2 * i] : 0u;
+          const unsigned int hi = (row[e] != nullptr && k + 2 * i + 1 < ke) ? row[e][k + 2 * i + 1] : 0u;
+          w[i] = lo | (hi << 16);
+        }
+        v4[e] = u4{w[0], w[1], w[2], w[3]};
+      }
+    }
+  }
+  __device__ __forceinline__ void store(__bf16 (*dst)[BigStage<1>::LD]) const {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) *reinterpret_cast<u4 *>(&dst[mn[e]][kk[e]]) = v4[e];
+  }
+};
+
+template <int PREC>
+union BigFusedSmem {
+  BigStage<PREC> st[2];
+  float cur[kBig][kBig + 1];
+};
+
+// H: bf16 operands in memory -- x rows bf16 [T, B, F] and the weight
+// transposed to wt [N, F] bf16 (k-contiguous); otherwise fp32 x and w [F, N].
+template <int PREC, int BT, bool H>
+__global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
+  constexpr int CH = kBig / BT;
+  constexpr int Q = BT / 2;
+  constexpr int KS = Prec<PREC>::KS;
+  __shared__ BigFusedSmem<PREC> sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBig, b0 = static_cast<int64_t>(blockIdx.y) * BT;
+  const int64_t BN = p.B * p.N;
+  const int h = w & 1, rg = w >> 1;
+  const int64_t n = n0 + 64 * h + lane;
+  const bool n_ok = n < p.N;
+  // batch row of slot q: brow + q (wave-uniform); its flat index brow_n + q*N + n
+  const int64_t brow = b0 + rg * Q, brow_n = brow * p.N;
+  float m[Q], cnt[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const bool act = brow + q < p.B && n_ok;
+    m[q] = (act && p.m0 != nullptr) ? p.m0[brow_n + q * p.N + n] : 0.0f;
+    cnt[q] = 0.0f;
+  }
+  const float bias_n = (p.bias != nullptr && n_ok) ? p.bias[n] : 0.0f;
+  int64_t next_ck = p.t_begin, ck_row = 0;
+
+  static_assert(!H || PREC == 1, "bf16 operands need the bf16 MFMA");
+  using LA = typename std::conditional<H, BigRowLoaderH, BigRowLoader<PREC>>::type;
+  using LB = typename std::conditional<H, BigLoaderH<true>, BigLoader<PREC, false>>::type;
+  LB lb;  // H: wt [N, F] rows are neurons; else w [F, N], neurons contiguous for a fixed k
+  lb.init(tid, H ? p.wt : static_cast<const void *>(p.w), n0, p.N, H ? p.F : p.N);
+  LA la;
+  la.init(tid);
+
+  for (int64_t t0 = p.t_begin; t0 < p.t_end; t0 += CH) {
+#pragma unroll
+    for (int e = 0; e < LA::NP; ++e) {
+      const int r = la.mn[e];
+      const int64_t t = t0 + r / BT, b = b0 + r % BT;
+      const bool ok = t < p.t_end && b < p.B;
+      if constexpr (H)
+        la.row[e] = ok ? p.xh + (t * p.B + b) * p.F : nullptr;
+      else
+        la.row[e] = ok ? p.x + (t * p.B + b) * p.F : nullptr;
+    }
+    la.full = t0 + CH <= p.t_end && b0 + BT <= p.B;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    la.load(0, p.F);
+    lb.load(0, p.F);
+    la.store(sm.st[0].a);
+    lb.store(sm.st[0].b);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t k0 = 0; k0 < p.F; k0 += KS) {
+      const bool more = k0 + KS < p.F;
+      if (more) {
+        la.load(k0 + KS, p.F);
+        lb.load(k0 + KS, p.F);
+      }
+      big_mfma<PREC>(sm.st[buf], wm, wn, lane, acc);
+      if (more) {
+        la.store(sm.st[buf ^ 1].a);
+        lb.store(sm.st[buf ^ 1].b);
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          sm.cur[64 * wm + 32 * i + acc_row(r, lane)][64 * wn + 32 * j + (lane & 31)] = acc[i][j][r];
+    __syncthreads();
+
+#pragma unroll 1
+    for (int j = 0; j < CH; ++j) {
+      const int64_t t = t0 + j;
+      if (t >= p.t_end) break;  // uniform
+      if (p.ckpt != nullptr && t == next_ck) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+          if (brow + q < p.B && n_ok) p.ckpt[ck_row * BN + brow_n + q * p.N + n] = m[q];
+        ++ck_row;
+        next_ck += p.ckpt_every;
+      }
+      bool s[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const bool act = brow + q < p.B && n_ok;
+        const int64_t flat = brow_n + q * p.N + n;
+        const float c_in = sm.cur[j * BT + rg * Q + q][64 * h + lane] + bias_n;
+        float mp = m[q] * p.decay;
+        mp = mp + c_in;
+        bool sp;
+        if (p.rule == MYELIN_RULE_THRESHOLD) {
+          sp = mp >= p.thr;
+        } else {
+          const float c = p.slope * (mp - p.thr);
+          sp = c >= 0.0f;
+        }
+        s[q] = act && sp;
+        if (act) {
+          if (p.pre != nullptr) p.pre[(t - p.t_begin) * BN + flat] = mp;
+          if (p.spikes != nullptr) __builtin_nontemporal_store(sp ? 1.0f : 0.0f, p.spikes + t * BN + flat);
+          m[q] = sp ? p.reset : mp;
+          cnt[q] = cnt[q] + (sp ? 1.0f : 0.0f);
+        }
+      }
+      if (p.packed != nullptr) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          const uint64_t bits = __ballot(s[q]);
+          const int64_t b = brow + q;
+          const int64_t word = (n0 + 64 * h) / 32 + (lane >> 5);
+          if ((lane & 31) == 0 && b < p.B && word < p.W)
+            p.packed[(t * p.B + b) * p.W + word] = static_cast<int32_t>(lane ? (bits >> 32) : (bits & 0xffffffffu));
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if (!(brow + q < p.B && n_ok)) continue;
+    const int64_t flat = brow_n + q * p.N + n;
+    if (p.m_final != nullptr) p.m_final[flat] = m[q];
+    if (p.rates != nullptr) p.rates[flat] = cnt[q] / p.rate_denominator;
+  }
+}
+
 struct PreBwdArgs {
   const float *pre;     // [C, BN]
   const float *gs;      // [C, BN] or null
   const float *grate;   // [BN] or null
   float *gm;            // [BN] in/out
-  float *G;             // [C, BN]
+  void *G;              // [C, BN] float, or bf16 bits when the GEMMs read bf16
   float *gbias_acc;     // [BN] or null (accumulated)
   int64_t C, BN;
   float decay, thr, reset, slope, rate_denominator;
@@ -705,7 +1136,7 @@ struct PreBwdArgs {
 // no load is predicated.
 constexpr int kPipe = 16;
 
-template <int SID, bool GS>
+template <int SID, bool GS, bool GH>
 __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, float pre, float gsv,
                                              float gstep, float &gm, float &gb) {
   const float c = p.slope * (pre - p.thr);
@@ -715,13 +1146,17 @@ __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int
   float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
   if constexpr (GS) gp = gp + gsv * d;
   if (p.grate != nullptr) gp = gp + gstep * d;
-  p.G[j * p.BN + i] = gp;
+  if constexpr (GH)
+    static_cast<uint16_t *>(p.G)[j * p.BN + i] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(gp));
+  else
+    static_cast<float *>(p.G)[j * p.BN + i] = gp;
   gb = gb + gp;
   gm = gp * p.decay;
 }
 
-// reverse time: relative index r = C - 1 - j
-template <int SID, bool GS>
+// reverse time: relative index r = C - 1 - j.  GH: G is written as bf16
+// (rounded as the bf16 GEMMs would round it).
+template <int SID, bool GS, bool GH>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= p.BN) return;
@@ -752,7 +1187,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     }
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      if (u < f) pre_bwd_step<SID, GS>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      if (u < f) pre_bwd_step<SID, GS, GH>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
@@ -770,7 +1205,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      pre_bwd_step<SID, GS>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      pre_bwd_step<SID, GS, GH>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
@@ -904,16 +1339,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool al16(const void *q) { return q == nullptr || myelin::aligned(q, 16); }
 
-template <int PREC, bool VEC>
+template <int PREC, bool VA, bool VB>
 void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
   if (!ta && !tb)
-    gemm_kernel<PREC, false, false, VEC><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, false, VA, VB><<<grid, dim3(256), 0, s>>>(g);
   else if (!ta && tb)
-    gemm_kernel<PREC, false, true, VEC><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, true, VA, VB><<<grid, dim3(256), 0, s>>>(g);
   else if (ta && !tb)
-    gemm_kernel<PREC, true, false, VEC><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, true, false, VA, VB><<<grid, dim3(256), 0, s>>>(g);
   else
-    gemm_kernel<PREC, true, true, VEC><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, true, true, VA, VB><<<grid, dim3(256), 0, s>>>(g);
 }
 
 // K splits for an output of `tiles` workgroups: split when the output alone
@@ -931,21 +1366,33 @@ int64_t plan_splits(int64_t tiles, int64_t K, bool big) {
   return splits < 1 ? 1 : splits;
 }
 
-// the 128 x 128 kernel takes outputs of at least one full tile per side
-// whose operands allow 16-byte loads
+// fp32 operands: the 128 x 128 kernel takes outputs of at least one full
+// tile per side whose operands allow 16-byte loads
 bool use_big(const GemmArgs &g) {
   return g.M >= kBig && g.N >= kBig && al16(g.A) && al16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0;
 }
 
+// bf16 operands (128 x 128 kernel only): k-contiguous rows 16-byte aligned,
+// mn-contiguous rows 8-byte aligned
+bool bf16_aligned(const void *q, int64_t ld, bool kcontig) {
+  return kcontig ? (myelin::aligned(q, 16) && ld % 8 == 0) : (myelin::aligned(q, 8) && ld % 4 == 0);
+}
+
 template <int PREC, bool TA, bool TB>
-void launch_big(const GemmArgs &g, dim3 grid, hipStream_t s) {
-  gemm_big<PREC, TA, TB><<<grid, dim3(256), 0, s>>>(g);
+void launch_big(const GemmArgs &g, bool half, dim3 grid, hipStream_t s) {
+  if constexpr (PREC == 1) {
+    if (half) {
+      gemm_big<1, TA, TB, uint16_t><<<grid, dim3(256), 0, s>>>(g);
+      return;
+    }
+  }
+  gemm_big<PREC, TA, TB, float><<<grid, dim3(256), 0, s>>>(g);
 }
 
 template <int PREC>
-int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
+int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s) {
   constexpr int KS = Prec<PREC>::KS;
-  const bool big = use_big(g);
+  const bool big = half || use_big(g);
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
   if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
@@ -958,20 +1405,25 @@ int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
   if (big) {
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
     if (!ta && !tb)
-      launch_big<PREC, false, false>(g, grid, s);
+      launch_big<PREC, false, false>(g, half, grid, s);
     else if (!ta && tb)
-      launch_big<PREC, false, true>(g, grid, s);
+      launch_big<PREC, false, true>(g, half, grid, s);
     else if (ta && !tb)
-      launch_big<PREC, true, false>(g, grid, s);
+      launch_big<PREC, true, false>(g, half, grid, s);
     else
-      launch_big<PREC, true, true>(g, grid, s);
+      launch_big<PREC, true, true>(g, half, grid, s);
   } else {
     const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
-    const bool vec = al16(g.A) && al16(g.B) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
-    if (vec)
-      launch_gemm_v<PREC, true>(g, ta, tb, grid, s);
+    // 16-byte loads per operand where its base and leading dimension allow
+    const bool va = al16(g.A) && g.lda % 4 == 0, vb = al16(g.B) && g.ldb % 4 == 0;
+    if (va && vb)
+      launch_gemm_v<PREC, true, true>(g, ta, tb, grid, s);
+    else if (va)
+      launch_gemm_v<PREC, true, false>(g, ta, tb, grid, s);
+    else if (vb)
+      launch_gemm_v<PREC, false, true>(g, ta, tb, grid, s);
     else
-      launch_gemm_v<PREC, false>(g, ta, tb, grid, s);
+      launch_gemm_v<PREC, false, false>(g, ta, tb, grid, s);
   }
   if (int rc = myelin::launched("gemm")) return rc;
   if (splits > 1) {
@@ -982,11 +1434,15 @@ int launch_gemm(GemmArgs g, int ta, int tb, int64_t ws_elems, hipStream_t s) {
 }
 
 template <int SID>
-void launch_pre_bwd(const PreBwdArgs &a, bool gs, dim3 grid, hipStream_t s) {
-  if (gs)
-    linear_pre_bwd<SID, true><<<grid, dim3(256), 0, s>>>(a);
+void launch_pre_bwd(const PreBwdArgs &a, bool gs, bool gh, dim3 grid, hipStream_t s) {
+  if (gs && gh)
+    linear_pre_bwd<SID, true, true><<<grid, dim3(256), 0, s>>>(a);
+  else if (gs)
+    linear_pre_bwd<SID, true, false><<<grid, dim3(256), 0, s>>>(a);
+  else if (gh)
+    linear_pre_bwd<SID, false, true><<<grid, dim3(256), 0, s>>>(a);
   else
-    linear_pre_bwd<SID, false><<<grid, dim3(256), 0, s>>>(a);
+    linear_pre_bwd<SID, false, false><<<grid, dim3(256), 0, s>>>(a);
 }
 
 template <bool PRE, bool SPK>
@@ -1023,16 +1479,26 @@ extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, 
   return most > 1 ? most * M * N : 0;
 }
 
-extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
-                               int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b,
-                               int accumulate, int precision, float *workspace, int64_t workspace_elems,
-                               myelin_stream_t stream) {
+extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype, const float *bias, float *C,
+                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a,
+                           int trans_b, int accumulate, int precision, float *workspace, int64_t workspace_elems,
+                           myelin_stream_t stream) {
   if (M < 0 || N < 0 || K < 0) return myelin::invalid("gemm: negative size");
   if (M == 0 || N == 0) return MYELIN_OK;
   if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm: null pointer");
   if (ldc < N) return myelin::invalid("gemm: ldc < N");
   if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N)) return myelin::invalid("gemm: bad leading dim");
   if (workspace_elems < 0) return myelin::invalid("gemm: negative workspace size");
+  if (precision != MYELIN_PREC_BF16 && precision != MYELIN_PREC_F32)
+    return myelin::invalid("gemm: unknown precision %d", precision);
+  if ((a_dtype != MYELIN_DT_F32 && a_dtype != MYELIN_DT_BF16) || b_dtype != a_dtype)
+    return myelin::invalid("gemm: operands must both be float32 or both bfloat16");
+  const bool half = a_dtype == MYELIN_DT_BF16;
+  if (half) {
+    if (precision != MYELIN_PREC_BF16) return myelin::invalid("gemm: bfloat16 operands need bf16 precision");
+    if (!bf16_aligned(A, lda, !trans_a) || !bf16_aligned(B, ldb, trans_b != 0))
+      return myelin::invalid("gemm: bfloat16 operand rows must be 16-byte (k-contiguous) or 8-byte aligned");
+  }
   GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;
@@ -1040,25 +1506,27 @@ extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias
     return myelin::launched("gemm (K = 0)");
   }
   hipStream_t s = myelin::as_hip(stream);
-  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, workspace_elems, s);
-  if (precision == MYELIN_PREC_F32) return launch_gemm<0>(g, trans_a, trans_b, workspace_elems, s);
-  return myelin::invalid("gemm: unknown precision %d", precision);
+  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s);
+  return launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s);
 }
 
-extern "C" int myelin_linear_lif_fwd(const float *x, const float *w, const float *bias, const float *m0,
-                                     float *m_final, float *spikes, float *pre, int32_t *packed, float *rates,
-                                     float *ckpt, int64_t T, int64_t B, int64_t F, int64_t N, int64_t t_begin,
-                                     int64_t t_end, int64_t ckpt_every, float decay, float threshold, float reset,
-                                     float slope, int rule, int precision, myelin_stream_t stream) {
+extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
+                               int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b,
+                               int accumulate, int precision, float *workspace, int64_t workspace_elems,
+                               myelin_stream_t stream) {
+  return myelin_gemm(A, MYELIN_DT_F32, B, MYELIN_DT_F32, bias, C, M, N, K, lda, ldb, ldc, trans_a, trans_b,
+                     accumulate, precision, workspace, workspace_elems, stream);
+}
+
+namespace {
+int fill_lin(LinArgs &a, const float *bias, const float *m0, float *m_final, float *spikes, float *pre,
+             int32_t *packed, float *rates, float *ckpt, int64_t T, int64_t B, int64_t F, int64_t N, int64_t t_begin,
+             int64_t t_end, int64_t ckpt_every, float decay, float threshold, float reset, float slope, int rule) {
   if (T < 1 || B < 1 || F < 1 || N < 1) return myelin::invalid("linear_lif_fwd: T, B, F, N must be positive");
   if (t_begin < 0 || t_end > T || t_begin >= t_end) return myelin::invalid("linear_lif_fwd: bad time range");
-  if (x == nullptr || w == nullptr) return myelin::invalid("linear_lif_fwd: x and w are required");
   if (ckpt != nullptr && ckpt_every < 1) return myelin::invalid("linear_lif_fwd: ckpt_every must be positive");
   if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
     return myelin::invalid("linear_lif_fwd: unknown rule %d", rule);
-  LinArgs a{};
-  a.x = x;
-  a.w = w;
   a.bias = bias;
   a.m0 = m0;
   a.m_final = m_final;
@@ -1081,15 +1549,75 @@ extern "C" int myelin_linear_lif_fwd(const float *x, const float *w, const float
   a.slope = slope;
   a.rate_denominator = static_cast<float>(T);
   a.rule = rule;
+  return MYELIN_OK;
+}
+}  // namespace
+
+extern "C" int myelin_linear_lif_fwd_bf16(const uint16_t *x, const uint16_t *wt, const float *bias, const float *m0,
+                                          float *m_final, float *spikes, float *pre, int32_t *packed, float *rates,
+                                          float *ckpt, int64_t T, int64_t B, int64_t F, int64_t N, int64_t t_begin,
+                                          int64_t t_end, int64_t ckpt_every, float decay, float threshold,
+                                          float reset, float slope, int rule, myelin_stream_t stream) {
+  if (x == nullptr || wt == nullptr) return myelin::invalid("linear_lif_fwd_bf16: x and wt are required");
+  LinArgs a{};
+  if (int rc = fill_lin(a, bias, m0, m_final, spikes, pre, packed, rates, ckpt, T, B, F, N, t_begin, t_end,
+                        ckpt_every, decay, threshold, reset, slope, rule))
+    return rc;
+  if (!myelin::aligned(x, 16) || !myelin::aligned(wt, 16) || F % 8 != 0)
+    return myelin::invalid("linear_lif_fwd_bf16: x and wt need 16-byte aligned rows (F %% 8 == 0)");
+  a.xh = x;
+  a.wt = wt;
+  const int bt = (cdiv(N, kBig) * cdiv(B, 16) >= 512) ? 16 : 8;
+  const dim3 grid(cdiv(N, kBig), cdiv(B, bt));
+  if (grid.y > 65535) return myelin::invalid("linear_lif_fwd_bf16: B too large");
+  hipStream_t s = myelin::as_hip(stream);
+  if (bt == 16)
+    linear_lif_fwd_big<1, 16, true><<<grid, dim3(256), 0, s>>>(a);
+  else
+    linear_lif_fwd_big<1, 8, true><<<grid, dim3(256), 0, s>>>(a);
+  return myelin::launched("linear_lif_fwd_bf16");
+}
+
+extern "C" int myelin_linear_lif_fwd(const float *x, const float *w, const float *bias, const float *m0,
+                                     float *m_final, float *spikes, float *pre, int32_t *packed, float *rates,
+                                     float *ckpt, int64_t T, int64_t B, int64_t F, int64_t N, int64_t t_begin,
+                                     int64_t t_end, int64_t ckpt_every, float decay, float threshold, float reset,
+                                     float slope, int rule, int precision, myelin_stream_t stream) {
+  if (x == nullptr || w == nullptr) return myelin::invalid("linear_lif_fwd: x and w are required");
+  LinArgs a{};
+  if (int rc = fill_lin(a, bias, m0, m_final, spikes, pre, packed, rates, ckpt, T, B, F, N, t_begin, t_end,
+                        ckpt_every, decay, threshold, reset, slope, rule))
+    return rc;
+  a.x = x;
+  a.w = w;
   if (precision != MYELIN_PREC_BF16 && precision != MYELIN_PREC_F32)
     return myelin::invalid("linear_lif_fwd: unknown precision %d", precision);
-  // 8 batch rows x 8 steps per tile, or 4 x 16 when that leaves the chip
-  // under ~2 workgroups per CU
+  const bool vec = al16(x) && al16(w) && (F % 4 == 0) && (N % 4 == 0);
+  hipStream_t s = myelin::as_hip(stream);
+  if (vec && N >= kBig) {
+    // 128 neurons x 16 batch rows x 8 steps per tile, or 8 x 16 when that
+    // leaves the chip under ~2 workgroups per CU
+    const int bt = (cdiv(N, kBig) * cdiv(B, 16) >= 512) ? 16 : 8;
+    const dim3 grid(cdiv(N, kBig), cdiv(B, bt));
+    if (grid.y > 65535) return myelin::invalid("linear_lif_fwd: B too large");
+    if (precision == MYELIN_PREC_BF16) {
+      if (bt == 16)
+        linear_lif_fwd_big<1, 16, false><<<grid, dim3(256), 0, s>>>(a);
+      else
+        linear_lif_fwd_big<1, 8, false><<<grid, dim3(256), 0, s>>>(a);
+    } else {
+      if (bt == 16)
+        linear_lif_fwd_big<0, 16, false><<<grid, dim3(256), 0, s>>>(a);
+      else
+        linear_lif_fwd_big<0, 8, false><<<grid, dim3(256), 0, s>>>(a);
+    }
+    return myelin::launched("linear_lif_fwd");
+  }
+  // 8 batch rows x 8 steps per 64 x 64 tile, or 4 x 16 when that leaves the
+  // chip under ~2 workgroups per CU
   const int bt = (cdiv(N, kTile) * cdiv(B, 8) >= 512) ? 8 : 4;
   const dim3 grid(cdiv(N, kTile), cdiv(B, bt));
   if (grid.y > 65535) return myelin::invalid("linear_lif_fwd: B too large");
-  const bool vec = al16(x) && al16(w) && (F % 4 == 0) && (N % 4 == 0);
-  hipStream_t s = myelin::as_hip(stream);
 #define MYELIN_LAUNCH_FUSED(P, BT)                                                     \
   do {                                                                                 \
     if (vec)                                                                           \
@@ -1113,23 +1641,25 @@ extern "C" int myelin_linear_lif_fwd(const float *x, const float *w, const float
 }
 
 extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes, const float *grad_rates,
-                                     float *grad_m, float *G, float *gbias_acc, int64_t C, int64_t BN,
+                                     float *grad_m, void *G, int g_dtype, float *gbias_acc, int64_t C, int64_t BN,
                                      int64_t T_total, float decay, float threshold, float reset, float slope,
                                      int surrogate_id, int rule, myelin_stream_t stream) {
   if (C < 1 || BN < 1) return myelin::invalid("linear_pre_bwd: C and BN must be positive");
   if (pre == nullptr || grad_m == nullptr || G == nullptr) return myelin::invalid("linear_pre_bwd: null pointer");
+  if (g_dtype != MYELIN_DT_F32 && g_dtype != MYELIN_DT_BF16)
+    return myelin::invalid("linear_pre_bwd: G must be float32 or bfloat16");
   PreBwdArgs a{pre, grad_spikes, grad_rates, grad_m, G, gbias_acc, C, BN, decay, threshold, reset, slope,
                static_cast<float>(T_total), rule};
   const dim3 grid(cdiv(BN, 256));
   hipStream_t s = myelin::as_hip(stream);
-  const bool gs = grad_spikes != nullptr;
+  const bool gs = grad_spikes != nullptr, gh = g_dtype == MYELIN_DT_BF16;
   switch (surrogate_id) {
-    case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, grid, s); break;
-    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, grid, s); break;
-    case MYELIN_SG_ATAN: launch_pre_bwd<MYELIN_SG_ATAN>(a, gs, grid, s); break;
-    case MYELIN_SG_TRIANGULAR: launch_pre_bwd<MYELIN_SG_TRIANGULAR>(a, gs, grid, s); break;
-    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd<MYELIN_SG_SUPERSPIKE>(a, gs, grid, s); break;
-    case MYELIN_SG_MULTI_GAUSSIAN: launch_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN>(a, gs, grid, s); break;
+    case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_ATAN: launch_pre_bwd<MYELIN_SG_ATAN>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_TRIANGULAR: launch_pre_bwd<MYELIN_SG_TRIANGULAR>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd<MYELIN_SG_SUPERSPIKE>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_MULTI_GAUSSIAN: launch_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN>(a, gs, gh, grid, s); break;
     default: return myelin::invalid("linear_pre_bwd: unknown surrogate id %d", surrogate_id);
   }
   return myelin::launched("linear_pre_bwd");
@@ -1185,4 +1715,68 @@ extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, f
   const int64_t lanes = B * a.W * 32;
   launch_currents(a, dim3(cdiv(lanes, 256)), myelin::as_hip(stream));
   return myelin::launched("lif_currents_fwd");
+}
+
+// ---------------------------------------------------------------------------
+// fp32 -> bf16 operand copies for the bf16 GEMMs (round to nearest even,
+// exactly as the GEMM loaders round fp32 operands).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ uint16_t to_bf16(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+
+// 8 elements per thread, one 32-byte read and one 16-byte write
+__global__ __launch_bounds__(256) void cast_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                 int64_t n) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    const f4 a = *reinterpret_cast<const f4 *>(src + i);
+    const f4 b = *reinterpret_cast<const f4 *>(src + i + 4);
+    const u4 o{to_bf16(a.x) | (unsigned)to_bf16(a.y) << 16, to_bf16(a.z) | (unsigned)to_bf16(a.w) << 16,
+               to_bf16(b.x) | (unsigned)to_bf16(b.y) << 16, to_bf16(b.z) | (unsigned)to_bf16(b.w) << 16};
+    *reinterpret_cast<u4 *>(dst + i) = o;
+  } else {
+    for (int64_t j = i; j < n; ++j) dst[j] = to_bf16(src[j]);
+  }
+}
+
+// dst[c, r] = bf16(src[r, c]) through a 64 x 64 LDS tile
+__global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                      int64_t rows, int64_t cols) {
+  __shared__ float tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
+    tile[ty + 4 * k][tx] = (r < rows && c < cols) ? src[r * cols + c] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < cols && r < rows) dst[c * rows + r] = to_bf16(tile[tx][ty + 4 * k]);
+  }
+}
+
+}  // namespace
+
+extern "C" int myelin_cast_bf16(const float *src, uint16_t *dst, int64_t n, myelin_stream_t stream) {
+  if (n < 0) return myelin::invalid("cast_bf16: negative size");
+  if (n == 0) return MYELIN_OK;
+  if (src == nullptr || dst == nullptr) return myelin::invalid("cast_bf16: null pointer");
+  if (!myelin::aligned(src, 16) || !myelin::aligned(dst, 16))
+    return myelin::invalid("cast_bf16: src and dst must be 16-byte aligned");
+  cast_bf16<<<dim3(cdiv(cdiv(n, 8), 256)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, n);
+  return myelin::launched("cast_bf16");
+}
+
+extern "C" int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows, int64_t cols,
+                                     myelin_stream_t stream) {
+  if (rows < 0 || cols < 0) return myelin::invalid("transpose_bf16: negative size");
+  if (rows == 0 || cols == 0) return MYELIN_OK;
+  if (src == nullptr || dst == nullptr) return myelin::invalid("transpose_bf16: null pointer");
+  if (cdiv(rows, 64) > 65535) return myelin::invalid("transpose_bf16: too many rows");
+  transpose_bf16<<<dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, rows, cols);
+  return myelin::launched("transpose_bf16");
 }

@@ -33,10 +33,35 @@ from myelin_amd import _lib
 
 
 def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None):
+    """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16."""
+
     n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec)
     ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
-    _lib.call("myelin_gemm_f32", _lib.ptr(A), _lib.ptr(B), _lib.ptr(bias), _lib.ptr(C), M, N, K, lda, ldb, ldc,
-              int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws), n_ws, stream)
+    _lib.call("myelin_gemm", _lib.ptr(A), _lib.DT[A.dtype], _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
+              _lib.ptr(C), M, N, K, lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws),
+              n_ws, stream)
+
+
+def _half(prec: int, F: int, N: int) -> bool:
+    """bf16 synapse with operand rows the bf16 kernels can load 16 bytes at a
+    time: its GEMMs then read bf16 copies of x, W and dL/dI (half the
+    bytes, bit-identical results)."""
+
+    return prec == _lib.PREC["bf16"] and F % 8 == 0 and N % 8 == 0
+
+
+def _cast_bf16(t, stream):
+    out = torch.empty(t.shape, dtype=torch.bfloat16, device=t.device)
+    _lib.call("myelin_cast_bf16", _lib.ptr(t), _lib.ptr(out), t.numel(), stream)
+    return out
+
+
+def _transpose_bf16(w, stream):
+    """[F, N] fp32 -> [N, F] bf16."""
+
+    out = torch.empty((w.shape[1], w.shape[0]), dtype=torch.bfloat16, device=w.device)
+    _lib.call("myelin_transpose_bf16", _lib.ptr(w), _lib.ptr(out), w.shape[0], w.shape[1], stream)
+    return out
 
 
 class HipLinearFunction(torch.autograd.Function):
@@ -106,27 +131,29 @@ def _fused_grid(B: int, N: int) -> int:
 
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
-             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1):
+             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
-    Fused (one launch, currents stay in LDS) when N >= 64 and the fused grid
-    has >= 1024 workgroups.  Otherwise each workgroup would walk many chunks
-    serially, so the steps are processed in chunks of up to 2**25 currents:
-    an MFMA GEMM (split-K when narrow) writes ``x_t @ W + b`` for the chunk,
-    then the recurrence kernel consumes it, carrying the membrane and the
-    spike counts across chunks.  ``pre`` is indexed from t0; checkpoint rows
-    from t0.
+    ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
+    the bf16 transposed weight ``[N, F]``.  Fused (one launch, currents stay
+    in LDS) when N >= 64 and the fused grid has >= 1024 workgroups.
+    Otherwise each workgroup would walk many chunks serially, so the steps
+    are processed in chunks of up to 2**25 currents: an MFMA GEMM (split-K
+    when narrow) writes ``x_t @ W + b`` for the chunk, then the recurrence
+    kernel consumes it, carrying the membrane and the spike counts across
+    chunks.  ``pre`` is indexed from t0; checkpoint rows from t0.
     """
 
     T, B, F = x.shape
-    N = w.shape[1]
+    half = x.dtype == torch.bfloat16
+    N = wt.shape[0] if half else w.shape[1]
     if N >= 64 and _fused_grid(B, N) >= 1024:
-        _lib.call(
-            "myelin_linear_lif_fwd",
-            _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre),
-            _lib.ptr(packed), _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold,
-            reset, slope, rule, prec, stream,
-        )
+        outs = (_lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
+                _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule)
+        if half:
+            _lib.call("myelin_linear_lif_fwd_bf16", _lib.ptr(x), _lib.ptr(wt), *outs, stream)
+        else:
+            _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *outs, prec, stream)
         return
     dev = x.device
     step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
@@ -136,7 +163,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     for c0 in range(t0, t1, step):
         c1 = min(c0 + step, t1)
         rows = (c1 - c0) * B
-        _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
+        if half:
+            _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, stream, bias=b)
+        else:
+            _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
         last = c1 == t1
         _lib.call(
             "myelin_lif_currents_fwd",
@@ -159,6 +189,8 @@ class HipLinearLIFFunction(torch.autograd.Function):
         dev = x.device
         stream = _lib.stream(dev)
         need = any(ctx.needs_input_grad[:3])
+        half = _half(prec, F, N)
+        xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
         pre = ckpt = None
@@ -167,13 +199,14 @@ class HipLinearLIFFunction(torch.autograd.Function):
                 pre = torch.empty((T, B, N), dtype=x.dtype, device=dev)
             else:
                 ckpt = torch.empty((math.ceil(T / checkpoint), B, N), dtype=x.dtype, device=dev)
-        _lif_fwd(x, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
+        _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1)
+                 ckpt_every=checkpoint or 1, wt=wt)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:
-            ctx.save_for_backward(x, w, b, pre, ckpt)
+            # the bf16 synapse keeps the bf16 copies of x and W^T (what its GEMMs read)
+            ctx.save_for_backward(xs, w, b, pre, ckpt, wt)
         return m_final, out
 
     @staticmethod
@@ -182,23 +215,25 @@ class HipLinearLIFFunction(torch.autograd.Function):
         if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
             return none
         decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
-        x, w, b, pre, ckpt = ctx.saved_tensors
-        T, B, F = x.shape
+        xs, w, b, pre, ckpt, wt = ctx.saved_tensors
+        T, B, F = xs.shape
         N = w.shape[1]
         BN = B * N
-        dev = x.device
+        dev = xs.device
+        half = xs.dtype == torch.bfloat16
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
         with torch.cuda.device(dev):
             stream = _lib.stream(dev)
+            wg = _cast_bf16(w, stream) if (half and need_x) else w
             gm = g_m.float().contiguous().clone() if g_m is not None else torch.zeros((B, N), device=dev)
             g_out = None if g_out is None else g_out.float().contiguous()
             g_spikes = None if rate else g_out
             g_rates = g_out if rate else None
-            gx = torch.empty_like(x) if need_x else None
+            gx = torch.empty((T, B, F), device=dev) if need_x else None
             gw = torch.zeros_like(w) if need_w else None
             gb_acc = torch.zeros((B, N), device=dev) if (need_b and has_b) else None
             chunk = T if checkpoint is None else checkpoint
-            G = torch.empty((min(chunk, T), B, N), device=dev)
+            G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
             scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
             n_chunks = math.ceil(T / chunk)
             for k in range(n_chunks - 1, -1, -1):
@@ -208,22 +243,22 @@ class HipLinearLIFFunction(torch.autograd.Function):
                 if checkpoint is None:
                     pre_k = pre
                 else:
-                    _lif_fwd(x, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
-                             pre=scratch)
+                    _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
+                             pre=scratch, wt=wt)
                     pre_k = scratch
                 _lib.call(
                     "myelin_linear_pre_bwd",
                     _lib.ptr(pre_k), _lib.ptr(g_spikes[t0:t1]) if g_spikes is not None else None,
-                    _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.ptr(gb_acc),
+                    _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT[G.dtype], _lib.ptr(gb_acc),
                     C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
                 )
                 rows = C * B
                 if gx is not None:
                     # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
-                    _gemm(G, w, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
+                    _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
                 if gw is not None:
                     # dW += X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                    _gemm(x[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
+                    _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
             gb = None
             if gb_acc is not None:
                 gb = torch.empty((N,), device=dev)

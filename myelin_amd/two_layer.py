@@ -36,7 +36,7 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import _gemm, _lif_fwd
+from myelin_amd.linear import _cast_bf16, _gemm, _half, _lif_fwd, _transpose_bf16
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
@@ -78,19 +78,22 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         hs = torch.empty((L0, B, H), device=dev)
         cur = torch.empty((L0, B, O), device=dev)
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
+        # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
+        half = _half(prec, F, H)
+        xs, wt = (_cast_bf16(x, stream), _transpose_bf16(wh, stream)) if half else (x, None)
         for k in range(K):
             t0 = k * C
             t1 = min(t0 + C, T)
             L = t1 - t0
-            _lif_fwd(x[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
+            _lif_fwd(xs[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
                      m_final=m_h, spikes=hs[:L], packed=None if words is None else words[t0:t1],
-                     ckpt=None if ck_h is None else ck_h[k], ckpt_every=L)
+                     ckpt=None if ck_h is None else ck_h[k], ckpt_every=L, wt=wt)
             _readout_chunk(cur[:L], hs[:L], wo, bo, m_o, m_o, None, counts, rates if t1 == T else None, ck_o, T,
                            t0, t1, C, decay, threshold, reset, slope, prec, stream)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
         if need:
-            ctx.save_for_backward(x, wh, bh, wo, bo, ck_h, ck_o, words)
+            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt)
         return rates
 
     @staticmethod
@@ -99,13 +102,14 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         if g_rates is None or not any(ctx.needs_input_grad[:5]):
             return none
         decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
-        x, wh, bh, wo, bo, ck_h, ck_o, words = ctx.saved_tensors
+        xs, wh, bh, wo, bo, ck_h, ck_o, words, wt = ctx.saved_tensors
+        half = xs.dtype == torch.bfloat16
         need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
         need_hidden = need_x or need_wh or (need_bh and has_bh)
-        T, B, F = x.shape
+        T, B, F = xs.shape
         H = wh.shape[1]
         O = wo.shape[1]
-        dev = x.device
+        dev = xs.device
         K = math.ceil(T / C)
         L0 = min(C, T)
         with torch.cuda.device(dev):
@@ -113,7 +117,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             g_rates = g_rates.float().contiguous()
             gm_o = torch.zeros((B, O), device=dev)
             gm_h = torch.zeros((B, H), device=dev) if need_hidden else None
-            gx = torch.empty_like(x) if need_x else None
+            gx = torch.empty((T, B, F), device=dev) if need_x else None
+            whg = _cast_bf16(wh, stream) if (half and need_x) else wh
             gwh = torch.zeros_like(wh) if need_wh else None
             gwo = torch.zeros_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
@@ -124,7 +129,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             pre_o = torch.empty((L0, B, O), device=dev)
             G_o = torch.empty((L0, B, O), device=dev)
             ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
-            G_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
+            G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
+                   if need_hidden else None)
             for k in range(K - 1, -1, -1):
                 t0 = k * C
                 t1 = min(t0 + C, T)
@@ -134,16 +140,17 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     _lib.call("myelin_unpack", _lib.ptr(words[t0:t1]), _lib.ptr(hs), _lib.DT[torch.float32],
                               rows, H, stream)
                     if need_hidden:
-                        _lif_fwd(x[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
-                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L])
+                        _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
+                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L], wt=wt)
                 else:
-                    _lif_fwd(x[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
-                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L])
+                    _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
+                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt)
                 _readout_chunk(cur[:L], hs[:L], wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
                                decay, threshold, reset, slope, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.ptr(gbo_acc),
+                    _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
+                    _lib.ptr(gbo_acc),
                     L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
                 if gwo is not None:
@@ -155,13 +162,14 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h), _lib.ptr(gbh_acc),
+                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h), _lib.DT[G_h.dtype],
+                    _lib.ptr(gbh_acc),
                     L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
                 if gx is not None:
-                    _gemm(G_h, wh, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
+                    _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
                 if gwh is not None:
-                    _gemm(x[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, True, prec, stream)
+                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, True, prec, stream)
             gbh = gbo = None
             if gbh_acc is not None:
                 gbh = torch.empty((H,), device=dev)

@@ -272,3 +272,117 @@ def test_streamed_synapse_bf16_config_subset():
     assert_norm_close(to_np(w2d.grad), w2r.grad, 2e-2, "grad_w2")
     assert_norm_close(to_np(b1d.grad), b1r.grad, 2e-2, "grad_b1")
     assert_norm_close(to_np(b2d.grad), b2r.grad, 2e-2, "grad_b2")
+
+
+@pytest.mark.parametrize("T,B,F,N", [(13, 20, 200, 300), (9, 48, 96, 256), (5, 7, 64, 128), (20, 3, 44, 64)])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_fused_forward_equals_gemm_then_recurrence(T, B, F, N, prec):
+    """myelin_linear_lif_fwd (128 x 128 fused tiles when N >= 128, 64 x 64
+    otherwise) against the unfused route (MFMA GEMM with the bias epilogue,
+    then myelin_lif_currents_fwd): same k order, same per-step arithmetic, so
+    every output is bit-identical.  K stays short enough that the GEMM does
+    not split."""
+
+    _print_case(test="fused_vs_unfused", T=T, B=B, F=F, N=N, prec=prec)
+    g = seeded(T * 1000 + N)
+    x = (torch.rand(T, B, F, generator=g) < 0.4).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.4) * 0.5).to(DEV)
+    bias = (torch.rand(N, generator=g) * 0.1).to(DEV)
+    m0 = (torch.rand(B, N, generator=g) * 0.5).to(DEV)
+    pr = _lib.PREC[prec]
+    stream = _lib.stream(torch.device(DEV))
+    W = (N + 31) // 32
+    ck_every = 3
+    nck = -(-T // ck_every)
+
+    def outputs():
+        return dict(m=torch.empty(B, N, device=DEV), s=torch.empty(T, B, N, device=DEV),
+                    pre=torch.empty(T, B, N, device=DEV), pk=torch.empty(T, B, W, dtype=torch.int32, device=DEV),
+                    r=torch.empty(B, N, device=DEV), ck=torch.empty(nck, B, N, device=DEV))
+
+    a = outputs()
+    _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(m0), _lib.ptr(a["m"]),
+              _lib.ptr(a["s"]), _lib.ptr(a["pre"]), _lib.ptr(a["pk"]), _lib.ptr(a["r"]), _lib.ptr(a["ck"]), T, B, F, N,
+              0, T, ck_every, 0.9, 0.6, -0.1, 5.0, _lib.RULE_THRESHOLD, pr, stream)
+    b = outputs()
+    cur = torch.empty(T, B, N, device=DEV)
+    _gemm(x, w, cur, T * B, N, F, F, N, N, False, False, False, pr, stream, bias=bias)
+    _lib.call("myelin_lif_currents_fwd", _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(b["m"]), _lib.ptr(b["s"]),
+              _lib.ptr(b["pre"]), _lib.ptr(b["pk"]), _lib.ptr(b["r"]), None, _lib.ptr(b["ck"]), T, B, N, 0, T, 0, 0,
+              ck_every, 0.9, 0.6, -0.1, 5.0, _lib.RULE_THRESHOLD, stream)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    assert torch.equal(a["pk"], myelin.pack_spikes(a["s"]).data)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (64, 64), (130, 257), (1000, 24)])
+def test_bf16_copies_round_like_torch(rows, cols):
+    _print_case(test="bf16_copies", rows=rows, cols=cols)
+    g = seeded(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 3).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    from myelin_amd.linear import _cast_bf16, _transpose_bf16
+    assert torch.equal(_cast_bf16(x, stream), x.to(torch.bfloat16))
+    assert torch.equal(_transpose_bf16(x, stream), x.t().contiguous().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 8, 8), (72, 40, 104), (128, 128, 64), (304, 264, 1000), (256, 384, 3000),
+                                   (520, 136, 200)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_bf16_operands(M, N, K, ta, tb):
+    """bf16 operands in memory: within 1e-5 of the float64 product of the
+    bf16 values, and bit-identical to the same values passed as fp32 when
+    neither call splits K (both run one k order)."""
+
+    _print_case(test="gemm_bf16_operands", M=M, N=N, K=K, ta=ta, tb=tb)
+    g = seeded(M * 5 + N * 11 + K)
+    A = _bf16(torch.randn((K, M) if ta else (M, K), generator=g))
+    B = _bf16(torch.randn((N, K) if tb else (K, N), generator=g))
+    ref = (A.t() if ta else A).double() @ (B.t() if tb else B).double()
+    stream = _lib.stream(torch.device(DEV))
+    C = torch.empty(M, N, device=DEV)
+    Ah, Bh = A.to(DEV).to(torch.bfloat16), B.to(DEV).to(torch.bfloat16)
+    _gemm(Ah, Bh, C, M, N, K, A.shape[1], B.shape[1], N, ta, tb, False, _lib.PREC["bf16"], stream)
+    assert_norm_close(C.cpu().double(), ref, 1e-5, "C")
+    if K < 512:
+        C32 = torch.empty(M, N, device=DEV)
+        _gemm(A.to(DEV), B.to(DEV), C32, M, N, K, A.shape[1], B.shape[1], N, ta, tb, False, _lib.PREC["bf16"], stream)
+        assert torch.equal(C, C32)
+
+
+def test_gemm_bf16_operands_misaligned_rows_are_rejected():
+    stream = _lib.stream(torch.device(DEV))
+    A = torch.zeros(16, 20, dtype=torch.bfloat16, device=DEV)  # k-contiguous rows of 40 bytes
+    B = torch.zeros(20, 16, dtype=torch.bfloat16, device=DEV)
+    C = torch.empty(16, 16, device=DEV)
+    with pytest.raises(ValueError, match="aligned"):
+        _gemm(A, B, C, 16, 16, 20, 20, 16, 16, False, False, False, _lib.PREC["bf16"], stream)
+    with pytest.raises(ValueError, match="bf16 precision"):
+        _gemm(A[:, :16], B[:16], C, 16, 16, 16, 20, 16, 16, False, False, False, _lib.PREC["fp32"], stream)
+
+
+@pytest.mark.parametrize("T,B,F,N", [(13, 20, 200, 304), (9, 48, 96, 256), (5, 7, 64, 128), (20, 3, 48, 64)])
+def test_fused_forward_bf16_operands_match_fp32_operands(T, B, F, N):
+    _print_case(test="fused_bf16_operands", T=T, B=B, F=F, N=N)
+    g = seeded(T * 77 + N)
+    x = (torch.rand(T, B, F, generator=g) < 0.4).float().to(DEV)
+    w = _bf16((torch.rand(F, N, generator=g) - 0.4) * 0.5).to(DEV)
+    bias = (torch.rand(N, generator=g) * 0.1).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    from myelin_amd.linear import _cast_bf16, _transpose_bf16
+    res = []
+    for half in (False, True):
+        m = torch.empty(B, N, device=DEV)
+        s = torch.empty(T, B, N, device=DEV)
+        pre = torch.empty(T, B, N, device=DEV)
+        tail = (_lib.ptr(bias), None, _lib.ptr(m), _lib.ptr(s), _lib.ptr(pre), None, None, None, T, B, F, N, 0, T, 1,
+                0.9, 0.6, -0.1, 5.0, _lib.RULE_THRESHOLD)
+        if half:
+            xh, wt = _cast_bf16(x, stream), _transpose_bf16(w, stream)
+            _lib.call("myelin_linear_lif_fwd_bf16", _lib.ptr(xh), _lib.ptr(wt), *tail, stream)
+        else:
+            _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *tail, _lib.PREC["bf16"], stream)
+        res.append((m.cpu(), s.cpu(), pre.cpu()))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
