@@ -331,251 +331,205 @@ __device__ __forceinline__ void store_kvec(typename Prec<PREC>::T *dst, const fl
   }
 }
 
-// One operand's stage: 128 (mn) x KS (k) from fp32 global memory.
+// One operand's stage: 128 (mn) x KS (k), loaded from global memory into
+// one of D register sets (so up to D stages can be in flight) and stored
+// to LDS as [mn][k] in the MFMA input type, always as 16-byte writes.
 //  KC: element (mn, k) at base[mn * ld + k];  MN: at base[k * ld + mn].
-// Requires 16-byte aligned base and ld % 4 == 0.
-template <int PREC, bool KC>
-struct BigLoader {
-  static constexpr int KS = Prec<PREC>::KS;
-  static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));  // k per LDS vector
-  static constexpr int NP = KC ? kBig * KS / KQ / 256 : 1;                          // pieces per thread (4 | 1)
-  float v[4 * KQ];
-  const float *p;
-  int64_t ld, mn_lim;
-  int mn[NP], kk[NP];
-  bool full;  // all 128 mn of the tile exist (uniform)
-
-  __device__ __forceinline__ void init(int tid, const void *base_, int64_t mn0, int64_t mn_total, int64_t ld_) {
-    const float *base = static_cast<const float *>(base_);
-    ld = ld_;
-    mn_lim = mn_total - mn0;
-    full = mn_lim >= kBig;
-    if constexpr (KC) {
-#pragma unroll
-      for (int e = 0; e < NP; ++e) {
-        const int idx = e * 256 + tid;
-        mn[e] = idx / (KS / KQ);
-        kk[e] = (idx % (KS / KQ)) * KQ;
-      }
-      p = base + mn0 * ld;
-    } else {
-      mn[0] = (tid & 31) * 4;
-      kk[0] = (tid >> 5) * KQ;
-      p = base + mn0;
-    }
-  }
-
-  // interior stages: straight-line 16-byte loads, no guards
-  __device__ __forceinline__ void fast(int64_t k0) {
-    if constexpr (KC) {
-#pragma unroll
-      for (int e = 0; e < NP; ++e) {
-        const float *q = p + mn[e] * ld + k0 + kk[e];
-#pragma unroll
-        for (int h = 0; h < KQ; h += 4) {
-          const f4 t = *reinterpret_cast<const f4 *>(q + h);
-          v[e * KQ + h] = t.x;
-          v[e * KQ + h + 1] = t.y;
-          v[e * KQ + h + 2] = t.z;
-          v[e * KQ + h + 3] = t.w;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < KQ; ++j) {
-        const f4 t = *reinterpret_cast<const f4 *>(p + (k0 + kk[0] + j) * ld + mn[0]);
-        v[4 * j] = t.x;
-        v[4 * j + 1] = t.y;
-        v[4 * j + 2] = t.z;
-        v[4 * j + 3] = t.w;
-      }
-    }
-  }
-
-  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
-    if (full && k0 + KS <= ke)
-      fast(k0);
-    else
-      slow(k0, ke);
-  }
-
-  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
-    if constexpr (KC) {
-#pragma unroll
-      for (int e = 0; e < NP; ++e) {
-        const int64_t k = k0 + kk[e];
-        const float *q = p + mn[e] * ld + k;
-        if (mn[e] < mn_lim && k + KQ <= ke) {
-#pragma unroll
-          for (int h = 0; h < KQ; h += 4) {
-            const f4 t = *reinterpret_cast<const f4 *>(q + h);
-            v[e * KQ + h] = t.x;
-            v[e * KQ + h + 1] = t.y;
-            v[e * KQ + h + 2] = t.z;
-            v[e * KQ + h + 3] = t.w;
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < KQ; ++i) v[e * KQ + i] = (mn[e] < mn_lim && k + i < ke) ? q[i] : 0.0f;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < KQ; ++j) {
-        const int64_t k = k0 + kk[0] + j;
-        const float *q = p + k * ld + mn[0];
-        if (k < ke && mn[0] + 3 < mn_lim) {
-          const f4 t = *reinterpret_cast<const f4 *>(q);
-          v[4 * j] = t.x;
-          v[4 * j + 1] = t.y;
-          v[4 * j + 2] = t.z;
-          v[4 * j + 3] = t.w;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[4 * j + i] = (k < ke && mn[0] + i < mn_lim) ? q[i] : 0.0f;
-        }
-      }
-    }
-  }
-
-  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
-    if constexpr (KC) {
-#pragma unroll
-      for (int e = 0; e < NP; ++e) store_kvec<PREC>(&dst[mn[e]][kk[e]], &v[e * KQ]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x[KQ];
-#pragma unroll
-        for (int j = 0; j < KQ; ++j) x[j] = v[4 * j + i];
-        store_kvec<PREC>(&dst[mn[0] + i][kk[0]], x);
-      }
-    }
-  }
-};
-
-// The same stage from bf16 operands in memory (raw 16-bit values; bf16 MFMA
-// only).  KC: one 16-byte load of 8 k per piece, copied to LDS as is.  MN: a
-// thread loads a 4 (mn) x 8 (k) block as eight 8-byte rows and regroups the
-// halves into four 8-k vectors.  Requires 16-byte (KC) / 8-byte (MN)
-// aligned rows: base aligned and ld % 8 == 0 (KC) / ld % 4 == 0 (MN).
+// Source S = float: KC pieces are KQ consecutive k (one LDS vector); an MN
+// thread loads a 4 (mn) x KQ (k) block as KQ float4 rows and writes four
+// k-vectors.  S = uint16_t (bf16 bits, bf16 MFMA only): KC pieces are one
+// 16-byte load of 8 k copied as is; an MN thread loads a 4 x 8 block as
+// eight 8-byte rows and regroups the 16-bit halves into four 8-k vectors.
+// Alignment: fp32 rows 16 bytes (ld % 4 == 0); bf16 KC rows 16 bytes
+// (ld % 8 == 0), bf16 MN rows 8 bytes (ld % 4 == 0).  The per-piece
+// addresses are computed once; load() takes a uniform fast path (no guards)
+// for stages fully inside the tile and K range.
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
 
-template <bool KC>
-struct BigLoaderH {
-  static constexpr int KS = Prec<1>::KS;  // 64
-  static constexpr int NP = KC ? 4 : 1;
-  u4 v4[KC ? 4 : 1];
-  u2 v2[KC ? 1 : 8];
-  const uint16_t *p;
+template <int PREC, bool KC, typename S, int D>
+struct BigLoader {
+  static constexpr bool H = sizeof(S) == 2;
+  static_assert(!H || PREC == 1, "bf16 operands need the bf16 MFMA");
+  static constexpr int KS = Prec<PREC>::KS;
+  static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));  // k per LDS vector
+  static constexpr int NP = KC ? kBig * KS / KQ / 256 : 1;                          // pieces per thread
+  // register set: fp32 -> 4*KQ floats; bf16 KC -> 4 x u4; bf16 MN -> 8 x u2
+  static constexpr int NW = H ? (KC ? 16 : 16) : 4 * KQ;
+  unsigned int v[D][NW];
+  const S *q[NP];      // KC: piece row + its k offset; MN: k row kk, column mn
+  int kk[NP];          // k offset of the piece (KC) / of the thread's k rows (MN)
+  bool ok[NP];         // KC: piece row exists; MN: all 4 columns exist
+  int mn0_;            // MN: first column of the thread's block
   int64_t ld, mn_lim;
-  int mn[NP], kk[NP];
-  bool full;  // all 128 mn of the tile exist (uniform)
 
   __device__ __forceinline__ void init(int tid, const void *base_, int64_t mn0, int64_t mn_total, int64_t ld_) {
-    const uint16_t *base = static_cast<const uint16_t *>(base_);
+    const S *base = static_cast<const S *>(base_);
     ld = ld_;
     mn_lim = mn_total - mn0;
-    full = mn_lim >= kBig;
+    // fast() reads rows / columns past the tile edge from a clamped, in-range
+    // address: they only feed outputs the epilogue discards
     if constexpr (KC) {
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
         const int idx = e * 256 + tid;
-        mn[e] = idx / 8;
-        kk[e] = (idx % 8) * 8;
+        const int mn = idx / (KS / KQ);
+        kk[e] = (idx % (KS / KQ)) * KQ;
+        ok[e] = mn < mn_lim;
+        const int64_t mc = ok[e] ? mn : mn_lim - 1;
+        q[e] = base + (mn0 + mc) * ld + kk[e];
       }
-      p = base + mn0 * ld;
     } else {
-      mn[0] = (tid & 31) * 4;
-      kk[0] = (tid >> 5) * 8;
-      p = base + mn0;
+      mn0_ = (tid & 31) * 4;
+      kk[0] = (tid >> 5) * (H ? 8 : KQ);
+      ok[0] = mn0_ + 3 < mn_lim;
+      const int64_t mc = ok[0] ? mn0_ : ((mn_lim - 4) & ~static_cast<int64_t>(3));
+      q[0] = base + kk[0] * ld + mn0 + mc;
     }
   }
 
+  template <int d>
   __device__ __forceinline__ void fast(int64_t k0) {
     if constexpr (KC) {
 #pragma unroll
-      for (int e = 0; e < NP; ++e) v4[e] = *reinterpret_cast<const u4 *>(p + mn[e] * ld + k0 + kk[e]);
-    } else {
+      for (int e = 0; e < NP; ++e) {
+        const S *src = q[e] + k0;
+        if constexpr (H) {
+          const u4 t = *reinterpret_cast<const u4 *>(src);
+          v[d][4 * e] = t.x;
+          v[d][4 * e + 1] = t.y;
+          v[d][4 * e + 2] = t.z;
+          v[d][4 * e + 3] = t.w;
+        } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v2[j] = *reinterpret_cast<const u2 *>(p + (k0 + kk[0] + j) * ld + mn[0]);
+          for (int h = 0; h < KQ; h += 4) {
+            const u4 t = *reinterpret_cast<const u4 *>(src + h);
+            v[d][e * KQ + h] = t.x;
+            v[d][e * KQ + h + 1] = t.y;
+            v[d][e * KQ + h + 2] = t.z;
+            v[d][e * KQ + h + 3] = t.w;
+          }
+        }
+      }
+    } else {
+      const S *src = q[0] + k0 * ld;
+      if constexpr (H) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const u2 t = *reinterpret_cast<const u2 *>(src + j * ld);
+          v[d][2 * j] = t.x;
+          v[d][2 * j + 1] = t.y;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < KQ; ++j) {
+          const u4 t = *reinterpret_cast<const u4 *>(src + j * ld);
+          v[d][4 * j] = t.x;
+          v[d][4 * j + 1] = t.y;
+          v[d][4 * j + 2] = t.z;
+          v[d][4 * j + 3] = t.w;
+        }
+      }
     }
   }
 
-  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
-    if (full && k0 + KS <= ke)
-      fast(k0);
-    else
-      slow(k0, ke);
+  // column the MN fast path reads from (clamped at the tile edge)
+  __device__ __forceinline__ int64_t mcol() const {
+    return ok[0] ? mn0_ : ((mn_lim - 4) & ~static_cast<int64_t>(3));
   }
 
+  // one element (raw bits, zero when out of range)
+  __device__ __forceinline__ unsigned int elem(const S *src, bool in) const {
+    if (!in) return 0u;
+    if constexpr (H)
+      return *src;
+    else
+      return __builtin_bit_cast(unsigned int, *src);
+  }
+
+  template <int d>
   __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
     if constexpr (KC) {
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
+        const S *src = q[e] + k0;
         const int64_t k = k0 + kk[e];
-        const uint16_t *q = p + mn[e] * ld + k;
-        if (mn[e] < mn_lim && k + 8 <= ke) {
-          v4[e] = *reinterpret_cast<const u4 *>(q);
-        } else {
-          unsigned int w[4];
+        if constexpr (H) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const unsigned int lo = (mn[e] < mn_lim && k + 2 * i < ke) ? q[2 * i] : 0u;
-            const unsigned int hi = (mn[e] < mn_lim && k + 2 * i + 1 < ke) ? q[2 * i + 1] : 0u;
-            w[i] = lo | (hi << 16);
+            const unsigned int lo = elem(src + 2 * i, ok[e] && k + 2 * i < ke);
+            const unsigned int hi = elem(src + 2 * i + 1, ok[e] && k + 2 * i + 1 < ke);
+            v[d][4 * e + i] = lo | (hi << 16);
           }
-          v4[e] = u4{w[0], w[1], w[2], w[3]};
+        } else {
+#pragma unroll
+          for (int i = 0; i < KQ; ++i) v[d][e * KQ + i] = elem(src + i, ok[e] && k + i < ke);
         }
       }
     } else {
+      // unclamped column base (q[0] may be clamped)
+      const S *src = q[0] + k0 * ld + (mn0_ - mcol());
+      const int64_t kbase = k0 + kk[0];
+      if constexpr (H) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t k = k0 + kk[0] + j;
-        const uint16_t *q = p + k * ld + mn[0];
-        if (k < ke && mn[0] + 3 < mn_lim) {
-          v2[j] = *reinterpret_cast<const u2 *>(q);
-        } else {
+        for (int j = 0; j < 8; ++j) {
           unsigned int e4[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) e4[i] = (k < ke && mn[0] + i < mn_lim) ? q[i] : 0u;
-          v2[j] = u2{e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+          for (int i = 0; i < 4; ++i) e4[i] = elem(src + j * ld + i, kbase + j < ke && mn0_ + i < mn_lim);
+          v[d][2 * j] = e4[0] | (e4[1] << 16);
+          v[d][2 * j + 1] = e4[2] | (e4[3] << 16);
         }
+      } else {
+#pragma unroll
+        for (int j = 0; j < KQ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[d][4 * j + i] = elem(src + j * ld + i, kbase + j < ke && mn0_ + i < mn_lim);
       }
     }
   }
 
-  __device__ __forceinline__ void store(__bf16 (*dst)[BigStage<1>::LD]) const {
+  // fast() addresses are valid: the tile has a row (KC) / four columns (MN)
+  __device__ __forceinline__ bool fast_ok() const { return KC ? mn_lim >= 1 : mn_lim >= 4; }
+
+  template <int d>
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
     if constexpr (KC) {
+      const int tid = threadIdx.x;
 #pragma unroll
-      for (int e = 0; e < NP; ++e) *reinterpret_cast<u4 *>(&dst[mn[e]][kk[e]]) = v4[e];
+      for (int e = 0; e < NP; ++e) {
+        const int mn = (e * 256 + tid) / (KS / KQ);
+        if constexpr (H) {
+          *reinterpret_cast<u4 *>(&dst[mn][kk[e]]) = u4{v[d][4 * e], v[d][4 * e + 1], v[d][4 * e + 2], v[d][4 * e + 3]};
+        } else {
+          float x[KQ];
+#pragma unroll
+          for (int i = 0; i < KQ; ++i) x[i] = __builtin_bit_cast(float, v[d][e * KQ + i]);
+          store_kvec<PREC>(&dst[mn][kk[e]], x);
+        }
+      }
     } else {
-      // v2[j] = {mn0 | mn1 << 16, mn2 | mn3 << 16} at k = j; vector for mn i
-      // packs k = 2d, 2d + 1 into word d
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        unsigned int w[4];
+        if constexpr (H) {
+          // v[2j] = {mn0 | mn1 << 16}, v[2j+1] = {mn2 | mn3 << 16} at k = j;
+          // the vector for column i packs k = 2w, 2w + 1 into word w
+          unsigned int w4[4];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const unsigned int a = (i < 2) ? v2[2 * d].x : v2[2 * d].y;
-          const unsigned int b = (i < 2) ? v2[2 * d + 1].x : v2[2 * d + 1].y;
-          w[d] = (i & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+          for (int w = 0; w < 4; ++w) {
+            const unsigned int a = v[d][2 * (2 * w) + (i >> 1)];
+            const unsigned int b = v[d][2 * (2 * w + 1) + (i >> 1)];
+            w4[w] = (i & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+          }
+          *reinterpret_cast<u4 *>(&dst[mn0_ + i][kk[0]]) = u4{w4[0], w4[1], w4[2], w4[3]};
+        } else {
+          float x[KQ];
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) x[j] = __builtin_bit_cast(float, v[d][4 * j + i]);
+          store_kvec<PREC>(&dst[mn0_ + i][kk[0]], x);
         }
-        *reinterpret_cast<u4 *>(&dst[mn[0] + i][kk[0]]) = u4{w[0], w[1], w[2], w[3]};
       }
     }
   }
-};
-
-// loader for operand source type S (float, or uint16_t = bf16 bits)
-template <int PREC, bool KC, typename S>
-struct PickLoader {
-  using type = BigLoader<PREC, KC>;
-};
-template <bool KC>
-struct PickLoader<1, KC, uint16_t> {
-  using type = BigLoaderH<KC>;
 };
 
 template <int PREC>
@@ -604,21 +558,106 @@ __device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int w
   }
 }
 
+// acc += A[128 x (kb..ke)] B[(kb..ke) x 128] over LDS double buffers.
+// Interior tiles (every row of both operands present) run the full KS-wide
+// stages with unguarded loads only, so the loop body is straight-line and
+// the compiler's wait counts stay exact: with DEPTH 2 register sets a
+// stage's loads are issued two stages before it is stored to LDS (two MFMA
+// stages hide their latency; fetches past the last full stage re-read it).
+// A partial last stage is then loaded with guards and applied, so the k
+// order is the same as in every other path.  Edge tiles take one guarded
+// stage at a time.  DEPTH 1 (fp32 operands of the bf16 MFMA, 64 registers
+// per set): one stage ahead.
+template <int PREC, int DEPTH, class LA, class LB>
+__device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke, BigStage<PREC> (&st)[2], int wm,
+                                          int wn, int lane, f32x16 (&acc)[2][2]) {
+  constexpr int KS = Prec<PREC>::KS;
+  if (kb >= ke) return;
+  const int64_t nfull = (ke - kb) / KS;
+  if (la.fast_ok() && lb.fast_ok() && nfull > 0) {
+    const int64_t klast = kb + (nfull - 1) * KS;
+    auto kof = [&](int64_t stage) { return stage < nfull ? kb + stage * KS : klast; };
+    la.template fast<0>(kb);
+    lb.template fast<0>(kb);
+    la.template store<0>(st[0].a);
+    lb.template store<0>(st[0].b);
+    if constexpr (DEPTH == 1) {
+      __syncthreads();
+      for (int64_t sg = 0; sg < nfull; ++sg) {
+        const int buf = sg & 1;
+        la.template fast<0>(kof(sg + 1));
+        lb.template fast<0>(kof(sg + 1));
+        big_mfma<PREC>(st[buf], wm, wn, lane, acc);
+        if (sg + 1 < nfull) {
+          la.template store<0>(st[buf ^ 1].a);
+          lb.template store<0>(st[buf ^ 1].b);
+        }
+        __syncthreads();
+      }
+    } else {
+      la.template fast<1>(kof(1));
+      lb.template fast<1>(kof(1));
+      __syncthreads();
+      for (int64_t sg = 0; sg < nfull; sg += 2) {
+        // stage sg in st[0]; set 1 holds stage sg + 1; fetch sg + 2 into set 0
+        la.template fast<0>(kof(sg + 2));
+        lb.template fast<0>(kof(sg + 2));
+        big_mfma<PREC>(st[0], wm, wn, lane, acc);
+        if (sg + 1 < nfull) {
+          la.template store<1>(st[1].a);
+          lb.template store<1>(st[1].b);
+        }
+        __syncthreads();
+        if (sg + 1 >= nfull) break;
+        // stage sg + 1 in st[1]; set 0 holds stage sg + 2; fetch sg + 3 into set 1
+        la.template fast<1>(kof(sg + 3));
+        lb.template fast<1>(kof(sg + 3));
+        big_mfma<PREC>(st[1], wm, wn, lane, acc);
+        if (sg + 2 < nfull) {
+          la.template store<0>(st[0].a);
+          lb.template store<0>(st[0].b);
+        }
+        __syncthreads();
+      }
+    }
+    kb += nfull * KS;
+    if (kb >= ke) return;
+  }
+  // guarded stages: edge tiles, and the partial last stage of interior ones
+  for (int64_t k0 = kb; k0 < ke; k0 += KS) {
+    la.template slow<0>(k0, ke);
+    lb.template slow<0>(k0, ke);
+    la.template store<0>(st[0].a);
+    lb.template store<0>(st[0].b);
+    __syncthreads();
+    big_mfma<PREC>(st[0], wm, wn, lane, acc);
+    __syncthreads();
+  }
+}
+
+// register sets per operand: 2, except fp32 operands feeding the bf16 MFMA
+template <int PREC, typename S>
+constexpr int big_depth() {
+  return (PREC == 1 && sizeof(S) == 4) ? 1 : 2;
+}
+
 // Workgroup -> output tile.  Consecutive workgroup ids go round-robin to the
 // 8 XCDs (each with its own L2), so when the grid is a multiple of 8 each
 // XCD is handed a contiguous run of logical tiles; logical tiles walk groups
 // of 8 tile rows column by column, so a run shares A rows and B columns.
-__device__ __forceinline__ void big_tile(int64_t bid, int64_t nblk, int64_t tiles_m, int64_t tiles_n, int64_t &tm,
+__device__ __forceinline__ void big_tile(uint32_t bid, uint32_t nblk, uint32_t tiles_m, uint32_t tiles_n, int64_t &tm,
                                          int64_t &tn) {
-  int64_t t = bid;
+  uint32_t t = bid;
   if (nblk % 8 == 0) t = (bid % 8) * (nblk / 8) + bid / 8;
-  constexpr int64_t G = 8;
-  const int64_t per_group = G * tiles_n;
-  const int64_t group = t / per_group, first = group * G;
-  const int64_t gs = (tiles_m - first < G) ? tiles_m - first : G;
-  const int64_t in = t - group * per_group;
-  tm = first + in % gs;
-  tn = in / gs;
+  constexpr uint32_t G = 8;
+  const uint32_t per_group = G * tiles_n;
+  const uint32_t group = t / per_group, first = group * G;
+  const uint32_t gs = (tiles_m - first < G) ? tiles_m - first : G;
+  const uint32_t in = t - group * per_group;
+  // wave-uniform by construction; pinned to scalar registers so the tile
+  // bounds below branch on scalars
+  tm = __builtin_amdgcn_readfirstlane(first + in % gs);
+  tn = __builtin_amdgcn_readfirstlane(in / gs);
 }
 
 template <int PREC, bool TA, bool TB, typename S>
@@ -627,16 +666,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   constexpr int KS = Prec<PREC>::KS;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
-  const int64_t tiles_m = (g.M + kBig - 1) / kBig, tiles_n = (g.N + kBig - 1) / kBig;
+  const uint32_t tiles_m = static_cast<uint32_t>((g.M + kBig - 1) / kBig);
+  const uint32_t tiles_n = static_cast<uint32_t>((g.N + kBig - 1) / kBig);
   int64_t tm, tn;
   big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = tm * kBig, n0 = tn * kBig;
   const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
-  typename PickLoader<PREC, !TA, S>::type la;
+  constexpr int D = big_depth<PREC, S>();
+  BigLoader<PREC, !TA, S, D> la;
+  BigLoader<PREC, TB, S, D> lb;
   la.init(tid, g.A, m0, g.M, g.lda);
-  typename PickLoader<PREC, TB, S>::type lb;
   lb.init(tid, g.B, n0, g.N, g.ldb);
 
   f32x16 acc[2][2];
@@ -646,29 +687,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  if (kb < ke) {
-    la.load(kb, ke);
-    lb.load(kb, ke);
-    la.store(st[0].a);
-    lb.store(st[0].b);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t k0 = kb; k0 < ke; k0 += KS) {
-      const bool more = k0 + KS < ke;
-      if (more) {
-        la.load(k0 + KS, ke);
-        lb.load(k0 + KS, ke);
-      }
-      big_mfma<PREC>(st[buf], wm, wn, lane, acc);
-      if (more) {
-        la.store(st[buf ^ 1].a);
-        lb.store(st[buf ^ 1].b);
-      }
-      __syncthreads();
-      buf ^= 1;
-    }
-  }
+  big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
 
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -858,15 +877,21 @@ __device__ __forceinline__ float sg_deriv(float c) {
 // and consumed by the recurrence, wave w taking neurons 64*(w & 1) + lane
 // of batch rows (w >> 1)*Q .. +Q-1 (Q = BT / 2).  Same arithmetic per step
 // as linear_lif_fwd: m' = m*decay + (x_t W + bias).
-template <int PREC>
-struct BigRowLoader {  // A operand: 128 rows given by pointer (null = zero row), k-contiguous
+// A operand of the fused kernel: 128 rows given by pointer (null = zero
+// row), k-contiguous, S = float or bf16 bits, D register sets.  The caller
+// sets row[] and `full` (every row present, uniform) for each time chunk.
+template <int PREC, typename S, int D>
+struct BigRowLoader {
+  static constexpr bool H = sizeof(S) == 2;
+  static_assert(!H || PREC == 1, "bf16 operands need the bf16 MFMA");
   static constexpr int KS = Prec<PREC>::KS;
   static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));
   static constexpr int NP = kBig * KS / KQ / 256;
-  float v[NP * KQ];
-  const float *row[NP];
+  static constexpr int NW = H ? 4 : KQ;  // words per piece
+  unsigned int v[D][NP * NW];
+  const S *row[NP];
   int mn[NP], kk[NP];
-  bool full;  // every row pointer is set (uniform; set by the caller)
+  bool rok[NP];
 
   __device__ __forceinline__ void init(int tid) {
 #pragma unroll
@@ -876,98 +901,55 @@ struct BigRowLoader {  // A operand: 128 rows given by pointer (null = zero row)
       kk[e] = (idx % (KS / KQ)) * KQ;
     }
   }
+  template <int d>
   __device__ __forceinline__ void fast(int64_t k0) {
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
 #pragma unroll
-      for (int h = 0; h < KQ; h += 4) {
-        const f4 t = *reinterpret_cast<const f4 *>(row[e] + k0 + kk[e] + h);
-        v[e * KQ + h] = t.x;
-        v[e * KQ + h + 1] = t.y;
-        v[e * KQ + h + 2] = t.z;
-        v[e * KQ + h + 3] = t.w;
+      for (int h = 0; h < NW; h += 4) {
+        const u4 t = *reinterpret_cast<const u4 *>(row[e] + k0 + kk[e] + (H ? 0 : h));
+        v[d][e * NW + h] = t.x;
+        v[d][e * NW + h + 1] = t.y;
+        v[d][e * NW + h + 2] = t.z;
+        v[d][e * NW + h + 3] = t.w;
       }
     }
   }
-  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
-    if (full && k0 + KS <= ke)
-      fast(k0);
-    else
-      slow(k0, ke);
-  }
+  template <int d>
   __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       const int64_t k = k0 + kk[e];
-      if (row[e] != nullptr && k + KQ <= ke) {
-#pragma unroll
-        for (int h = 0; h < KQ; h += 4) {
-          const f4 t = *reinterpret_cast<const f4 *>(row[e] + k + h);
-          v[e * KQ + h] = t.x;
-          v[e * KQ + h + 1] = t.y;
-          v[e * KQ + h + 2] = t.z;
-          v[e * KQ + h + 3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < KQ; ++i) v[e * KQ + i] = (row[e] != nullptr && k + i < ke) ? row[e][k + i] : 0.0f;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) store_kvec<PREC>(&dst[mn[e]][kk[e]], &v[e * KQ]);
-  }
-};
-
-// A operand rows from bf16 inputs: one 16-byte load of 8 k per piece
-struct BigRowLoaderH {
-  static constexpr int KS = Prec<1>::KS;
-  static constexpr int NP = 4;
-  u4 v4[NP];
-  const uint16_t *row[NP];
-  int mn[NP], kk[NP];
-  bool full;  // every row pointer is set (uniform; set by the caller)
-
-  __device__ __forceinline__ void init(int tid) {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) {
-      const int idx = e * 256 + tid;
-      mn[e] = idx / 8;
-      kk[e] = (idx % 8) * 8;
-    }
-  }
-  __device__ __forceinline__ void fast(int64_t k0) {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) v4[e] = *reinterpret_cast<const u4 *>(row[e] + k0 + kk[e]);
-  }
-  __device__ __forceinline__ void load(int64_t k0, int64_t ke) {
-    if (full && k0 + KS <= ke)
-      fast(k0);
-    else
-      slow(k0, ke);
-  }
-  __device__ __forceinline__ void slow(int64_t k0, int64_t ke) {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) {
-      const int64_t k = k0 + kk[e];
-      if (row[e] != nullptr && k + 8 <= ke) {
-        v4[e] = *reinterpret_cast<const u4 *>(row[e] + k);
-      } else {
-        unsigned int w[4];
+      const bool ok = rok[e];
+      if constexpr (H) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const unsigned int lo = (row[e] != nullptr && k + 2 * i < ke) ? row[e][k + 2 * i] : 0u;
-          const unsigned int hi = (row[e] != nullptr && k + 2 * i + 1 < ke) ? row[e][k + 2 * i + 1] : 0u;
-          w[i] = lo | (hi << 16);
+          const unsigned int lo = (ok && k + 2 * i < ke) ? row[e][k + 2 * i] : 0u;
+          const unsigned int hi = (ok && k + 2 * i + 1 < ke) ? row[e][k + 2 * i + 1] : 0u;
+          v[d][e * NW + i] = lo | (hi << 16);
         }
-        v4[e] = u4{w[0], w[1], w[2], w[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < KQ; ++i)
+          v[d][e * NW + i] = (ok && k + i < ke) ? __builtin_bit_cast(unsigned int, row[e][k + i]) : 0u;
       }
     }
   }
-  __device__ __forceinline__ void store(__bf16 (*dst)[BigStage<1>::LD]) const {
+  __device__ __forceinline__ bool fast_ok() const { return true; }
+  template <int d>
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
 #pragma unroll
-    for (int e = 0; e < NP; ++e) *reinterpret_cast<u4 *>(&dst[mn[e]][kk[e]]) = v4[e];
+    for (int e = 0; e < NP; ++e) {
+      if constexpr (H) {
+        *reinterpret_cast<u4 *>(&dst[mn[e]][kk[e]]) =
+            u4{v[d][e * NW], v[d][e * NW + 1], v[d][e * NW + 2], v[d][e * NW + 3]};
+      } else {
+        float x[KQ];
+#pragma unroll
+        for (int i = 0; i < KQ; ++i) x[i] = __builtin_bit_cast(float, v[d][e * NW + i]);
+        store_kvec<PREC>(&dst[mn[e]][kk[e]], x);
+      }
+    }
   }
 };
 
@@ -1004,26 +986,29 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
   const float bias_n = (p.bias != nullptr && n_ok) ? p.bias[n] : 0.0f;
   int64_t next_ck = p.t_begin, ck_row = 0;
 
-  static_assert(!H || PREC == 1, "bf16 operands need the bf16 MFMA");
-  using LA = typename std::conditional<H, BigRowLoaderH, BigRowLoader<PREC>>::type;
-  using LB = typename std::conditional<H, BigLoaderH<true>, BigLoader<PREC, false>>::type;
-  LB lb;  // H: wt [N, F] rows are neurons; else w [F, N], neurons contiguous for a fixed k
-  lb.init(tid, H ? p.wt : static_cast<const void *>(p.w), n0, p.N, H ? p.F : p.N);
-  LA la;
+  using S = typename std::conditional<H, uint16_t, float>::type;
+  constexpr int D = 1;  // the recurrence state leaves no room for a second register set
+  // H: wt [N, F] rows are neurons (k-contiguous); else w [F, N], neurons
+  // contiguous for a fixed k
+  BigLoader<PREC, H, S, D> lb;
+  lb.init(tid, H ? static_cast<const void *>(p.wt) : static_cast<const void *>(p.w), n0, p.N, H ? p.F : p.N);
+  BigRowLoader<PREC, S, D> la;
   la.init(tid);
 
   for (int64_t t0 = p.t_begin; t0 < p.t_end; t0 += CH) {
 #pragma unroll
-    for (int e = 0; e < LA::NP; ++e) {
+    for (int e = 0; e < BigRowLoader<PREC, S, D>::NP; ++e) {
       const int r = la.mn[e];
       const int64_t t = t0 + r / BT, b = b0 + r % BT;
       const bool ok = t < p.t_end && b < p.B;
+      // row (t0, b0) always exists
+      const int64_t rix = ok ? t * p.B + b : t0 * p.B + b0;
+      la.rok[e] = ok;
       if constexpr (H)
-        la.row[e] = ok ? p.xh + (t * p.B + b) * p.F : nullptr;
+        la.row[e] = p.xh + rix * p.F;
       else
-        la.row[e] = ok ? p.x + (t * p.B + b) * p.F : nullptr;
+        la.row[e] = p.x + rix * p.F;
     }
-    la.full = t0 + CH <= p.t_end && b0 + BT <= p.B;
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -1031,26 +1016,7 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    la.load(0, p.F);
-    lb.load(0, p.F);
-    la.store(sm.st[0].a);
-    lb.store(sm.st[0].b);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t k0 = 0; k0 < p.F; k0 += KS) {
-      const bool more = k0 + KS < p.F;
-      if (more) {
-        la.load(k0 + KS, p.F);
-        lb.load(k0 + KS, p.F);
-      }
-      big_mfma<PREC>(sm.st[buf], wm, wn, lane, acc);
-      if (more) {
-        la.store(sm.st[buf ^ 1].a);
-        lb.store(sm.st[buf ^ 1].b);
-      }
-      __syncthreads();
-      buf ^= 1;
-    }
+    big_kloop<PREC, D>(la, lb, 0, p.F, sm.st, wm, wn, lane, acc);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
