@@ -342,8 +342,10 @@ __device__ __forceinline__ void store_kvec(typename Prec<PREC>::T *dst, const fl
 // eight 8-byte rows and regroups the 16-bit halves into four 8-k vectors.
 // Alignment: fp32 rows 16 bytes (ld % 4 == 0); bf16 KC rows 16 bytes
 // (ld % 8 == 0), bf16 MN rows 8 bytes (ld % 4 == 0).  The per-piece
-// addresses are computed once; load() takes a uniform fast path (no guards)
-// for stages fully inside the tile and K range.
+// addresses are computed once.  fast() loads a whole KS-wide stage with no
+// guards (rows / columns past the tile edge come from a clamped in-range
+// address); slow() guards every element and zero-fills (the partial last
+// stage).
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
 
@@ -559,15 +561,14 @@ __device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int w
 }
 
 // acc += A[128 x (kb..ke)] B[(kb..ke) x 128] over LDS double buffers.
-// Interior tiles (every row of both operands present) run the full KS-wide
-// stages with unguarded loads only, so the loop body is straight-line and
-// the compiler's wait counts stay exact: with DEPTH 2 register sets a
-// stage's loads are issued two stages before it is stored to LDS (two MFMA
-// stages hide their latency; fetches past the last full stage re-read it).
-// A partial last stage is then loaded with guards and applied, so the k
-// order is the same as in every other path.  Edge tiles take one guarded
-// stage at a time.  DEPTH 1 (fp32 operands of the bf16 MFMA, 64 registers
-// per set): one stage ahead.
+// The full KS-wide stages run with unguarded loads only, so the loop body
+// is straight-line and the compiler's wait counts stay exact: with DEPTH 2
+// register sets a stage's loads are issued two stages before it is stored
+// to LDS (two MFMA stages hide their latency; fetches past the last full
+// stage re-read it).  A partial last stage is then loaded with guards and
+// applied, so the k order is the same as in every other path.  DEPTH 1
+// (fp32 operands of the bf16 MFMA, 64 registers per set): one stage ahead.
+// Operands too narrow for clamped fast loads take guarded stages only.
 template <int PREC, int DEPTH, class LA, class LB>
 __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke, BigStage<PREC> (&st)[2], int wm,
                                           int wn, int lane, f32x16 (&acc)[2][2]) {
@@ -623,7 +624,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
     kb += nfull * KS;
     if (kb >= ke) return;
   }
-  // guarded stages: edge tiles, and the partial last stage of interior ones
+  // guarded stages: the partial last stage, or every stage of a too-narrow operand
   for (int64_t k0 = kb; k0 < ke; k0 += KS) {
     la.template slow<0>(k0, ke);
     lb.template slow<0>(k0, ke);
