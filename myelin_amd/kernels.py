@@ -279,11 +279,32 @@ def linear_surrogate_lif_rate_forward(
     sid = surrogate_id(surrogate)
     _check_backend(backend)
     if not hard_forward:
+        if backend == "triton_compile":
+            raise ValueError(
+                "backend='triton_compile' is experimental and currently supports only hard_forward=True"
+            )
         raise ValueError("HIP spike-rate LIF currently supports only hard_forward=True")
     if reduction not in ("mean", "none"):
         raise ValueError("reduction must be 'mean' or 'none'")
     ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
-    m, rates = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, True, synapse_precision)
+    if backend == "triton_compile":
+        # the compile-visible operators (kernels.py:637-684 of the reference)
+        if surrogate != "fast_sigmoid":
+            raise ValueError(
+                "backend='triton_compile' is experimental and currently supports only surrogate='fast_sigmoid'"
+            )
+        from myelin_amd import compile_ops
+
+        if bias is None:
+            m, rates, _ = compile_ops.linear_lif_checkpoint_rate_forward_no_bias_op(
+                inputs, weight, params.decay, params.threshold, params.reset, surrogate_slope, ck, block_b,
+                block_n, block_f)
+        else:
+            m, rates, _ = compile_ops.linear_lif_checkpoint_rate_forward_bias_op(
+                inputs, weight, bias, params.decay, params.threshold, params.reset, surrogate_slope, ck, block_b,
+                block_n, block_f)
+    else:
+        m, rates = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, True, synapse_precision)
     if reduction == "mean":
         return LIFState(membrane=m), rates.mean()
     return LIFState(membrane=m), rates

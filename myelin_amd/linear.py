@@ -216,54 +216,70 @@ class HipLinearLIFFunction(torch.autograd.Function):
             return none
         decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
         xs, w, b, pre, ckpt, wt = ctx.saved_tensors
-        T, B, F = xs.shape
-        N = w.shape[1]
-        BN = B * N
-        dev = xs.device
-        half = xs.dtype == torch.bfloat16
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
-        with torch.cuda.device(dev):
-            stream = _lib.stream(dev)
-            wg = _cast_bf16(w, stream) if (half and need_x) else w
-            gm = g_m.float().contiguous().clone() if g_m is not None else torch.zeros((B, N), device=dev)
-            g_out = None if g_out is None else g_out.float().contiguous()
-            g_spikes = None if rate else g_out
-            g_rates = g_out if rate else None
-            gx = torch.empty((T, B, F), device=dev) if need_x else None
-            gw = torch.zeros_like(w) if need_w else None
-            gb_acc = torch.zeros((B, N), device=dev) if (need_b and has_b) else None
-            chunk = T if checkpoint is None else checkpoint
-            G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
-            scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
-            n_chunks = math.ceil(T / chunk)
-            for k in range(n_chunks - 1, -1, -1):
-                t0 = k * chunk
-                t1 = min(t0 + chunk, T)
-                C = t1 - t0
-                if checkpoint is None:
-                    pre_k = pre
-                else:
-                    _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
-                             pre=scratch, wt=wt)
-                    pre_k = scratch
-                _lib.call(
-                    "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_k), _lib.ptr(g_spikes[t0:t1]) if g_spikes is not None else None,
-                    _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT[G.dtype], _lib.ptr(gb_acc),
-                    C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
-                )
-                rows = C * B
-                if gx is not None:
-                    # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
-                    _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
-                if gw is not None:
-                    # dW += X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                    _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
-            gb = None
-            if gb_acc is not None:
-                gb = torch.empty((N,), device=dev)
-                _lib.call("myelin_col_sum_f32", _lib.ptr(gb_acc), _lib.ptr(gb), B, N, 0, stream)
+        gx, gw, gb = linear_backward(xs, w, b if has_b else None, pre, ckpt, wt, g_m, g_out, decay, threshold,
+                                     reset, sid, slope, checkpoint, rate, prec, rule, need_x, need_w,
+                                     need_b and has_b)
         return gx, gw, gb, None, None, None, None, None, None, None, None, None
+
+
+def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset, sid, slope, checkpoint, rate,
+                    prec, rule, need_x=True, need_w=True, need_b=True):
+    """Gradients (dX, dW, db) of the streamed-synapse LIF, chunk by chunk in
+    reverse time: recompute the chunk's pre-reset trace from its checkpoint
+    (``checkpoint=None``: the saved trace ``pre`` covers all T), reverse the
+    recurrence into G = dL/dI, then ``dX = G W^T`` and ``dW += X^T G`` on
+    the MFMA GEMM and ``db`` as a fixed-order column sum.  ``xs`` is fp32, or
+    bf16 with ``wt = W^T`` bf16 for the bf16 synapse; ``g_out`` is dL/dspikes
+    ``[T, B, N]`` or, with ``rate``, dL/drates ``[B, N]``."""
+
+    T, B, F = xs.shape
+    N = w.shape[1]
+    BN = B * N
+    dev = xs.device
+    half = xs.dtype == torch.bfloat16
+    with torch.cuda.device(dev):
+        stream = _lib.stream(dev)
+        wg = _cast_bf16(w, stream) if (half and need_x) else w
+        gm = g_m.float().contiguous().clone() if g_m is not None else torch.zeros((B, N), device=dev)
+        g_out = None if g_out is None else g_out.float().contiguous()
+        g_spikes = None if rate else g_out
+        g_rates = g_out if rate else None
+        gx = torch.empty((T, B, F), device=dev) if need_x else None
+        gw = torch.zeros_like(w) if need_w else None
+        gb_acc = torch.zeros((B, N), device=dev) if (need_b and b is not None) else None
+        chunk = T if checkpoint is None else checkpoint
+        G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
+        scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
+        n_chunks = math.ceil(T / chunk)
+        for k in range(n_chunks - 1, -1, -1):
+            t0 = k * chunk
+            t1 = min(t0 + chunk, T)
+            C = t1 - t0
+            if checkpoint is None:
+                pre_k = pre
+            else:
+                _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
+                         pre=scratch, wt=wt)
+                pre_k = scratch
+            _lib.call(
+                "myelin_linear_pre_bwd",
+                _lib.ptr(pre_k), _lib.ptr(g_spikes[t0:t1]) if g_spikes is not None else None,
+                _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT[G.dtype], _lib.ptr(gb_acc),
+                C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
+            )
+            rows = C * B
+            if gx is not None:
+                # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
+                _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
+            if gw is not None:
+                # dW += X[t0:t1]^T @ G : [F, rows] x [rows, N]
+                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
+        gb = None
+        if gb_acc is not None:
+            gb = torch.empty((N,), device=dev)
+            _lib.call("myelin_col_sum_f32", _lib.ptr(gb_acc), _lib.ptr(gb), B, N, 0, stream)
+    return gx, gw, gb
 
 
 def linear_forward(x, w, b, params, surrogate_id: int, slope: float, checkpoint, rate: bool, precision: str,
