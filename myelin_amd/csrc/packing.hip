@@ -115,6 +115,8 @@ __global__ __launch_bounds__(256) void unpack_generic(const int32_t *__restrict_
 }
 
 // ---- counts --------------------------------------------------------------
+inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
 struct LeadInfo {
   int ndim;
   int64_t shape[8];
@@ -180,6 +182,55 @@ __global__ __launch_bounds__(256) void row_counts_lane(const int32_t *__restrict
     out[row] = c;
   } else {
     atomicAdd(reinterpret_cast<unsigned long long *>(out + out_index(row, li)), static_cast<unsigned long long>(c));
+  }
+}
+
+// Counts whose kept leading dims form one contiguous block: output o sums
+// the rows (a*P + o)*Q + i, a < A, i < Q (k = a*Q + i runs over AQ = A*Q).
+// Blocks (o, s) of 16 waves split output o's AQ rows into S slices; wave q
+// of a block takes k = q, q + 16, ... of its slice, four rows per pass, and
+// wave 0 adds the 16 wave sums.  S == 1 stores the count; S > 1 adds the S
+// slice counts atomically (out zeroed; a handful of atomics per output, and
+// integer sums are order-independent).
+constexpr int kBlkWaves = 16;
+
+__global__ __launch_bounds__(1024) void row_counts_block(const int32_t *__restrict__ words, int64_t W,
+                                                         uint32_t last_mask, int64_t P, int64_t Q, int64_t AQ,
+                                                         int64_t slice, int atomic, int64_t *__restrict__ out) {
+  __shared__ int64_t part[kBlkWaves];
+  const int lane = static_cast<int>(threadIdx.x & 63), q = static_cast<int>(threadIdx.x >> 6);
+  const int64_t o = blockIdx.x;
+  const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * slice;
+  const int64_t k_end = (k_begin + slice < AQ) ? k_begin + slice : AQ;
+  int64_t c = 0;
+  for (int64_t k = k_begin + q; k < k_end; k += 4 * kBlkWaves) {
+    const int32_t *rw[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t kk = k + u * kBlkWaves;
+      ok[u] = kk < k_end;
+      const int64_t a = kk / Q, i = kk - a * Q;
+      rw[u] = ok[u] ? words + ((a * P + o) * Q + i) * W : words;
+    }
+    for (int64_t j = lane; j < W; j += kWave) {
+      const uint32_t m = (j == W - 1) ? last_mask : 0xffffffffu;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (ok[u]) c += __popc(static_cast<uint32_t>(rw[u][j]) & m);
+    }
+  }
+  c = wave_sum(c);
+  if (lane == 0) part[q] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t t = 0;
+#pragma unroll
+    for (int i = 0; i < kBlkWaves; ++i) t += part[i];
+    if (atomic)
+      atomicAdd(reinterpret_cast<unsigned long long *>(out + o), static_cast<unsigned long long>(t));
+    else
+      out[o] = t;
   }
 }
 
@@ -356,8 +407,36 @@ extern "C" int myelin_packed_counts(const int32_t *words, int ndim_lead, const i
     }
   }
   hipStream_t s = myelin::as_hip(stream);
-  const bool direct = (reduce_mask & ((1u << ndim_lead) - 1u)) == 0;
-  if (!direct) {
+  const uint32_t lead_mask = ndim_lead > 0 ? ((1u << ndim_lead) - 1u) : 0u;
+  const bool direct = (reduce_mask & lead_mask) == 0;
+  // kept leading dims [d0, d1] contiguous (or none kept): out = (row / Q) % P
+  int d0 = -1, d1 = -1;
+  for (int d = 0; d < ndim_lead; ++d)
+    if (!(reduce_mask & (1u << d))) {
+      if (d0 < 0) d0 = d;
+      d1 = d;
+    }
+  bool block_ok = !direct;
+  int64_t P = 1, Q = 1;
+  if (block_ok) {
+    for (int d = (d0 < 0 ? ndim_lead : d0); d <= d1; ++d) {
+      if (reduce_mask & (1u << d)) block_ok = false;
+      P *= lead_shape[d];
+    }
+    for (int d = (d1 < 0 ? ndim_lead : d1 + 1); d < ndim_lead; ++d) Q *= lead_shape[d];
+  }
+  // heavy reductions onto few outputs take the block kernel; others scatter
+  const int64_t AQ = kept > 0 ? rows / kept : 0;
+  block_ok = block_ok && kept <= 65535 && AQ >= 16;
+  int64_t S = 1;
+  if (block_ok) {
+    S = cdiv64(256, kept);
+    const int64_t by_rows = cdiv64(AQ, 64);
+    if (S > by_rows) S = by_rows;
+    if (S > 65535) S = 65535;
+    if (S < 1) S = 1;
+  }
+  if (!direct && (!block_ok || S > 1)) {
     fill_i64<<<dim3(blocks(kept)), dim3(256), 0, s>>>(out, kept);
     if (int rc = myelin::launched("packed_counts zero")) return rc;
   }
@@ -366,7 +445,11 @@ extern "C" int myelin_packed_counts(const int32_t *words, int ndim_lead, const i
   const int64_t W = (n + 31) / 32;
   const int rem = static_cast<int>(n % 32);
   const uint32_t last_mask = rem ? ((1u << rem) - 1u) : 0xffffffffu;
-  if (W >= 16) {
+  if (block_ok) {
+    const int64_t slice = cdiv64(AQ, S);
+    row_counts_block<<<dim3(static_cast<unsigned>(kept), static_cast<unsigned>(S)), dim3(1024), 0, s>>>(
+        words, W, last_mask, P, Q, AQ, slice, S > 1 ? 1 : 0, out);
+  } else if (W >= 16) {
     const dim3 grid(blocks(rows * 64));
     if (direct)
       row_counts_wave<true><<<grid, dim3(256), 0, s>>>(words, rows, W, last_mask, li, out);

@@ -72,7 +72,10 @@ def test_pack_signed_zero_nan_and_high_bit():
     assert torch.equal(myelin.pack_spikes(h.to(DEV)).data.cpu(), R.pack_spikes(h)[0])
 
 
-@pytest.mark.parametrize("shape", [(3, 2, 35), (4, 3, 64), (2, 3, 5, 33), (6, 100)])
+# the last three reduce >= 16 rows onto each output, which takes the
+# atomic-free block kernel when the kept leading dims are contiguous
+@pytest.mark.parametrize("shape", [(3, 2, 35), (4, 3, 64), (2, 3, 5, 33), (6, 100), (40, 6, 5, 70), (300, 4, 100),
+                                   (64, 3, 2100)])
 def test_counts_and_rates_every_dim_bit_exact(shape):
     _print_case(test="counts", shape=shape)
     s = _spikes(shape, 11 + len(shape))
