@@ -574,6 +574,13 @@ int launch_fwd(const FwdArgs &a, hipStream_t stream) {
     if (ok) break;
     v >>= 1;
   }
+  // Small grids (under two waves per SIMD at this width) without
+  // checkpoints: one neuron per lane and 32 steps in flight, so a latency-
+  // bound walk over T has twice the lanes and four times the loads outstanding.
+  if (a.ckpt_m == nullptr && (a.BN + v - 1) / v < 2 * 1024 * 64) {
+    fwd_dense<ALIF, RULE, 1, 4 * MYELIN_FWD_UNROLL><<<dim3(blocks_for(a.BN)), dim3(256), 0, stream>>>(a);
+    return myelin::launched("fwd_dense");
+  }
   const int64_t lanes = (a.BN + v - 1) / v;
   const dim3 grid(blocks_for(lanes));
   constexpr int U = MYELIN_FWD_UNROLL;
