@@ -310,13 +310,13 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
 // ---------------------------------------------------------------------------
 constexpr int kBig = 128;
 
-template <int PREC>
+template <int PREC, int BM = kBig, int BN = kBig>
 struct BigStage {
   using T = typename Prec<PREC>::T;
   static constexpr int KS = Prec<PREC>::KS;                         // 128 bytes of k per row
   static constexpr int LD = KS + 16 / static_cast<int>(sizeof(T));  // + 16-byte pad
-  alignas(16) T a[kBig][LD];
-  alignas(16) T b[kBig][LD];
+  alignas(16) T a[BM][LD];
+  alignas(16) T b[BN][LD];
 };
 
 template <int PREC>
@@ -349,13 +349,18 @@ __device__ __forceinline__ void store_kvec(typename Prec<PREC>::T *dst, const fl
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
 
-template <int PREC, bool KC, typename S, int D>
+template <int PREC, bool KC, typename S, int D, int ROWS = kBig, int NT = 256>
 struct BigLoader {
   static constexpr bool H = sizeof(S) == 2;
   static_assert(!H || PREC == 1, "bf16 operands need the bf16 MFMA");
   static constexpr int KS = Prec<PREC>::KS;
   static constexpr int KQ = 16 / static_cast<int>(sizeof(typename Prec<PREC>::T));  // k per LDS vector
-  static constexpr int NP = KC ? kBig * KS / KQ / 256 : 1;                          // pieces per thread
+  static constexpr int NP = KC ? ROWS * KS / KQ / NT : 1;                            // pieces per thread
+  // MN: ROWS/4 column blocks x 8 k-groups; with more threads than blocks the
+  // extra threads load and store a duplicate of block tid % MNB (same data)
+  static constexpr int MNB = ROWS / 4 * 8;
+  static_assert(KC ? (ROWS * KS / KQ) % NT == 0 : NT % MNB == 0 || MNB % NT == 0, "thread mapping");
+  static_assert(KC || MNB <= NT, "one MN block per thread at most");
   // register set: fp32 -> 4*KQ floats; bf16 KC -> 4 x u4; bf16 MN -> 8 x u2
   static constexpr int NW = H ? (KC ? 16 : 16) : 4 * KQ;
   unsigned int v[D][NW];
@@ -374,7 +379,7 @@ struct BigLoader {
     if constexpr (KC) {
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
-        const int idx = e * 256 + tid;
+        const int idx = e * NT + tid;
         const int mn = idx / (KS / KQ);
         kk[e] = (idx % (KS / KQ)) * KQ;
         ok[e] = mn < mn_lim;
@@ -382,8 +387,9 @@ struct BigLoader {
         q[e] = base + (mn0 + mc) * ld + kk[e];
       }
     } else {
-      mn0_ = (tid & 31) * 4;
-      kk[0] = (tid >> 5) * (H ? 8 : KQ);
+      const int tt = tid % MNB;
+      mn0_ = (tt % (ROWS / 4)) * 4;
+      kk[0] = (tt / (ROWS / 4)) * (H ? 8 : KQ);
       ok[0] = mn0_ + 3 < mn_lim;
       const int64_t mc = ok[0] ? mn0_ : ((mn_lim - 4) & ~static_cast<int64_t>(3));
       q[0] = base + kk[0] * ld + mn0 + mc;
@@ -499,7 +505,7 @@ struct BigLoader {
       const int tid = threadIdx.x;
 #pragma unroll
       for (int e = 0; e < NP; ++e) {
-        const int mn = (e * 256 + tid) / (KS / KQ);
+        const int mn = (e * NT + tid) / (KS / KQ);
         if constexpr (H) {
           *reinterpret_cast<u4 *>(&dst[mn][kk[e]]) = u4{v[d][4 * e], v[d][4 * e + 1], v[d][4 * e + 2], v[d][4 * e + 3]};
         } else {
@@ -534,8 +540,8 @@ struct BigLoader {
   }
 };
 
-template <int PREC>
-__device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
+template <int PREC, class ST>
+__device__ __forceinline__ void big_mfma(const ST &st, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
   constexpr int KS = Prec<PREC>::KS, KM = Prec<PREC>::KM, KV = Prec<PREC>::KV;
   const int r = 64 * wm + (lane & 31), c = 64 * wn + (lane & 31), kq = (lane >> 5) * KV;
 #pragma unroll
@@ -569,9 +575,9 @@ __device__ __forceinline__ void big_mfma(const BigStage<PREC> &st, int wm, int w
 // applied, so the k order is the same as in every other path.  DEPTH 1
 // (fp32 operands of the bf16 MFMA, 64 registers per set): one stage ahead.
 // Operands too narrow for clamped fast loads take guarded stages only.
-template <int PREC, int DEPTH, class LA, class LB>
-__device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke, BigStage<PREC> (&st)[2], int wm,
-                                          int wn, int lane, f32x16 (&acc)[2][2]) {
+template <int PREC, int DEPTH, class LA, class LB, class ST>
+__device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke, ST (&st)[2], int wm, int wn,
+                                          int lane, f32x16 (&acc)[2][2]) {
   constexpr int KS = Prec<PREC>::KS;
   if (kb >= ke) return;
   const int64_t nfull = (ke - kb) / KS;
@@ -588,7 +594,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         const int buf = sg & 1;
         la.template fast<0>(kof(sg + 1));
         lb.template fast<0>(kof(sg + 1));
-        big_mfma<PREC>(st[buf], wm, wn, lane, acc);
+        big_mfma<PREC, ST>(st[buf], wm, wn, lane, acc);
         if (sg + 1 < nfull) {
           la.template store<0>(st[buf ^ 1].a);
           lb.template store<0>(st[buf ^ 1].b);
@@ -603,7 +609,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         // stage sg in st[0]; set 1 holds stage sg + 1; fetch sg + 2 into set 0
         la.template fast<0>(kof(sg + 2));
         lb.template fast<0>(kof(sg + 2));
-        big_mfma<PREC>(st[0], wm, wn, lane, acc);
+        big_mfma<PREC, ST>(st[0], wm, wn, lane, acc);
         if (sg + 1 < nfull) {
           la.template store<1>(st[1].a);
           lb.template store<1>(st[1].b);
@@ -613,7 +619,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         // stage sg + 1 in st[1]; set 0 holds stage sg + 2; fetch sg + 3 into set 1
         la.template fast<1>(kof(sg + 3));
         lb.template fast<1>(kof(sg + 3));
-        big_mfma<PREC>(st[1], wm, wn, lane, acc);
+        big_mfma<PREC, ST>(st[1], wm, wn, lane, acc);
         if (sg + 2 < nfull) {
           la.template store<0>(st[0].a);
           lb.template store<0>(st[0].b);
@@ -631,7 +637,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
     la.template store<0>(st[0].a);
     lb.template store<0>(st[0].b);
     __syncthreads();
-    big_mfma<PREC>(st[0], wm, wn, lane, acc);
+    big_mfma<PREC, ST>(st[0], wm, wn, lane, acc);
     __syncthreads();
   }
 }
@@ -661,23 +667,25 @@ __device__ __forceinline__ void big_tile(uint32_t bid, uint32_t nblk, uint32_t t
   tn = __builtin_amdgcn_readfirstlane(in / gs);
 }
 
-template <int PREC, bool TA, bool TB, typename S>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
-  __shared__ BigStage<PREC> st[2];
-  constexpr int KS = Prec<PREC>::KS;
+// BM x BN output tile, one wave per 64 x 64 quarter: (BM/64) x (BN/64)
+// waves of 2 x 2 MFMA blocks.
+template <int PREC, bool TA, bool TB, typename S, int BM, int BN>
+__global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
+  constexpr int NT = BM * BN / 64;
+  __shared__ BigStage<PREC, BM, BN> st[2];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
-  const uint32_t tiles_m = static_cast<uint32_t>((g.M + kBig - 1) / kBig);
-  const uint32_t tiles_n = static_cast<uint32_t>((g.N + kBig - 1) / kBig);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / (BN / 64), wn = w % (BN / 64);
+  const uint32_t tiles_m = static_cast<uint32_t>((g.M + BM - 1) / BM);
+  const uint32_t tiles_n = static_cast<uint32_t>((g.N + BN - 1) / BN);
   int64_t tm, tn;
   big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = tm * kBig, n0 = tn * kBig;
+  const int64_t m0 = tm * BM, n0 = tn * BN;
   const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
   constexpr int D = big_depth<PREC, S>();
-  BigLoader<PREC, !TA, S, D> la;
-  BigLoader<PREC, TB, S, D> lb;
+  BigLoader<PREC, !TA, S, D, BM, NT> la;
+  BigLoader<PREC, TB, S, D, BN, NT> lb;
   la.init(tid, g.A, m0, g.M, g.lda);
   lb.init(tid, g.B, n0, g.N, g.ldb);
 
@@ -1319,12 +1327,10 @@ void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) 
 }
 
 // K splits for an output of `tiles` workgroups: split when the output alone
-// gives under ~2 workgroups per CU (load latency stays exposed with one) and
-// K is long.
+// gives under `want` workgroups (about two per CU) and K is long.
 template <int PREC>
-int64_t plan_splits(int64_t tiles, int64_t K, bool big) {
+int64_t plan_splits(int64_t tiles, int64_t K, int64_t want) {
   constexpr int KS = Prec<PREC>::KS;
-  const int64_t want = 512;
   if (tiles >= want || K < 8 * KS) return 1;
   int64_t splits = cdiv(want, tiles);
   const int64_t max_by_k = K / (4 * KS);
@@ -1345,15 +1351,31 @@ bool bf16_aligned(const void *q, int64_t ld, bool kcontig) {
   return kcontig ? (myelin::aligned(q, 16) && ld % 8 == 0) : (myelin::aligned(q, 8) && ld % 4 == 0);
 }
 
-template <int PREC, bool TA, bool TB>
+template <int PREC, bool TA, bool TB, int BM, int BN>
 void launch_big(const GemmArgs &g, bool half, dim3 grid, hipStream_t s) {
+  constexpr int NT = BM * BN / 64;
   if constexpr (PREC == 1) {
     if (half) {
-      gemm_big<1, TA, TB, uint16_t><<<grid, dim3(256), 0, s>>>(g);
+      gemm_big<1, TA, TB, uint16_t, BM, BN><<<grid, dim3(NT), 0, s>>>(g);
       return;
     }
   }
-  gemm_big<PREC, TA, TB, float><<<grid, dim3(256), 0, s>>>(g);
+  gemm_big<PREC, TA, TB, float, BM, BN><<<grid, dim3(NT), 0, s>>>(g);
+}
+
+// Only 128 x 128 tiles are launched: 256 x 128 (8 waves, 110 KB of LDS, so
+// one workgroup per CU) measured slower on the synapse shapes, every stage
+// barrier stalling all 8 waves where two 4-wave workgroups overlap.
+template <int PREC, int BM, int BN>
+void launch_big_t(const GemmArgs &g, int ta, int tb, bool half, dim3 grid, hipStream_t s) {
+  if (!ta && !tb)
+    launch_big<PREC, false, false, BM, BN>(g, half, grid, s);
+  else if (!ta && tb)
+    launch_big<PREC, false, true, BM, BN>(g, half, grid, s);
+  else if (ta && !tb)
+    launch_big<PREC, true, false, BM, BN>(g, half, grid, s);
+  else
+    launch_big<PREC, true, true, BM, BN>(g, half, grid, s);
 }
 
 template <int PREC>
@@ -1363,7 +1385,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
   if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
-  int64_t splits = g.ws != nullptr ? plan_splits<PREC>(tiles, g.K, big) : 1;
+  int64_t splits = g.ws != nullptr ? plan_splits<PREC>(tiles, g.K, 512) : 1;
   while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
   g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
   splits = cdiv(g.K, g.kchunk);
@@ -1371,14 +1393,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   g.splits = static_cast<int>(splits);
   if (big) {
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
-    if (!ta && !tb)
-      launch_big<PREC, false, false>(g, half, grid, s);
-    else if (!ta && tb)
-      launch_big<PREC, false, true>(g, half, grid, s);
-    else if (ta && !tb)
-      launch_big<PREC, true, false>(g, half, grid, s);
-    else
-      launch_big<PREC, true, true>(g, half, grid, s);
+    launch_big_t<PREC, kBig, kBig>(g, ta, tb, half, grid, s);
   } else {
     const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
     // 16-byte loads per operand where its base and leading dimension allow
@@ -1436,11 +1451,11 @@ void launch_currents(const CurArgs &a, dim3 grid, hipStream_t s) {
 
 extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, int precision) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // the largest split either tiling of this output could use
   int64_t most = 1;
   for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
     const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
-    const bool big = edge == kBig;
-    const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, big) : plan_splits<0>(tiles, K, big);
+    const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, 512) : plan_splits<0>(tiles, K, 512);
     if (s > most) most = s;
   }
   return most > 1 ? most * M * N : 0;

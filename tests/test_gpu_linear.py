@@ -43,7 +43,7 @@ def _bf16(t):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (64, 64, 64), (70, 33, 100), (300, 17, 784), (5, 200, 10),
                                    (129, 65, 31), (128, 128, 64), (300, 260, 1000), (256, 384, 3000),
-                                   (520, 132, 200), (129, 130, 64)])
+                                   (520, 132, 200), (129, 130, 64), (8200, 1032, 72)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
 def test_gemm(M, N, K, ta, tb, prec):
@@ -71,13 +71,14 @@ def test_gemm(M, N, K, ta, tb, prec):
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
-def test_gemm_tile_sizes_sum_identically(ta, tb, prec):
-    """The 128 x 128 kernel (16-byte-aligned operands) and the 64 x 64 kernel
-    (same operands one float off alignment) run the same k order per output
-    element, so with no K split both give bit-identical products."""
+@pytest.mark.parametrize("M,N,K", [(260, 200, 300), (8200, 1032, 72)])
+def test_gemm_tile_sizes_sum_identically(ta, tb, prec, M, N, K):
+    """The 128 x 128 / 256 x 128 kernels (16-byte-aligned operands) and the
+    64 x 64 kernel (same operands one float off alignment) run the same k
+    order per output element, so with no K split all give bit-identical
+    products."""
 
-    _print_case(test="gemm_tiles", ta=ta, tb=tb, prec=prec)
-    M, N, K = 260, 200, 300
+    _print_case(test="gemm_tiles", ta=ta, tb=tb, prec=prec, M=M, N=N, K=K)
     g = seeded(99)
     A = torch.randn((K, M) if ta else (M, K), generator=g)
     B = torch.randn((N, K) if tb else (K, N), generator=g)
@@ -328,7 +329,7 @@ def test_bf16_copies_round_like_torch(rows, cols):
 
 
 @pytest.mark.parametrize("M,N,K", [(8, 8, 8), (72, 40, 104), (128, 128, 64), (304, 264, 1000), (256, 384, 3000),
-                                   (520, 136, 200)])
+                                   (520, 136, 200), (8200, 1032, 72)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 def test_gemm_bf16_operands(M, N, K, ta, tb):
     """bf16 operands in memory: within 1e-5 of the float64 product of the
