@@ -290,8 +290,11 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
   const int64_t row = i / g.N, col = i - row * g.N;
   float *dst = g.C + row * g.ldc + col;
   float v = g.accumulate ? *dst : 0.0f;
+  // loads issued ahead, adds in split order
   float part = 0.0f;
-  for (int z = 0; z < g.splits; ++z) part = part + g.ws[static_cast<int64_t>(z) * g.M * g.N + i];
+  const int64_t plane = g.M * g.N;
+#pragma unroll 8
+  for (int z = 0; z < g.splits; ++z) part = part + g.ws[z * plane + i];
   v = v + part;
   if (g.bias != nullptr) v = v + g.bias[col];
   *dst = v;
