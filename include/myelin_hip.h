@@ -61,6 +61,7 @@ typedef struct ihipStream_t *myelin_stream_t;
 #define MYELIN_DT_I32 4
 #define MYELIN_DT_I64 5
 #define MYELIN_DT_F64 6
+#define MYELIN_DT_BITS 7 /* packed spike bits: int32 words, bit i of word w = column 32w + i */
 
 const char *myelin_last_error(void);
 int myelin_abi_version(void);
@@ -209,6 +210,10 @@ int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C,
  * always on 128 x 128 tiles; k-contiguous operand rows 16-byte aligned,
  * mn-contiguous ones 8-byte aligned).  bf16 operands give bit-identical
  * results to fp32 operands holding the same values, at half the bytes.
+ * a_dtype = MYELIN_DT_BITS with b_dtype = MYELIN_DT_F32: A is packed spike
+ * bits in myelin_pack's format (lda counts int32 words: A(m,k) is bit k of
+ * row m, or with trans_a bit m of row k), expanded to 0/1 on load on
+ * 64 x 64 tiles -- bit-identical to the unpacked float32 A on those tiles.
  * Replaces: as myelin_gemm_f32.
  */
 int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype,

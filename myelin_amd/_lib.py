@@ -21,6 +21,7 @@ OK, EINVAL, EHIP = 0, 1, 2
 RULE_THRESHOLD, RULE_SURROGATE = 0, 1
 SG_NONE = 6
 PREC = {"fp32": 0, "bf16": 1}
+DT_BITS = 7  # packed spike bits (int32 words) as a GEMM operand
 DT = {
     torch.float32: 0,
     torch.float16: 1,

@@ -184,6 +184,82 @@ struct TileLoader {
   }
 };
 
+// An operand held as packed spike bits (bit i of word w = column 32w + i,
+// the format of myelin_pack), expanded to exact 0/1 on load; same interface
+// as TileLoader.  KCONTIG: element (row, k) is bit k of the row's words.
+// Otherwise (rows along mn): element (mn, k) is bit mn of row k's words
+// (word k*ld + mn/32).  A piece's 4 elements never straddle a word.
+template <int PREC, bool KCONTIG>
+struct BitLoader {
+  static constexpr int KS = Prec<PREC>::KS;
+  static constexpr int NV = KS * kTile / 1024;
+  const int32_t *base[NV];
+  int koff[NV], roff[NV], nvalid[NV], sh[NV];
+  int64_t ld;
+  float v[NV][4];
+
+  __device__ __forceinline__ void map_kcontig(int tid) {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int idx = e * 256 + tid;
+      roff[e] = idx / (KS / 4);
+      koff[e] = 4 * (idx % (KS / 4));
+      nvalid[e] = 4;
+      sh[e] = 0;
+    }
+  }
+  __device__ __forceinline__ void map_rowcontig(int tid, const int32_t *ptr, int64_t row0, int64_t rows,
+                                                int64_t ld_) {
+    ld = ld_;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int idx = e * 256 + tid;
+      koff[e] = idx / 16;
+      roff[e] = 4 * (idx % 16);
+      const int64_t left = rows - (row0 + roff[e]);
+      nvalid[e] = left <= 0 ? 0 : (left >= 4 ? 4 : static_cast<int>(left));
+      base[e] = ptr + (row0 + roff[e]) / 32;
+      sh[e] = static_cast<int>((row0 + roff[e]) % 32);
+    }
+  }
+
+  __device__ __forceinline__ void load(int64_t k0, int64_t kend) {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      uint32_t bits = 0;
+      int n = 0;
+      if constexpr (KCONTIG) {
+        const int64_t k = k0 + koff[e];
+        if (base[e] != nullptr && k < kend) {
+          bits = static_cast<uint32_t>(base[e][k >> 5]) >> (k & 31);
+          n = kend - k >= 4 ? 4 : static_cast<int>(kend - k);
+        }
+      } else {
+        const int64_t k = k0 + koff[e];
+        if (k < kend && nvalid[e] > 0) {
+          bits = static_cast<uint32_t>(base[e][k * ld]) >> sh[e];
+          n = nvalid[e];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[e][i] = (i < n && ((bits >> i) & 1u)) ? 1.0f : 0.0f;
+    }
+  }
+
+  __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[Stage<PREC>::LD]) const {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (KCONTIG)
+          dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
+        else
+          dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+      }
+    }
+  }
+};
+
 // acc += A[64 x (kb..ke)] B[(kb..ke) x 64], software-pipelined: the next
 // stage's global loads are in flight while the current stage runs on MFMA
 // from the other LDS buffer (one barrier per stage).
@@ -231,7 +307,8 @@ struct GemmArgs {
   int accumulate, splits;
 };
 
-template <int PREC, bool TA, bool TB, bool VA, bool VB>
+// PA: A holds packed spike bits (lda in words), read by BitLoader.
+template <int PREC, bool TA, bool TB, bool VA, bool VB, bool PA>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   __shared__ Stage<PREC> st[2];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
@@ -239,15 +316,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int64_t kb = static_cast<int64_t>(blockIdx.z) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
-  TileLoader<PREC, !TA, VA> la;
+  using SA = typename std::conditional<PA, int32_t, float>::type;
+  typename std::conditional<PA, BitLoader<PREC, !TA>, TileLoader<PREC, !TA, VA>>::type la;
   if constexpr (TA) {
-    la.map_rowcontig(tid, static_cast<const float *>(g.A), m0, g.M, g.lda);
+    la.map_rowcontig(tid, static_cast<const SA *>(g.A), m0, g.M, g.lda);
   } else {
     la.map_kcontig(tid);
 #pragma unroll
     for (int e = 0; e < TileLoader<PREC, true, VA>::NV; ++e) {
       const int64_t m = m0 + la.roff[e];
-      la.base[e] = m < g.M ? static_cast<const float *>(g.A) + m * g.lda : nullptr;
+      la.base[e] = m < g.M ? static_cast<const SA *>(g.A) + m * g.lda : nullptr;
     }
   }
   TileLoader<PREC, TB, VB> lb;
@@ -1317,16 +1395,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool al16(const void *q) { return q == nullptr || myelin::aligned(q, 16); }
 
-template <int PREC, bool VA, bool VB>
+template <int PREC, bool VA, bool VB, bool PA = false>
 void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
   if (!ta && !tb)
-    gemm_kernel<PREC, false, false, VA, VB><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, false, VA, VB, PA><<<grid, dim3(256), 0, s>>>(g);
   else if (!ta && tb)
-    gemm_kernel<PREC, false, true, VA, VB><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, false, true, VA, VB, PA><<<grid, dim3(256), 0, s>>>(g);
   else if (ta && !tb)
-    gemm_kernel<PREC, true, false, VA, VB><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, true, false, VA, VB, PA><<<grid, dim3(256), 0, s>>>(g);
   else
-    gemm_kernel<PREC, true, true, VA, VB><<<grid, dim3(256), 0, s>>>(g);
+    gemm_kernel<PREC, true, true, VA, VB, PA><<<grid, dim3(256), 0, s>>>(g);
 }
 
 // K splits for an output of `tiles` workgroups: split when the output alone
@@ -1382,9 +1460,9 @@ void launch_big_t(const GemmArgs &g, int ta, int tb, bool half, dim3 grid, hipSt
 }
 
 template <int PREC>
-int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s) {
+int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s, bool bits = false) {
   constexpr int KS = Prec<PREC>::KS;
-  const bool big = half || use_big(g);
+  const bool big = !bits && (half || use_big(g));
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
   if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
@@ -1401,7 +1479,12 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     const dim3 grid(cdiv(g.N, kTile), cdiv(g.M, kTile), static_cast<unsigned>(splits));
     // 16-byte loads per operand where its base and leading dimension allow
     const bool va = al16(g.A) && g.lda % 4 == 0, vb = al16(g.B) && g.ldb % 4 == 0;
-    if (va && vb)
+    if (bits) {
+      if (vb)
+        launch_gemm_v<PREC, false, true, true>(g, ta, tb, grid, s);
+      else
+        launch_gemm_v<PREC, false, false, true>(g, ta, tb, grid, s);
+    } else if (va && vb)
       launch_gemm_v<PREC, true, true>(g, ta, tb, grid, s);
     else if (va)
       launch_gemm_v<PREC, true, false>(g, ta, tb, grid, s);
@@ -1472,12 +1555,19 @@ extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtyp
   if (M == 0 || N == 0) return MYELIN_OK;
   if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm: null pointer");
   if (ldc < N) return myelin::invalid("gemm: ldc < N");
-  if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N)) return myelin::invalid("gemm: bad leading dim");
+  if ((a_dtype != MYELIN_DT_BITS && (trans_a ? lda < M : lda < K)) || (trans_b ? ldb < K : ldb < N))
+    return myelin::invalid("gemm: bad leading dim");
   if (workspace_elems < 0) return myelin::invalid("gemm: negative workspace size");
   if (precision != MYELIN_PREC_BF16 && precision != MYELIN_PREC_F32)
     return myelin::invalid("gemm: unknown precision %d", precision);
-  if ((a_dtype != MYELIN_DT_F32 && a_dtype != MYELIN_DT_BF16) || b_dtype != a_dtype)
-    return myelin::invalid("gemm: operands must both be float32 or both bfloat16");
+  const bool bits = a_dtype == MYELIN_DT_BITS;
+  if (bits) {
+    if (b_dtype != MYELIN_DT_F32) return myelin::invalid("gemm: packed-bit A needs a float32 B");
+    if (trans_a ? lda < (M + 31) / 32 : lda < (K + 31) / 32)
+      return myelin::invalid("gemm: packed-bit A: lda (words per row) too small");
+  } else if ((a_dtype != MYELIN_DT_F32 && a_dtype != MYELIN_DT_BF16) || b_dtype != a_dtype) {
+    return myelin::invalid("gemm: operands must both be float32 or both bfloat16 (or packed-bit A, float32 B)");
+  }
   const bool half = a_dtype == MYELIN_DT_BF16;
   if (half) {
     if (precision != MYELIN_PREC_BF16) return myelin::invalid("gemm: bfloat16 operands need bf16 precision");
@@ -1491,8 +1581,8 @@ extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtyp
     return myelin::launched("gemm (K = 0)");
   }
   hipStream_t s = myelin::as_hip(stream);
-  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s);
-  return launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s);
+  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s, bits);
+  return launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s, bits);
 }
 
 extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,

@@ -32,12 +32,14 @@ import torch
 from myelin_amd import _lib
 
 
-def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None):
-    """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16."""
+def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None, a_bits=False):
+    """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16, or
+    (``a_bits``) A packed spike words (int32, lda in words) with B float32."""
 
     n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec)
     ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
-    _lib.call("myelin_gemm", _lib.ptr(A), _lib.DT[A.dtype], _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
+    a_dt = _lib.DT_BITS if a_bits else _lib.DT[A.dtype]
+    _lib.call("myelin_gemm", _lib.ptr(A), a_dt, _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
               _lib.ptr(C), M, N, K, lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws),
               n_ws, stream)
 
@@ -158,7 +160,12 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     dev = x.device
     step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
     cur = torch.empty((step, B, N), dtype=torch.float32, device=dev)
-    state = torch.zeros((B, N), dtype=torch.float32, device=dev) if m0 is None else m0.clone()
+    # the membrane carried across chunks lives in m_final (each lane reads
+    # its m0 before writing, so m0 may be m_final); a single chunk needs no
+    # carry buffer at all
+    state = m_final
+    if state is None and step < t1 - t0:
+        state = torch.empty((B, N), dtype=torch.float32, device=dev)
     counts = torch.zeros((B, N), dtype=torch.float32, device=dev) if rates is not None else None
     for c0 in range(t0, t1, step):
         c1 = min(c0 + step, t1)
@@ -170,12 +177,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
         last = c1 == t1
         _lib.call(
             "myelin_lif_currents_fwd",
-            _lib.ptr(cur), _lib.ptr(state), _lib.ptr(state), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
-            _lib.ptr(rates) if last else None, _lib.ptr(counts), _lib.ptr(ckpt), T, B, N, c0, c1, t0, t0,
-            ckpt_every, decay, threshold, reset, slope, rule, stream,
+            _lib.ptr(cur), _lib.ptr(m0 if c0 == t0 else state), _lib.ptr(state), _lib.ptr(spikes), _lib.ptr(pre),
+            _lib.ptr(packed), _lib.ptr(rates) if last else None, _lib.ptr(counts), _lib.ptr(ckpt), T, B, N, c0, c1,
+            t0, t0, ckpt_every, decay, threshold, reset, slope, rule, stream,
         )
-    if m_final is not None:
-        m_final.copy_(state)
 
 
 class HipLinearLIFFunction(torch.autograd.Function):

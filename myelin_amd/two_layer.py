@@ -11,21 +11,25 @@ hidden-spike gradient.
 
 Here both passes walk time in chunks of C steps (the checkpoint size):
 
-* forward, chunk k: hidden ``x_t @ W_h`` + LIF from the carried hidden
-  membrane -> hidden spikes of the chunk ``[C, B, H]`` (and, packed variant,
-  their words ``[T, B, ceil(H/32)]``); readout ``s_t @ W_o`` + LIF from the
-  carried readout membrane and spike counts.  Chunk-start membranes of both
-  layers are kept ``[ceil(T/C), B, H + O]``.
+* forward, a group of chunks at a time (as many as keep the group's hidden
+  currents within 2**25 elements): hidden ``x_t @ W_h`` + LIF from the
+  carried hidden membrane -> hidden spikes of the group (dense, or in the
+  packed variant only their words ``[T, B, ceil(H/32)]``); readout
+  ``s_t @ W_o`` + LIF from the carried readout membrane and spike counts.
+  Chunk-start membranes of both layers are kept ``[ceil(T/C), B, H + O]``.
 * backward, chunks in reverse: recompute the hidden chunk (pre-reset trace;
-  its spikes, or the unpacked words of the packed variant, feed the readout),
+  its spikes, or in the packed variant the stored words read as bits by
+  the readout GEMMs, feed the readout),
   recompute the readout chunk, reverse the readout recurrence (adjoint
   carried across chunks), ``dS = G_o @ W_o^T`` for the chunk only, then
   reverse the hidden recurrence with ``dS`` as its spike gradient.
 
 So no tensor with T in its shape is written except the input gradient and,
-in the packed variant, the packed words.  The arithmetic of each step is
-that of the one-layer checkpointed path (same kernels), so rates and
-gradients equal those of composing the two one-layer functions.
+in the packed variant, the packed words -- which its readout GEMMs read
+directly, so that variant never forms dense hidden spikes at all.  The
+arithmetic of each step is that of the one-layer checkpointed path (same
+kernels), so rates and gradients equal those of composing the two
+one-layer functions.
 """
 
 from __future__ import annotations
@@ -36,18 +40,23 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import _cast_bf16, _gemm, _half, _lif_fwd, _transpose_bf16
+from myelin_amd.linear import _CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _lif_fwd, _transpose_bf16
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
                    slope, prec, stream):
     """Readout currents ``hs @ W_o + b_o`` for steps [t0, t1) then the LIF
-    recurrence over them in absolute time (counts and rates over all T)."""
+    recurrence over them in absolute time (counts and rates over all T).
+    ``hs`` is the chunk's hidden spikes, dense fp32 ``[L, B, H]`` or packed
+    words ``[L, B, ceil(H/32)]`` int32 (read as bits by the GEMM)."""
 
     B, O = m0.shape
     H = wo.shape[0]
     L = t1 - t0
-    _gemm(hs, wo, cur, L * B, O, H, H, O, O, False, False, False, prec, stream, bias=bo)
+    if hs.dtype == torch.int32:
+        _gemm(hs, wo, cur, L * B, O, H, hs.shape[-1], O, O, False, False, False, prec, stream, bias=bo, a_bits=True)
+    else:
+        _gemm(hs, wo, cur, L * B, O, H, H, O, O, False, False, False, prec, stream, bias=bo)
     _lib.call(
         "myelin_lif_currents_fwd",
         _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(m_final), None, _lib.ptr(pre), None, _lib.ptr(rates),
@@ -75,20 +84,29 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         m_o = torch.zeros((B, O), device=dev)
         counts = torch.zeros((B, O), device=dev)
         rates = torch.empty((B, O), device=dev)
-        hs = torch.empty((L0, B, H), device=dev)
-        cur = torch.empty((L0, B, O), device=dev)
+        # the forward has no per-chunk state to keep beyond the checkpoints,
+        # so it runs whole groups of chunks: a group's hidden currents fill
+        # up to 2**25 elements, as in the one-layer chunked path
+        G = max(1, min(K, _CURRENT_CHUNK_ELEMS // (L0 * B * H)))
+        LG = min(G * C, T)
+        # the packed variant never forms dense hidden spikes: its readout
+        # GEMM reads the words
+        hs = None if packed_hidden else torch.empty((LG, B, H), device=dev)
+        cur = torch.empty((LG, B, O), device=dev)
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(wh, stream)) if half else (x, None)
-        for k in range(K):
+        for k in range(0, K, G):
             t0 = k * C
-            t1 = min(t0 + C, T)
+            t1 = min(t0 + G * C, T)
             L = t1 - t0
             _lif_fwd(xs[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
-                     m_final=m_h, spikes=hs[:L], packed=None if words is None else words[t0:t1],
-                     ckpt=None if ck_h is None else ck_h[k], ckpt_every=L, wt=wt)
-            _readout_chunk(cur[:L], hs[:L], wo, bo, m_o, m_o, None, counts, rates if t1 == T else None, ck_o, T,
+                     m_final=m_h, spikes=None if hs is None else hs[:L],
+                     packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
+                     ckpt_every=C, wt=wt)
+            s_in = words[t0:t1] if hs is None else hs[:L]
+            _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None, counts, rates if t1 == T else None, ck_o, T,
                            t0, t1, C, decay, threshold, reset, slope, prec, stream)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
@@ -123,7 +141,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gwo = torch.zeros_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
-            hs = torch.empty((L0, B, H), device=dev)
+            hs = None if words is not None else torch.empty((L0, B, H), device=dev)
             pre_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
             cur = torch.empty((L0, B, O), device=dev)
             pre_o = torch.empty((L0, B, O), device=dev)
@@ -137,15 +155,15 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 L = t1 - t0
                 rows = L * B
                 if words is not None:
-                    _lib.call("myelin_unpack", _lib.ptr(words[t0:t1]), _lib.ptr(hs), _lib.DT[torch.float32],
-                              rows, H, stream)
+                    s_in = words[t0:t1]
                     if need_hidden:
                         _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
                                  _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L], wt=wt)
                 else:
+                    s_in = hs[:L]
                     _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
                              prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt)
-                _readout_chunk(cur[:L], hs[:L], wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
+                _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
                                decay, threshold, reset, slope, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
@@ -154,8 +172,12 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
                 if gwo is not None:
-                    # dW_o += S[t0:t1]^T @ G_o
-                    _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, True, prec, stream)
+                    # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
+                    if words is not None:
+                        _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, True, prec, stream,
+                              a_bits=True)
+                    else:
+                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, True, prec, stream)
                 if not need_hidden:
                     continue
                 # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this chunk

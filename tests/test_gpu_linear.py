@@ -387,3 +387,49 @@ def test_fused_forward_bf16_operands_match_fp32_operands(T, B, F, N):
         res.append((m.cpu(), s.cpu(), pre.cpu()))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (70, 33, 100), (300, 17, 784), (64, 100, 33), (100, 300, 500),
+                                   (1000, 100, 2048), (4096, 20, 6400)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_gemm_packed_bit_operand_equals_dense(M, N, K, ta, tb, prec):
+    """A given as packed spike words (the readout input of the packed-hidden
+    network) gives the same bits as the same 0/1 matrix given densely: both
+    run the 64 x 64 kernel (outputs narrower than 128) with the same k order
+    and the same K split, and 0/1 is exact in either MFMA input type."""
+
+    _print_case(test="gemm_bits", M=M, N=N, K=K, ta=ta, tb=tb, prec=prec)
+    g = seeded(M + 3 * N + 5 * K)
+    A = (torch.rand((K, M) if ta else (M, K), generator=g) < 0.2).float()
+    B = torch.randn((N, K) if tb else (K, N), generator=g)
+    bias = torch.randn(N, generator=g).to(DEV)
+    Ad, Bd = A.to(DEV), B.to(DEV)
+    words = myelin.pack_spikes(Ad).data
+    # a word array with slack columns: lda is the row pitch in words
+    wide = torch.full((words.shape[0], words.shape[1] + 3), -1, dtype=torch.int32, device=DEV)
+    wide[:, :words.shape[1]] = words
+    stream = _lib.stream(torch.device(DEV))
+    C0 = torch.randn(M, N, generator=g).to(DEV)
+    for acc in (False, True):
+        dense, bits, bits_wide = C0.clone(), C0.clone(), C0.clone()
+        args = (M, N, K)
+        _gemm(Ad, Bd, dense, *args, A.shape[1], B.shape[1], N, ta, tb, acc, _lib.PREC[prec], stream, bias=bias)
+        _gemm(words, Bd, bits, *args, words.shape[1], B.shape[1], N, ta, tb, acc, _lib.PREC[prec], stream,
+              bias=bias, a_bits=True)
+        _gemm(wide, Bd, bits_wide, *args, wide.shape[1], B.shape[1], N, ta, tb, acc, _lib.PREC[prec], stream,
+              bias=bias, a_bits=True)
+        assert torch.equal(bits, dense)
+        assert torch.equal(bits_wide, dense)
+
+
+def test_gemm_packed_bit_operand_checks():
+    stream = _lib.stream(torch.device(DEV))
+    words = torch.zeros(16, 2, dtype=torch.int32, device=DEV)
+    B = torch.zeros(40, 8, device=DEV)
+    C = torch.empty(16, 8, device=DEV)
+    with pytest.raises(ValueError, match="words per row"):
+        _gemm(words, B, C, 16, 8, 40, 1, 8, 8, False, False, False, _lib.PREC["fp32"], stream, a_bits=True)
+    with pytest.raises(ValueError, match="float32 B"):
+        _gemm(words, B.to(torch.bfloat16), C, 16, 8, 40, 2, 8, 8, False, False, False, _lib.PREC["bf16"], stream,
+              a_bits=True)

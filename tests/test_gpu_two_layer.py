@@ -5,8 +5,10 @@ Bars (as for the one-layer linear paths): readout rates equal to the
 reference's when the rasters agree (rates are counts / T), gradients within
 1e-4 max-norm relative of the reference's (the MFMA GEMM sums in another
 order than the CPU matmul; the reference's own packed-vs-dense test uses
-atol 1e-4 / rtol 1e-3, tests/test_triton_lif.py:2500-2504).  The two
-variants run the same arithmetic, so they must agree bit for bit.
+atol 1e-4 / rtol 1e-3, tests/test_triton_lif.py:2500-2504).  The packed
+variant's readout GEMMs read the hidden spikes as packed bits; for readouts
+narrower than 128 neurons both variants run the same GEMM kernel and K
+split, so they must agree bit for bit (wider: within 1e-5).
 """
 
 from __future__ import annotations
@@ -80,8 +82,10 @@ def _random_net(seed, T, B, F, H, O):
 
 
 # (T, B, F, H, O): ragged word edges, a hidden layer on the fused kernel
-# (B x H fills >= 1024 workgroups) and one on the GEMM + recurrence route
-SHAPES = [(13, 3, 20, 37, 5), (29, 6, 70, 100, 20), (5, 256, 32, 2048, 10)]
+# (B x H fills >= 1024 workgroups), one on the GEMM + recurrence route, and
+# a readout of 128+ neurons (the dense variant's readout GEMMs then take the
+# 128 x 128 kernel, whose K split differs from the packed variant's)
+SHAPES = [(13, 3, 20, 37, 5), (29, 6, 70, 100, 20), (5, 256, 32, 2048, 10), (9, 32, 40, 300, 130)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -95,8 +99,15 @@ def test_two_layer_matches_oracle_and_variants_agree(shape):
         r, leaves = _run(fn, tensors, True, p, surrogate="fast_sigmoid", surrogate_slope=5.0, checkpoint_size=4)
         r.backward(grate.to(DEV))
         out[name] = [to_np(r)] + _grads(leaves)
-    for a, b in zip(out["recompute"], out["packed"]):
-        assert np.array_equal(a, b)
+    if O < 128:
+        # same GEMM kernel and K split for words and dense spikes
+        for a, b in zip(out["recompute"], out["packed"]):
+            assert np.array_equal(a, b)
+    else:
+        assert np.abs(out["recompute"][0] - out["packed"][0]).max() <= 1.0 / T + 1e-7
+        if np.array_equal(out["recompute"][0], out["packed"][0]):
+            for name, a, b in zip(("x", "wh", "bh", "wo", "bo"), out["recompute"][1:], out["packed"][1:]):
+                assert_norm_close(a, b, 1e-5, f"packed vs recompute grad_{name}")
     leaves = [t.clone().requires_grad_() for t in tensors]
     rr = R.two_layer_rate(*leaves, 8.0, 0.7, -0.2, "fast_sigmoid", 5.0, 4)
     rr.backward(grate)
