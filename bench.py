@@ -188,18 +188,25 @@ def _workload_lif_fwd(torch, myelin, args):
     stream = _lib.stream(dev)
     m_final = torch.empty(Bl, Nl, device=dev)
     spikes = torch.empty(Tl, Bl, Nl, device=dev)
-    reps = max(args.steps, 8)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
-    for i in range(-2, reps):
-        if i >= 0:
-            ev[2 * i].record()
+    # one event pair around back-to-back launches: a pair around each launch
+    # would also time the host's launch latency while the GPU sits idle
+    reps = max(args.steps, 8) * 8
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def launch(i):
         _lib.call("myelin_lif_fwd_f32", xs[i % 8].data_ptr(), m0.membrane.data_ptr(), m_final.data_ptr(),
                   spikes.data_ptr(), None, None, Tl, Bl, Nl, p.decay, p.threshold, p.reset, 0.0,
                   _lib.RULE_THRESHOLD, 1, stream)
-        if i >= 0:
-            ev[2 * i + 1].record()
+
+    for i in range(8):
+        launch(i)
     torch.cuda.synchronize()
-    kern_ms = sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
+    ev0.record()
+    for i in range(reps):
+        launch(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    kern_ms = ev0.elapsed_time(ev1) / reps
     # algorithmic bytes: read x, write spikes (8 B per neuron-step) + m0 in, m_final out
     nbytes = 8 * E + 8 * Bl * Nl
     gbps = nbytes / (kern_ms * 1e-3) / 1e9

@@ -241,13 +241,15 @@ __global__ __launch_bounds__(256) void fill_i64(int64_t *__restrict__ p, int64_t
 
 // Per-neuron counts over R leading rows: words [R, K, W] -> out [K, n].
 // Block = 8 waves x 64 word-columns; wave q walks rows r = q, q+8, ...
-// inside the block's row range.  Bit counts are accumulated SWAR-style:
-// acc[j] holds, in its 4 bytes, the counts of bits j, j+8, j+16, j+24, and
-// is flushed into 32-bit counters every 255 rows.  The 8 waves are then
-// reduced through LDS; a block covering all R rows stores, otherwise it
-// atomically adds (out zeroed).
+// inside the block's row range, 16 rows' loads issued before any is used.
+// Bit counts are accumulated SWAR-style: acc[j] holds, in its 4 bytes, the
+// counts of bits j, j+8, j+16, j+24.  A block spans at most 8 * 255 rows,
+// so no byte passes 255 before the wave's counts are unpacked.  The 8
+// waves are then reduced through LDS; a block covering all R rows stores,
+// otherwise it atomically adds (out zeroed).
 constexpr int kKeepWaves = 8;
-constexpr int kKeepRows = 2040;  // rows per block (multiple of 8 * 255)
+constexpr int kKeepRows = kKeepWaves * 255;  // rows per block
+constexpr int kKeepAhead = 16;               // row loads in flight per lane
 
 __global__ __launch_bounds__(512) void keep_last_counts(const int32_t *__restrict__ words, int64_t R, int64_t KW,
                                                         int64_t W, int64_t n, int64_t *__restrict__ out,
@@ -261,32 +263,31 @@ __global__ __launch_bounds__(512) void keep_last_counts(const int32_t *__restric
   const int64_t r_end = (r_begin + kKeepRows < R) ? r_begin + kKeepRows : R;
 
   int32_t cnt[32];
-#pragma unroll
-  for (int b = 0; b < 32; ++b) cnt[b] = 0;
   uint32_t acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0;
-  int pending = 0;
   if (active) {
-    for (int64_t r = r_begin + q; r < r_end; r += kKeepWaves) {
-      const uint32_t w = static_cast<uint32_t>(words[r * KW + col]);
+    const int32_t *p = words + col;
+    int64_t r = r_begin + q;
+    for (; r + (kKeepAhead - 1) * kKeepWaves < r_end; r += kKeepAhead * kKeepWaves) {
+      uint32_t w[kKeepAhead];
+#pragma unroll
+      for (int u = 0; u < kKeepAhead; ++u) w[u] = static_cast<uint32_t>(p[(r + u * kKeepWaves) * KW]);
+#pragma unroll
+      for (int u = 0; u < kKeepAhead; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += (w[u] >> j) & 0x01010101u;
+    }
+    for (; r < r_end; r += kKeepWaves) {
+      const uint32_t w = static_cast<uint32_t>(p[r * KW]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] += (w >> j) & 0x01010101u;
-      if (++pending == 255) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-#pragma unroll
-          for (int y = 0; y < 4; ++y) cnt[8 * y + j] += (acc[j] >> (8 * y)) & 0xffu;
-          acc[j] = 0;
-        }
-        pending = 0;
-      }
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int y = 0; y < 4; ++y) cnt[8 * y + j] += (acc[j] >> (8 * y)) & 0xffu;
   }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) cnt[8 * y + j] = static_cast<int32_t>((acc[j] >> (8 * y)) & 0xffu);
   if (q > 0) {
 #pragma unroll
     for (int b = 0; b < 32; ++b) red[q - 1][b][lane] = cnt[b];
