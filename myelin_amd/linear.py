@@ -133,7 +133,7 @@ def _fused_grid(B: int, N: int) -> int:
 
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
-             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None):
+             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, cur_out=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
@@ -144,12 +144,14 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     when narrow) writes ``x_t @ W + b`` for the chunk, then the recurrence
     kernel consumes it, carrying the membrane and the spike counts across
     chunks.  ``pre`` is indexed from t0; checkpoint rows from t0.
+    ``cur_out`` (``[t1 - t0, B, N]``, chunked route only) receives all the
+    currents, for a backward that reuses them instead of recomputing.
     """
 
     T, B, F = x.shape
     half = x.dtype == torch.bfloat16
     N = wt.shape[0] if half else w.shape[1]
-    if N >= 64 and _fused_grid(B, N) >= 1024:
+    if cur_out is None and N >= 64 and _fused_grid(B, N) >= 1024:
         outs = (_lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
                 _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule)
         if half:
@@ -158,8 +160,11 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
             _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *outs, prec, stream)
         return
     dev = x.device
-    step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
-    cur = torch.empty((step, B, N), dtype=torch.float32, device=dev)
+    if cur_out is not None:
+        step, cur = t1 - t0, cur_out
+    else:
+        step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
+        cur = torch.empty((step, B, N), dtype=torch.float32, device=dev)
     # the membrane carried across chunks lives in m_final (each lane reads
     # its m0 before writing, so m0 may be m_final); a single chunk needs no
     # carry buffer at all
@@ -183,6 +188,27 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
         )
 
 
+def _keep_currents(F: int, N: int) -> bool:
+    """A checkpointed layer keeps its forward currents ``[T, B, N]`` (and its
+    backward runs only the recurrence from them, no synapse GEMM) when they
+    are narrow: at most 32 neurons and at most 1/8 of the saved input's
+    bytes -- the readout layers, whose recompute GEMM would re-read the whole
+    input to rebuild a few columns."""
+
+    return N <= 32 and 8 * N <= F
+
+
+def _recompute_pre(cur, m0, pre, T, B, N, t0, t1, decay, threshold, reset, slope, rule, stream):
+    """Pre-reset trace of steps [t0, t1) from saved currents (row 0 = step t0)
+    and the chunk-start membrane ``m0``; ``pre`` rows from t0."""
+
+    _lib.call(
+        "myelin_lif_currents_fwd",
+        _lib.ptr(cur), _lib.ptr(m0), None, None, _lib.ptr(pre), None, None, None, None, T, B, N, t0, t1, t0, t0, 1,
+        decay, threshold, reset, slope, rule, stream,
+    )
+
+
 class HipLinearLIFFunction(torch.autograd.Function):
     """Outputs ``(final_membrane, spikes)`` or, with ``rate=True``,
     ``(final_membrane, rates)`` where ``rates = spike_count / T``."""
@@ -198,20 +224,22 @@ class HipLinearLIFFunction(torch.autograd.Function):
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
-        pre = ckpt = None
+        pre = ckpt = cur = None
         if need:
             if checkpoint is None:
                 pre = torch.empty((T, B, N), dtype=x.dtype, device=dev)
             else:
                 ckpt = torch.empty((math.ceil(T / checkpoint), B, N), dtype=x.dtype, device=dev)
+                if _keep_currents(F, N):
+                    cur = torch.empty((T, B, N), dtype=torch.float32, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1, wt=wt)
+                 ckpt_every=checkpoint or 1, wt=wt, cur_out=cur)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:
             # the bf16 synapse keeps the bf16 copies of x and W^T (what its GEMMs read)
-            ctx.save_for_backward(xs, w, b, pre, ckpt, wt)
+            ctx.save_for_backward(xs, w, b, pre, ckpt, wt, cur)
         return m_final, out
 
     @staticmethod
@@ -220,19 +248,20 @@ class HipLinearLIFFunction(torch.autograd.Function):
         if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
             return none
         decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
-        xs, w, b, pre, ckpt, wt = ctx.saved_tensors
+        xs, w, b, pre, ckpt, wt, cur = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
         gx, gw, gb = linear_backward(xs, w, b if has_b else None, pre, ckpt, wt, g_m, g_out, decay, threshold,
                                      reset, sid, slope, checkpoint, rate, prec, rule, need_x, need_w,
-                                     need_b and has_b)
+                                     need_b and has_b, cur=cur)
         return gx, gw, gb, None, None, None, None, None, None, None, None, None
 
 
 def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset, sid, slope, checkpoint, rate,
-                    prec, rule, need_x=True, need_w=True, need_b=True):
+                    prec, rule, need_x=True, need_w=True, need_b=True, cur=None):
     """Gradients (dX, dW, db) of the streamed-synapse LIF, chunk by chunk in
     reverse time: recompute the chunk's pre-reset trace from its checkpoint
-    (``checkpoint=None``: the saved trace ``pre`` covers all T), reverse the
+    (``checkpoint=None``: the saved trace ``pre`` covers all T; ``cur``: the
+    forward's saved currents, so no recompute GEMM), reverse the
     recurrence into G = dL/dI, then ``dX = G W^T`` and ``dW += X^T G`` on
     the MFMA GEMM and ``db`` as a fixed-order column sum.  ``xs`` is fp32, or
     bf16 with ``wt = W^T`` bf16 for the bf16 synapse; ``g_out`` is dL/dspikes
@@ -263,6 +292,10 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             C = t1 - t0
             if checkpoint is None:
                 pre_k = pre
+            elif cur is not None:
+                _recompute_pre(cur[t0:t1], ckpt[k], scratch, T, B, N, t0, t1, decay, threshold, reset, slope, rule,
+                               stream)
+                pre_k = scratch
             else:
                 _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
                          pre=scratch, wt=wt)

@@ -20,13 +20,15 @@ Here both passes walk time in chunks of C steps (the checkpoint size):
 * backward, chunks in reverse: recompute the hidden chunk (pre-reset trace;
   its spikes, or in the packed variant the stored words read as bits by
   the readout GEMMs, feed the readout),
-  recompute the readout chunk, reverse the readout recurrence (adjoint
+  recompute the readout chunk (from its saved currents when the readout is
+  narrow), reverse the readout recurrence (adjoint
   carried across chunks), ``dS = G_o @ W_o^T`` for the chunk only, then
   reverse the hidden recurrence with ``dS`` as its spike gradient.
 
-So no tensor with T in its shape is written except the input gradient and,
-in the packed variant, the packed words -- which its readout GEMMs read
-directly, so that variant never forms dense hidden spikes at all.  The
+So no tensor with T in its shape is written except the input gradient, the
+narrow readout's currents ``[T, B, O]`` and, in the packed variant, the
+packed words -- which its readout GEMMs read directly, so that variant
+never forms dense hidden spikes at all.  The
 arithmetic of each step is that of the one-layer checkpointed path (same
 kernels), so rates and gradients equal those of composing the two
 one-layer functions.
@@ -40,7 +42,8 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import _CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _lif_fwd, _transpose_bf16
+from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _keep_currents, _lif_fwd,
+                               _recompute_pre, _transpose_bf16)
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
@@ -92,7 +95,10 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         # the packed variant never forms dense hidden spikes: its readout
         # GEMM reads the words
         hs = None if packed_hidden else torch.empty((LG, B, H), device=dev)
-        cur = torch.empty((LG, B, O), device=dev)
+        # a narrow readout keeps all its currents [T, B, O] for the backward
+        # (no readout recompute GEMM there)
+        keep = need and _keep_currents(H, O)
+        cur = torch.empty((T if keep else LG, B, O), device=dev)
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
@@ -106,12 +112,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                      packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
                      ckpt_every=C, wt=wt)
             s_in = words[t0:t1] if hs is None else hs[:L]
-            _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None, counts, rates if t1 == T else None, ck_o, T,
-                           t0, t1, C, decay, threshold, reset, slope, prec, stream)
+            _readout_chunk(cur[t0:t1] if keep else cur[:L], s_in, wo, bo, m_o, m_o, None, counts,
+                           rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
+                           stream)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
         if need:
-            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt)
+            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, cur if keep else None)
         return rates
 
     @staticmethod
@@ -120,7 +127,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         if g_rates is None or not any(ctx.needs_input_grad[:5]):
             return none
         decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
-        xs, wh, bh, wo, bo, ck_h, ck_o, words, wt = ctx.saved_tensors
+        xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, cur_o = ctx.saved_tensors
         half = xs.dtype == torch.bfloat16
         need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
         need_hidden = need_x or need_wh or (need_bh and has_bh)
@@ -143,7 +150,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
             hs = None if words is not None else torch.empty((L0, B, H), device=dev)
             pre_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
-            cur = torch.empty((L0, B, O), device=dev)
+            cur = torch.empty((L0, B, O), device=dev) if cur_o is None else None
             pre_o = torch.empty((L0, B, O), device=dev)
             G_o = torch.empty((L0, B, O), device=dev)
             ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
@@ -163,8 +170,12 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     s_in = hs[:L]
                     _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
                              prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt)
-                _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
-                               decay, threshold, reset, slope, prec, stream)
+                if cur_o is not None:
+                    _recompute_pre(cur_o[t0:t1], ck_o[k], pre_o, T, B, O, t0, t1, decay, threshold, reset, slope,
+                                   _lib.RULE_THRESHOLD, stream)
+                else:
+                    _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
+                                   decay, threshold, reset, slope, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
                     _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
