@@ -307,6 +307,49 @@ struct GemmArgs {
   int accumulate, splits;
 };
 
+// Writes one wave's 32 x 32 accumulator tile (rows row0 + acc_row(r, lane),
+// column col): to plane `split` of the workspace when K is split, else
+// C (+)= acc (+ bias[col]) with the adds in that order.  The branches are
+// taken once per tile, and the bias and old C values are all loaded before
+// the first store, so no store waits behind a load (the vector memory
+// counter covers stores as well).
+__device__ __forceinline__ void store_acc(const GemmArgs &g, const f32x16 &acc, int64_t row0, int64_t col, int lane,
+                                          int64_t split) {
+  if (col >= g.N) return;
+  if (g.splits > 1) {
+    float *ws = g.ws + split * g.M * g.N + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + acc_row(r, lane);
+      if (row < g.M) ws[row * g.N] = acc[r];
+    }
+    return;
+  }
+  float *c = g.C + col;
+  if (!g.accumulate && g.bias == nullptr) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + acc_row(r, lane);
+      if (row < g.M) c[row * g.ldc] = acc[r];
+    }
+    return;
+  }
+  const float b = g.bias != nullptr ? g.bias[col] : 0.0f;
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = row0 + acc_row(r, lane);
+    v[r] = (g.accumulate && row < g.M) ? c[row * g.ldc] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = row0 + acc_row(r, lane);
+    float t = g.accumulate ? v[r] + acc[r] : acc[r];
+    if (g.bias != nullptr) t = t + b;
+    if (row < g.M) c[row * g.ldc] = t;
+  }
+}
+
 // PA: A holds packed spike bits (lda in words), read by BitLoader.
 template <int PREC, bool TA, bool TB, bool VA, bool VB, bool PA>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
@@ -345,21 +388,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
   tile_mma<PREC>(la, lb, kb, ke, st, wm, wn, lane, acc);
 
-  const int64_t col = n0 + 32 * wn + (lane & 31);
-  if (col >= g.N) return;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = m0 + 32 * wm + acc_row(r, lane);
-    if (row >= g.M) continue;
-    if (g.splits > 1) {
-      g.ws[(static_cast<int64_t>(blockIdx.z) * g.M + row) * g.N + col] = acc[r];
-    } else {
-      float *dst = g.C + row * g.ldc + col;
-      float v = g.accumulate ? *dst + acc[r] : acc[r];
-      if (g.bias != nullptr) v = v + g.bias[col];
-      *dst = v;
-    }
-  }
+  store_acc(g, acc, m0 + 32 * wm, n0 + 32 * wn + (lane & 31), lane, blockIdx.z);
 }
 
 __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
@@ -376,6 +405,363 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
   v = v + part;
   if (g.bias != nullptr) v = v + g.bias[col];
   *dst = v;
+}
+
+// ---------------------------------------------------------------------------
+// Narrow GEMMs for the readout layers: outputs at most 32 columns wide
+// (gemm_narrow: currents I = S W_o and dW_o = S^T G_o) or K at most 32
+// (gemm_smallk: dS = G_o W_o^T, on the vector ALUs, below).  gemm_narrow
+// streams the long operand A from global memory straight into MFMA
+// fragments -- it is read once, so it skips LDS -- with the narrow operand
+// in LDS.  Per-lane k layout of a group of 2*KG consecutive k:
+//   lane l holds k = k0 + KG * (l / 32) + [0, KG)       KG = 8 (bf16) | 4 (fp32)
+// bf16: one v_mfma_f32_32x32x16_bf16 per group; fp32: four
+// v_mfma_f32_32x32x2f32, the i-th taking element i of each lane (lanes < 32
+// give k0 + i, lanes >= 32 give k0 + 4 + i), the same k for A and B.
+// A(m, k) may be fp32 (TA: A[k*lda + m], else A[m*lda + k]) or packed spike
+// bits (PA: bit m%32 of word A[k*lda + m/32] with TA, else bit k%32 of word
+// A[m*lda + k/32]).
+// ---------------------------------------------------------------------------
+#ifndef MYELIN_NARROW_U
+#define MYELIN_NARROW_U 8  // A groups loaded per batch by the narrow kernel
+#endif
+#ifndef MYELIN_NARROW_WGS
+#define MYELIN_NARROW_WGS 512  // workgroups the narrow kernel's K splits aim for
+#endif
+#ifndef MYELIN_NARROW_KSUB0
+#define MYELIN_NARROW_KSUB0 256  // k per staged B sub-chunk, fp32
+#endif
+
+template <int PREC>
+struct Narrow;
+template <>
+struct Narrow<0> {
+  static constexpr int KG = 4, KSUB = MYELIN_NARROW_KSUB0, PAD = 4;
+};
+template <>
+struct Narrow<1> {
+  static constexpr int KG = 8, KSUB = 512, PAD = 8;
+};
+
+template <bool TA, bool PA>
+__device__ __forceinline__ float a_elem(const GemmArgs &g, int64_t m, int64_t k) {
+  if constexpr (PA) {
+    const int32_t *A = static_cast<const int32_t *>(g.A);
+    const uint32_t w = static_cast<uint32_t>(TA ? A[k * g.lda + (m >> 5)] : A[m * g.lda + (k >> 5)]);
+    return ((w >> (TA ? (m & 31) : (k & 31))) & 1u) ? 1.0f : 0.0f;
+  } else {
+    const float *A = static_cast<const float *>(g.A);
+    return TA ? A[k * g.lda + m] : A[m * g.lda + k];
+  }
+}
+
+template <bool TB>
+__device__ __forceinline__ float b_elem(const GemmArgs &g, int64_t k, int64_t n) {
+  const float *B = static_cast<const float *>(g.B);
+  return TB ? B[n * g.ldb + k] : B[k * g.ldb + n];
+}
+
+template <int PREC>
+struct BFrag;  // a lane's B fragment for one group
+template <>
+struct BFrag<0> {
+  using V = f4;
+};
+template <>
+struct BFrag<1> {
+  using V = bf16x8;
+};
+
+// One group: acc += A-fragment (KG fp32 values) x B-fragment.
+template <int PREC>
+__device__ __forceinline__ void group_mfma(const float *a, typename BFrag<PREC>::V bv, f32x16 &acc) {
+  if constexpr (PREC == 1) {
+    bf16x8 av;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) av[i] = static_cast<__bf16>(a[i]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[i], acc, 0, 0, 0);
+  }
+}
+
+// A lane's KG values of A for the group starting at k (row m).  FULL: the
+// whole group lies below kend (no guards); VA: 16-byte loads (k-contiguous
+// fp32 rows, aligned).
+template <int PREC, bool TA, bool PA, bool VA, bool FULL>
+__device__ __forceinline__ void load_group(const GemmArgs &g, int64_t m, int64_t k, int64_t kend, float *a) {
+  constexpr int KG = Narrow<PREC>::KG;
+  if constexpr (FULL && !TA && !PA && VA) {
+    const f4 *q = reinterpret_cast<const f4 *>(static_cast<const float *>(g.A) + m * g.lda + k);
+#pragma unroll
+    for (int v = 0; v < KG / 4; ++v) {
+      const f4 t = q[v];
+      a[4 * v] = t.x;
+      a[4 * v + 1] = t.y;
+      a[4 * v + 2] = t.z;
+      a[4 * v + 3] = t.w;
+    }
+  } else if constexpr (!TA && PA) {
+    // KG bits of one word (k is a multiple of KG, so they never straddle
+    // words); a group starting at or past kend reads nothing
+    const uint32_t w =
+        (FULL || k < kend) ? static_cast<uint32_t>(static_cast<const int32_t *>(g.A)[m * g.lda + (k >> 5)]) >> (k & 31)
+                           : 0u;
+#pragma unroll
+    for (int i = 0; i < KG; ++i) a[i] = ((FULL || k + i < kend) && ((w >> i) & 1u)) ? 1.0f : 0.0f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < KG; ++i) a[i] = (FULL || k + i < kend) ? a_elem<TA, PA>(g, m, k + i) : 0.0f;
+  }
+}
+
+template <int PREC>
+struct NarrowB {
+  static constexpr int LD = Narrow<PREC>::KSUB + Narrow<PREC>::PAD;
+  alignas(16) typename Prec<PREC>::T b[32][LD];
+};
+
+// Stages B(k, n) for k in [ks, ks + kpad), n < N into bs[n][k - ks] (zero
+// past klen; rows past N are never stored, so they stay unwritten).  The
+// elements are walked flat in memory order -- contiguous when ldb equals the
+// contiguous extent -- 8 loads issued before their LDS writes.
+template <int PREC, bool TB, int LD>
+__device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, int klen, int kpad, int N,
+                                               typename Prec<PREC>::T (*bs)[LD], int tid) {
+  constexpr int R = 8;
+  const float *B = static_cast<const float *>(g.B);
+  const int total = N * klen;
+  for (int e0 = tid; e0 < total; e0 += 256 * R) {
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int e = e0 + 256 * r;
+      e = e < total ? e : total - 1;  // clamped: every load in range
+      int n, kk;
+      if constexpr (TB) {
+        n = e / klen;
+        kk = e - n * klen;
+        v[r] = B[n * g.ldb + ks + kk];
+      } else {
+        kk = e / N;
+        n = e - kk * N;
+        v[r] = B[(ks + kk) * g.ldb + n];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = e0 + 256 * r;
+      if (e < total) {
+        int n, kk;
+        if constexpr (TB) {
+          n = e / klen;
+          kk = e - n * klen;
+        } else {
+          kk = e / N;
+          n = e - kk * N;
+        }
+        bs[n][kk] = cvt<PREC>(v[r]);
+      }
+    }
+  }
+  for (int e = tid; e < N * (kpad - klen); e += 256) {
+    const int n = e / (kpad - klen);
+    bs[n][klen + (e - n * (kpad - klen))] = cvt<PREC>(0.0f);
+  }
+}
+
+// C[M, N] (+)= op(A) op(B) (+ bias) for N <= 32.  Workgroup: 4 waves x 32
+// rows of the output; blockIdx.y selects a K split of kchunk (a multiple of
+// 64).  The split is walked in sub-chunks of KSUB: B's N columns over the
+// sub-chunk are staged to LDS, then each wave streams its rows of A, U
+// groups of loads at a time (the first batch issued before B is staged).
+template <int PREC, bool TA, bool TB, bool PA, bool VA>
+__global__ __launch_bounds__(256) void gemm_narrow(GemmArgs g) {
+  using T = typename Prec<PREC>::T;
+  using BV = typename BFrag<PREC>::V;
+  constexpr int KG = Narrow<PREC>::KG, KSUB = Narrow<PREC>::KSUB, LD = NarrowB<PREC>::LD;
+  constexpr int GS = 2 * KG;            // k per group
+  constexpr int U = MYELIN_NARROW_U;    // groups in flight per lane
+  __shared__ NarrowB<PREC> sb;
+  auto &bs = sb.b;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 128 + 32 * w;
+  const bool wave_on = m0 < g.M;  // uniform per wave
+  const int64_t m = (m0 + (lane & 31) < g.M) ? m0 + (lane & 31) : g.M - 1;
+  const int kh = (lane >> 5) * KG;
+  const int N = static_cast<int>(g.N);
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+  for (int64_t ks = kb; ks < ke; ks += KSUB) {
+    const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
+    const int kpad = (klen + GS - 1) / GS * GS;
+    const int ng = kpad / GS;
+    const int nfull = klen / (U * GS);  // batches of U groups wholly below ke
+    float a[U][KG];
+    if (wave_on && nfull > 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_group<PREC, TA, PA, VA, true>(g, m, ks + u * GS + kh, ke, a[u]);
+    }
+    if (ks != kb) __syncthreads();  // the previous sub-chunk's fragments are read
+    stage_narrow_b<PREC, TB, LD>(g, ks, klen, kpad, N, bs, tid);
+    __syncthreads();
+    if (!wave_on) continue;
+    const T *brow = &bs[lane & 31][kh];
+    for (int bi = 0; bi < nfull; ++bi) {
+      if (bi > 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          load_group<PREC, TA, PA, VA, true>(g, m, ks + (bi * U + u) * GS + kh, ke, a[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        group_mfma<PREC>(a[u], *reinterpret_cast<const BV *>(brow + (bi * U + u) * GS), acc);
+    }
+    for (int j = nfull * U; j < ng; ++j) {
+      float t[KG];
+      load_group<PREC, TA, PA, VA, false>(g, m, ks + j * GS + kh, ke, t);
+      group_mfma<PREC>(t, *reinterpret_cast<const BV *>(brow + j * GS), acc);
+    }
+  }
+  if (!wave_on) return;
+  store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
+}
+
+// Rounds an operand value to the MFMA input type of the precision (bf16:
+// round to nearest even), kept in fp32.
+template <int PREC>
+__device__ __forceinline__ float round_in(float v) {
+  if constexpr (PREC == 1)
+    return static_cast<float>(static_cast<__bf16>(v));
+  else
+    return v;
+}
+
+// C[M, N] (+)= op(A) op(B) (+ bias) for K <= KMAX <= 32, on the vector ALUs
+// (the arithmetic is a few FMAs per output; the cost is writing C).  Each
+// lane owns 4 adjacent columns and holds B's K x 4 block in registers (B
+// stored [N, K] is first staged k-major through LDS by the workgroup, whose
+// 4 waves share the 256 columns, from one coalesced read); a wave owns RW
+// rows.  The wave's RW x KMAX block of A is loaded up front,
+// spread over the lanes (value q = row * KMAX + k in lane q % 64), and each
+// value is broadcast to the wave with a lane read when its row is computed,
+// so all loads are in flight at once.  Each row is one 16-byte store per
+// lane, 1 KB contiguous per wave.  Products of the operands rounded to the
+// precision's input type, summed in k order with fused multiply-adds (bf16
+// products are exact in fp32).  VC: C rows allow 16-byte stores.
+#ifndef MYELIN_SMALLK_RW
+#define MYELIN_SMALLK_RW 16  // rows per wave of the small-K kernel
+#endif
+
+template <int PREC, bool TA, bool TB, bool PA, int KMAX, bool VC>
+__global__ __launch_bounds__(256) void gemm_smallk(GemmArgs g) {
+  constexpr int RW = MYELIN_SMALLK_RW;     // rows per wave
+  constexpr int SLOTS = RW * KMAX / 64;    // A values per lane
+  // TB (B stored [N, K]): the workgroup's 256 columns x K, k-major
+  __shared__ __attribute__((aligned(16))) float bt[TB ? KMAX : 1][TB ? 256 : 4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.y) * 4 + w) * RW;
+  const int K = static_cast<int>(g.K);
+  // the wave's block of A first (rows clamped into range, so a wave past
+  // the last row loads valid memory and discards it)
+  float av[SLOTS];
+#pragma unroll
+  for (int q = 0; q < SLOTS; ++q) {
+    const int idx = q * 64 + lane;
+    const int k = idx % KMAX;
+    const int64_t row = r0 + idx / KMAX;
+    const int64_t rr = row < g.M ? row : g.M - 1;
+    const float v = a_elem<TA, PA>(g, rr, k < K ? k : K - 1);
+    av[q] = (k < K && row < g.M) ? round_in<PREC>(v) : 0.0f;
+  }
+  if constexpr (TB) {
+    // B[n * ldb + k] for the 256 columns from n_begin, read in memory order
+    // (contiguous when ldb == K), stored k-major; zero past N
+    const int64_t n_begin = static_cast<int64_t>(blockIdx.x) * 256;
+    const float *B = static_cast<const float *>(g.B);
+    constexpr int PER = KMAX;  // 256 * K <= 256 * KMAX elements, PER per thread at most
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = i * 256 + static_cast<int>(threadIdx.x);
+      const int c = e / K, k = e - c * K;
+      const int64_t n = n_begin + c;
+      v[i] = (c < 256 && n < g.N) ? B[n * g.ldb + k] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = i * 256 + static_cast<int>(threadIdx.x);
+      const int c = e / K, k = e - c * K;
+      if (c < 256) bt[k][c] = v[i];
+    }
+    __syncthreads();
+  }
+  if (r0 >= g.M) return;  // uniform per wave
+  float b[KMAX][4];
+  const bool vb = !TB && (c0 + 3 < g.N) && (g.ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(g.B) & 15) == 0);
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int kk = k < K ? k : K - 1;
+    f4 t;
+    if constexpr (TB) {
+      t = *reinterpret_cast<const f4 *>(&bt[kk][4 * lane]);
+    } else if (vb) {
+      t = *reinterpret_cast<const f4 *>(static_cast<const float *>(g.B) + kk * g.ldb + c0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) t[j] = b_elem<TB>(g, kk, (c0 + j < g.N) ? c0 + j : g.N - 1);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[k][j] = k < K ? round_in<PREC>(t[j]) : 0.0f;
+  }
+  float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (g.bias != nullptr) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bias[j] = g.bias[(c0 + j < g.N) ? c0 + j : g.N - 1];
+  }
+  const bool full = c0 + 3 < g.N;
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= g.M) break;  // uniform
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int q = i * KMAX + k;
+      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av[q / 64]), q % 64));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = __builtin_fmaf(a, b[k][j], o[j]);
+    }
+    float *dst = g.C + r * g.ldc + c0;
+    if (VC && full) {
+      f4 prev = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (g.accumulate) prev = *reinterpret_cast<const f4 *>(dst);
+      f4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float t = g.accumulate ? prev[j] + o[j] : o[j];
+        if (g.bias != nullptr) t = t + bias[j];
+        v[j] = t;
+      }
+      *reinterpret_cast<f4 *>(dst) = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (c0 + j < g.N) {
+          float t = g.accumulate ? dst[j] + o[j] : o[j];
+          if (g.bias != nullptr) t = t + bias[j];
+          dst[j] = t;
+        }
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -779,6 +1165,7 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
 
+  // (the per-element form measures faster here than store_acc's)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t col = n0 + 64 * wn + 32 * j + (lane & 31);
@@ -1459,9 +1846,105 @@ void launch_big_t(const GemmArgs &g, int ta, int tb, bool half, dim3 grid, hipSt
     launch_big<PREC, true, true, BM, BN>(g, half, grid, s);
 }
 
+// K splits of the narrow kernel: only as many as bring the grid to about
+// 1024 workgroups (each split costs a partial [M, N] in the workspace).
+int64_t narrow_splits(int64_t M, int64_t K) {
+  int64_t s = cdiv(MYELIN_NARROW_WGS, cdiv(M, 128));
+  const int64_t by_k = cdiv(K, 64);
+  if (s > by_k) s = by_k;
+  if (s > 64) s = 64;
+  return s < 1 ? 1 : s;
+}
+
+template <int PREC, bool TA, bool TB, bool PA>
+void launch_narrow_v(const GemmArgs &g, bool va, dim3 grid, hipStream_t s) {
+  if constexpr (!TA && !PA) {
+    if (va) {
+      gemm_narrow<PREC, TA, TB, PA, true><<<grid, dim3(256), 0, s>>>(g);
+      return;
+    }
+  }
+  gemm_narrow<PREC, TA, TB, PA, false><<<grid, dim3(256), 0, s>>>(g);
+}
+
+template <int PREC, bool PA>
+void launch_narrow(const GemmArgs &g, int ta, int tb, bool va, dim3 grid, hipStream_t s) {
+  if (!ta && !tb)
+    launch_narrow_v<PREC, false, false, PA>(g, va, grid, s);
+  else if (!ta)
+    launch_narrow_v<PREC, false, true, PA>(g, va, grid, s);
+  else if (!tb)
+    launch_narrow_v<PREC, true, false, PA>(g, va, grid, s);
+  else
+    launch_narrow_v<PREC, true, true, PA>(g, va, grid, s);
+}
+
+template <int PREC, bool PA, int KMAX, bool VC>
+void launch_smallk_k(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
+  if (!ta && !tb)
+    gemm_smallk<PREC, false, false, PA, KMAX, VC><<<grid, dim3(256), 0, s>>>(g);
+  else if (!ta)
+    gemm_smallk<PREC, false, true, PA, KMAX, VC><<<grid, dim3(256), 0, s>>>(g);
+  else if (!tb)
+    gemm_smallk<PREC, true, false, PA, KMAX, VC><<<grid, dim3(256), 0, s>>>(g);
+  else
+    gemm_smallk<PREC, true, true, PA, KMAX, VC><<<grid, dim3(256), 0, s>>>(g);
+}
+
+template <int PREC, bool PA, int KMAX>
+void launch_smallk_c(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
+  if (al16(g.C) && g.ldc % 4 == 0)
+    launch_smallk_k<PREC, PA, KMAX, true>(g, ta, tb, grid, s);
+  else
+    launch_smallk_k<PREC, PA, KMAX, false>(g, ta, tb, grid, s);
+}
+
+// K <= 32, unrolled to the next multiple of 8
+template <int PREC, bool PA>
+void launch_smallk(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
+  if (g.K <= 8)
+    launch_smallk_c<PREC, PA, 8>(g, ta, tb, grid, s);
+  else if (g.K <= 16)
+    launch_smallk_c<PREC, PA, 16>(g, ta, tb, grid, s);
+  else if (g.K <= 24)
+    launch_smallk_c<PREC, PA, 24>(g, ta, tb, grid, s);
+  else
+    launch_smallk_c<PREC, PA, 32>(g, ta, tb, grid, s);
+}
+
 template <int PREC>
 int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s, bool bits = false) {
   constexpr int KS = Prec<PREC>::KS;
+  if (!half && g.N <= 32) {
+    // narrow output (readout currents, dW_o): stream A once
+    int64_t splits = g.ws != nullptr ? narrow_splits(g.M, g.K) : 1;
+    while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
+    g.kchunk = cdiv(cdiv(g.K, splits), 64) * 64;
+    splits = cdiv(g.K, g.kchunk);
+    g.splits = static_cast<int>(splits);
+    const dim3 grid(static_cast<unsigned>(cdiv(g.M, 128)), static_cast<unsigned>(splits));
+    const bool va = !bits && al16(g.A) && g.lda % 4 == 0;
+    if (bits)
+      launch_narrow<PREC, true>(g, ta, tb, va, grid, s);
+    else
+      launch_narrow<PREC, false>(g, ta, tb, va, grid, s);
+    if (int rc = myelin::launched("gemm (narrow)")) return rc;
+    if (splits > 1) {
+      splitk_reduce<<<dim3(cdiv(g.M * g.N, 256)), dim3(256), 0, s>>>(g);
+      return myelin::launched("gemm split-k reduce");
+    }
+    return MYELIN_OK;
+  }
+  if (!half && g.K <= 32 && cdiv(g.M, 4 * MYELIN_SMALLK_RW) <= 65535) {
+    // tiny K (dS = G_o W_o^T): one pass over the output
+    g.splits = 1;
+    const dim3 grid(static_cast<unsigned>(cdiv(g.N, 256)), static_cast<unsigned>(cdiv(g.M, 4 * MYELIN_SMALLK_RW)));
+    if (bits)
+      launch_smallk<PREC, true>(g, ta, tb, grid, s);
+    else
+      launch_smallk<PREC, false>(g, ta, tb, grid, s);
+    return myelin::launched("gemm (small K)");
+  }
   const bool big = !bits && (half || use_big(g));
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
@@ -1537,8 +2020,8 @@ void launch_currents(const CurArgs &a, dim3 grid, hipStream_t s) {
 
 extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, int precision) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  // the largest split either tiling of this output could use
-  int64_t most = 1;
+  // the largest split any kernel for this output could use
+  int64_t most = N <= 32 ? narrow_splits(M, K) : 1;
   for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
     const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
     const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, 512) : plan_splits<0>(tiles, K, 512);

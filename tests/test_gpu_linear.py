@@ -41,9 +41,12 @@ def _bf16(t):
     return t.to(torch.bfloat16).to(torch.float32)
 
 
+# includes the narrow-output route (N <= 32: readout currents and dW_o, with
+# K splits) and the small-K route (K <= 32: dS = G_o W_o^T)
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (64, 64, 64), (70, 33, 100), (300, 17, 784), (5, 200, 10),
                                    (129, 65, 31), (128, 128, 64), (300, 260, 1000), (256, 384, 3000),
-                                   (520, 132, 200), (129, 130, 64), (8200, 1032, 72)])
+                                   (520, 132, 200), (129, 130, 64), (8200, 1032, 72), (6400, 10, 2048),
+                                   (4096, 20, 1500), (257, 32, 1025), (33, 7, 5), (1440, 2050, 20), (70, 40, 32)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
 def test_gemm(M, N, K, ta, tb, prec):
@@ -390,14 +393,15 @@ def test_fused_forward_bf16_operands_match_fp32_operands(T, B, F, N):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (70, 33, 100), (300, 17, 784), (64, 100, 33), (100, 300, 500),
-                                   (1000, 100, 2048), (4096, 20, 6400)])
+                                   (1000, 100, 2048), (4096, 20, 6400), (200, 300, 20), (130, 32, 64)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
 def test_gemm_packed_bit_operand_equals_dense(M, N, K, ta, tb, prec):
     """A given as packed spike words (the readout input of the packed-hidden
     network) gives the same bits as the same 0/1 matrix given densely: both
-    run the 64 x 64 kernel (outputs narrower than 128) with the same k order
-    and the same K split, and 0/1 is exact in either MFMA input type."""
+    run the same kernel (narrow-output, small-K or 64 x 64, by shape) with
+    the same k order and K split, and 0/1 is exact in either MFMA input
+    type."""
 
     _print_case(test="gemm_bits", M=M, N=N, K=K, ta=ta, tb=tb, prec=prec)
     g = seeded(M + 3 * N + 5 * K)
