@@ -1794,8 +1794,12 @@ void launch_gemm_v(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) 
     gemm_kernel<PREC, true, true, VA, VB, PA><<<grid, dim3(256), 0, s>>>(g);
 }
 
+#ifndef MYELIN_SPLIT_WANT
+#define MYELIN_SPLIT_WANT 512  // tile GEMMs split K below this many output tiles
+#endif
+
 // K splits for an output of `tiles` workgroups: split when the output alone
-// gives under `want` workgroups (about two per CU) and K is long.
+// gives under `want` workgroups and K is long.
 template <int PREC>
 int64_t plan_splits(int64_t tiles, int64_t K, int64_t want) {
   constexpr int KS = Prec<PREC>::KS;
@@ -1949,7 +1953,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
   if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
-  int64_t splits = g.ws != nullptr ? plan_splits<PREC>(tiles, g.K, 512) : 1;
+  int64_t splits = g.ws != nullptr ? plan_splits<PREC>(tiles, g.K, MYELIN_SPLIT_WANT) : 1;
   while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
   g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
   splits = cdiv(g.K, g.kchunk);
@@ -2024,7 +2028,7 @@ extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, 
   int64_t most = N <= 32 ? narrow_splits(M, K) : 1;
   for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
     const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
-    const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, 512) : plan_splits<0>(tiles, K, 512);
+    const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, MYELIN_SPLIT_WANT) : plan_splits<0>(tiles, K, MYELIN_SPLIT_WANT);
     if (s > most) most = s;
   }
   return most > 1 ? most * M * N : 0;

@@ -280,7 +280,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         g_spikes = None if rate else g_out
         g_rates = g_out if rate else None
         gx = torch.empty((T, B, F), device=dev) if need_x else None
-        gw = torch.zeros_like(w) if need_w else None
+        gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) chunk overwrites it
         gb_acc = torch.zeros((B, N), device=dev) if (need_b and b is not None) else None
         chunk = T if checkpoint is None else checkpoint
         G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
@@ -311,8 +311,8 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
                 _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
             if gw is not None:
-                # dW += X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, True, prec, stream)
+                # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
+                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_chunks - 1, prec, stream)
         gb = None
         if gb_acc is not None:
             gb = torch.empty((N,), device=dev)

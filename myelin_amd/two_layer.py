@@ -144,8 +144,9 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gm_h = torch.zeros((B, H), device=dev) if need_hidden else None
             gx = torch.empty((T, B, F), device=dev) if need_x else None
             whg = _cast_bf16(wh, stream) if (half and need_x) else wh
-            gwh = torch.zeros_like(wh) if need_wh else None
-            gwo = torch.zeros_like(wo) if need_wo else None
+            # the first (last-in-time) chunk overwrites the weight gradients
+            gwh = torch.empty_like(wh) if need_wh else None
+            gwo = torch.empty_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
             hs = None if words is not None else torch.empty((L0, B, H), device=dev)
@@ -184,11 +185,12 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 )
                 if gwo is not None:
                     # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
+                    acc = k != K - 1
                     if words is not None:
-                        _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, True, prec, stream,
+                        _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, acc, prec, stream,
                               a_bits=True)
                     else:
-                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, True, prec, stream)
+                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream)
                 if not need_hidden:
                     continue
                 # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this chunk
@@ -202,7 +204,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 if gx is not None:
                     _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
                 if gwh is not None:
-                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, True, prec, stream)
+                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != K - 1, prec, stream)
             gbh = gbo = None
             if gbh_acc is not None:
                 gbh = torch.empty((H,), device=dev)
