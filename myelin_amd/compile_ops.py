@@ -44,7 +44,7 @@ def _rate_forward(inputs, weight, bias, decay, threshold, reset, checkpoint_size
     with torch.cuda.device(dev):
         _lif_fwd(x, w, b, None, 0, T, float(decay), float(threshold), float(reset), 10.0, _lib.RULE_THRESHOLD,
                  _lib.PREC["fp32"], _lib.stream(dev), m_final=final_membrane, rates=spike_rates, ckpt=chunk_starts,
-                 ckpt_every=checkpoint_size)
+                 ckpt_every=checkpoint_size, exact=True)
     return final_membrane, spike_rates, chunk_starts
 
 

@@ -32,11 +32,16 @@ import torch
 from myelin_amd import _lib
 
 
-def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None, a_bits=False):
+def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None, a_bits=False,
+          split=True):
     """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16, or
-    (``a_bits``) A packed spike words (int32, lda in words) with B float32."""
+    (``a_bits``) A packed spike words (int32, lda in words) with B float32.
+    ``split=False`` gives no workspace, so K is never split: every element is
+    then one k-ordered sum that does not depend on M (the synapse currents,
+    which a checkpointed backward recomputes over fewer rows and must
+    reproduce bit for bit)."""
 
-    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec)
+    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec) if split else 0
     ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
     a_dt = _lib.DT_BITS if a_bits else _lib.DT[A.dtype]
     _lib.call("myelin_gemm", _lib.ptr(A), a_dt, _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
@@ -133,7 +138,8 @@ def _fused_grid(B: int, N: int) -> int:
 
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
-             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, cur_out=None):
+             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, cur_out=None,
+             exact=False):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
@@ -146,6 +152,9 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     chunks.  ``pre`` is indexed from t0; checkpoint rows from t0.
     ``cur_out`` (``[t1 - t0, B, N]``, chunked route only) receives all the
     currents, for a backward that reuses them instead of recomputing.
+    ``exact``: the GEMM never splits K, so a checkpointed forward and the
+    backward's recompute of any chunk of it produce the same currents bit
+    for bit (the fused kernel always sums that way).
     """
 
     T, B, F = x.shape
@@ -176,9 +185,9 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
         c1 = min(c0 + step, t1)
         rows = (c1 - c0) * B
         if half:
-            _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, stream, bias=b)
+            _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, stream, bias=b, split=not exact)
         else:
-            _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b)
+            _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b, split=not exact)
         last = c1 == t1
         _lib.call(
             "myelin_lif_currents_fwd",
@@ -234,7 +243,7 @@ class HipLinearLIFFunction(torch.autograd.Function):
                     cur = torch.empty((T, B, N), dtype=torch.float32, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1, wt=wt, cur_out=cur)
+                 ckpt_every=checkpoint or 1, wt=wt, cur_out=cur, exact=ckpt is not None and cur is None)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:
@@ -298,7 +307,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 pre_k = scratch
             else:
                 _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
-                         pre=scratch, wt=wt)
+                         pre=scratch, wt=wt, exact=True)
                 pre_k = scratch
             _lib.call(
                 "myelin_linear_pre_bwd",

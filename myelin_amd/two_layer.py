@@ -47,19 +47,21 @@ from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
-                   slope, prec, stream):
+                   slope, prec, stream, exact=False):
     """Readout currents ``hs @ W_o + b_o`` for steps [t0, t1) then the LIF
     recurrence over them in absolute time (counts and rates over all T).
     ``hs`` is the chunk's hidden spikes, dense fp32 ``[L, B, H]`` or packed
-    words ``[L, B, ceil(H/32)]`` int32 (read as bits by the GEMM)."""
+    words ``[L, B, ceil(H/32)]`` int32 (read as bits by the GEMM).
+    ``exact``: no K split, so a recompute reproduces the currents exactly."""
 
     B, O = m0.shape
     H = wo.shape[0]
     L = t1 - t0
     if hs.dtype == torch.int32:
-        _gemm(hs, wo, cur, L * B, O, H, hs.shape[-1], O, O, False, False, False, prec, stream, bias=bo, a_bits=True)
+        _gemm(hs, wo, cur, L * B, O, H, hs.shape[-1], O, O, False, False, False, prec, stream, bias=bo, a_bits=True,
+              split=not exact)
     else:
-        _gemm(hs, wo, cur, L * B, O, H, H, O, O, False, False, False, prec, stream, bias=bo)
+        _gemm(hs, wo, cur, L * B, O, H, H, O, O, False, False, False, prec, stream, bias=bo, split=not exact)
     _lib.call(
         "myelin_lif_currents_fwd",
         _lib.ptr(cur), _lib.ptr(m0), _lib.ptr(m_final), None, _lib.ptr(pre), None, _lib.ptr(rates),
@@ -110,11 +112,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             _lif_fwd(xs[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
                      m_final=m_h, spikes=None if hs is None else hs[:L],
                      packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
-                     ckpt_every=C, wt=wt)
+                     ckpt_every=C, wt=wt, exact=need)
             s_in = words[t0:t1] if hs is None else hs[:L]
             _readout_chunk(cur[t0:t1] if keep else cur[:L], s_in, wo, bo, m_o, m_o, None, counts,
                            rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
-                           stream)
+                           stream, exact=need and not keep)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
         if need:
@@ -166,17 +168,18 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     s_in = words[t0:t1]
                     if need_hidden:
                         _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
-                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L], wt=wt)
+                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L], wt=wt, exact=True)
                 else:
                     s_in = hs[:L]
                     _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
-                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt)
+                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt,
+                             exact=True)
                 if cur_o is not None:
                     _recompute_pre(cur_o[t0:t1], ck_o[k], pre_o, T, B, O, t0, t1, decay, threshold, reset, slope,
                                    _lib.RULE_THRESHOLD, stream)
                 else:
                     _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
-                                   decay, threshold, reset, slope, prec, stream)
+                                   decay, threshold, reset, slope, prec, stream, exact=True)
                 _lib.call(
                     "myelin_linear_pre_bwd",
                     _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],

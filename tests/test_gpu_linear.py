@@ -437,3 +437,33 @@ def test_gemm_packed_bit_operand_checks():
     with pytest.raises(ValueError, match="float32 B"):
         _gemm(words, B.to(torch.bfloat16), C, 16, 8, 40, 2, 8, 8, False, False, False, _lib.PREC["bf16"], stream,
               a_bits=True)
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_checkpoint_recompute_reproduces_forward_trace_exactly(prec):
+    """The backward recomputes each checkpoint chunk's currents over that
+    chunk's rows only; its pre-reset trace must equal the forward's bit for
+    bit (as the reference's per-step recompute does).  Shape chosen so the
+    forward GEMM (8192 rows, 512 tiles) and a chunk's (128 rows, 8 tiles)
+    would split K differently if the current GEMMs were allowed to split."""
+
+    from myelin_amd.linear import _cast_bf16, _half, _lif_fwd, _transpose_bf16
+
+    _print_case(test="recompute_exact", prec=prec)
+    T, B, F, N, C = 1024, 8, 256, 1024, 16
+    g = seeded(17)
+    x = (torch.rand(T, B, F, generator=g) < 0.2).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.4) * 0.2).to(DEV)
+    b = (torch.rand(N, generator=g) * 0.05).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    p = _lib.PREC[prec]
+    half = _half(p, F, N)
+    xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
+    args = (0.95, 1.0, 0.0, 5.0, _lib.RULE_THRESHOLD, p, stream)
+    pre = torch.empty(T, B, N, device=DEV)
+    ck = torch.empty(T // C, B, N, device=DEV)
+    _lif_fwd(xs, w, b, None, 0, T, *args, pre=pre, ckpt=ck, ckpt_every=C, wt=wt, exact=True)
+    scratch = torch.empty(C, B, N, device=DEV)
+    for k in (0, 1, 37, T // C - 1):
+        _lif_fwd(xs, w, b, ck[k], k * C, (k + 1) * C, *args, pre=scratch, wt=wt, exact=True)
+        assert torch.equal(scratch, pre[k * C:(k + 1) * C]), f"chunk {k}"
