@@ -197,6 +197,21 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
         )
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for work that overlaps
+    the current stream's, created once."""
+
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(idx)
+    if s is None:
+        s = torch.cuda.Stream(device=idx)
+        _SIDE_STREAMS[idx] = s
+    return s
+
+
 def _keep_currents(F: int, N: int) -> bool:
     """A checkpointed layer keeps its forward currents ``[T, B, N]`` (and its
     backward runs only the recurrence from them, no synapse GEMM) when they
@@ -295,12 +310,41 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
         scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
         n_chunks = math.ceil(T / chunk)
+        # GEMM recomputes run one chunk ahead on a side stream, into two
+        # alternating trace buffers: chunk k-1's recompute overlaps chunk k's
+        # reverse pass and weight GEMMs (each alone leaves much of the GPU
+        # idle at these sizes).  ready[i]: buffer i holds its chunk's trace;
+        # free[i]: the reverse pass has read buffer i.
+        overlap = checkpoint is not None and cur is None and n_chunks > 1
+        if overlap:
+            main = torch.cuda.current_stream(dev)
+            side = _side_stream(dev)
+            bufs = [scratch, torch.empty_like(scratch)]
+            ready = [torch.cuda.Event(), torch.cuda.Event()]
+            free = [torch.cuda.Event(), torch.cuda.Event()]
+            side.wait_stream(main)
+
+            def recompute(j):
+                i = j % 2
+                with torch.cuda.stream(side):
+                    if j + 2 < n_chunks:
+                        side.wait_event(free[i])
+                    _lif_fwd(xs, w, b, ckpt[j], j * chunk, min(j * chunk + chunk, T), decay, threshold, reset,
+                             slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True)
+                    ready[i].record(side)
+
+            recompute(n_chunks - 1)
         for k in range(n_chunks - 1, -1, -1):
             t0 = k * chunk
             t1 = min(t0 + chunk, T)
             C = t1 - t0
             if checkpoint is None:
                 pre_k = pre
+            elif overlap:
+                if k > 0:
+                    recompute(k - 1)
+                main.wait_event(ready[k % 2])
+                pre_k = bufs[k % 2]
             elif cur is not None:
                 _recompute_pre(cur[t0:t1], ckpt[k], scratch, T, B, N, t0, t1, decay, threshold, reset, slope, rule,
                                stream)
@@ -315,6 +359,8 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT[G.dtype], _lib.ptr(gb_acc),
                 C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
             )
+            if overlap:
+                free[k % 2].record(main)
             rows = C * B
             if gx is not None:
                 # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
@@ -322,6 +368,11 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             if gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
                 _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_chunks - 1, prec, stream)
+        if overlap:
+            # every side-stream kernel is behind a ready[] the main stream
+            # waited on; the buffers' last users include the side stream
+            for t in (*bufs, xs, w, ckpt, *(() if b is None else (b,)), *(() if wt is None else (wt,))):
+                t.record_stream(side)
         gb = None
         if gb_acc is not None:
             gb = torch.empty((N,), device=dev)

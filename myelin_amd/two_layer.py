@@ -43,7 +43,7 @@ import torch
 
 from myelin_amd import _lib
 from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _keep_currents, _lif_fwd,
-                               _recompute_pre, _transpose_bf16)
+                               _recompute_pre, _side_stream, _transpose_bf16)
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
@@ -151,29 +151,59 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gwo = torch.empty_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
-            hs = None if words is not None else torch.empty((L0, B, H), device=dev)
-            pre_h = torch.empty((L0, B, H), device=dev) if need_hidden else None
             cur = torch.empty((L0, B, O), device=dev) if cur_o is None else None
             pre_o = torch.empty((L0, B, O), device=dev)
             G_o = torch.empty((L0, B, O), device=dev)
             ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
             G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
                    if need_hidden else None)
+            # The hidden recompute (its trace, and spikes in the dense
+            # variant) runs one chunk ahead on a side stream into two
+            # alternating buffer sets, overlapping the current chunk's
+            # readout and hidden reverse passes and GEMMs.  ready[i]: set i
+            # holds its chunk; free[i]: the chunk using set i is done with it.
+            recomputes = need_hidden or words is None
+            nset = 2 if (recomputes and K > 1) else 1
+            hs_b = [None if words is not None else torch.empty((L0, B, H), device=dev) for _ in range(nset)]
+            pre_b = [torch.empty((L0, B, H), device=dev) if need_hidden else None for _ in range(nset)]
+            main = torch.cuda.current_stream(dev)
+            side = _side_stream(dev) if nset == 2 else main
+            ready = [torch.cuda.Event() for _ in range(nset)]
+            free = [torch.cuda.Event() for _ in range(nset)]
+            if nset == 2:
+                side.wait_stream(main)
+
+            def hidden_recompute(j):
+                i = j % nset
+                a0, a1 = j * C, min(j * C + C, T)
+                n = a1 - a0
+                with torch.cuda.stream(side):
+                    if nset == 2 and j + 2 < K:
+                        side.wait_event(free[i])
+                    pre_j = None if pre_b[i] is None else pre_b[i][:n]
+                    if words is not None:
+                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j], 0, n, decay, threshold, reset, slope,
+                                 _lib.RULE_THRESHOLD, prec, side.cuda_stream, pre=pre_j, wt=wt, exact=True)
+                    else:
+                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j], 0, n, decay, threshold, reset, slope,
+                                 _lib.RULE_THRESHOLD, prec, side.cuda_stream, spikes=hs_b[i][:n], pre=pre_j, wt=wt,
+                                 exact=True)
+                    ready[i].record(side)
+
+            if recomputes:
+                hidden_recompute(K - 1)
             for k in range(K - 1, -1, -1):
                 t0 = k * C
                 t1 = min(t0 + C, T)
                 L = t1 - t0
                 rows = L * B
-                if words is not None:
-                    s_in = words[t0:t1]
-                    if need_hidden:
-                        _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope,
-                                 _lib.RULE_THRESHOLD, prec, stream, pre=pre_h[:L], wt=wt, exact=True)
-                else:
-                    s_in = hs[:L]
-                    _lif_fwd(xs[t0:t1], wh, bh, ck_h[k], 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD,
-                             prec, stream, spikes=hs[:L], pre=None if pre_h is None else pre_h[:L], wt=wt,
-                             exact=True)
+                i = k % nset
+                if recomputes:
+                    if nset == 2 and k > 0:
+                        hidden_recompute(k - 1)
+                    main.wait_event(ready[i])
+                hs, pre_h = hs_b[i], pre_b[i]
+                s_in = words[t0:t1] if words is not None else hs[:L]
                 if cur_o is not None:
                     _recompute_pre(cur_o[t0:t1], ck_o[k], pre_o, T, B, O, t0, t1, decay, threshold, reset, slope,
                                    _lib.RULE_THRESHOLD, stream)
@@ -195,6 +225,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     else:
                         _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream)
                 if not need_hidden:
+                    if nset == 2:
+                        free[i].record(main)  # dW_o was the last reader of the spikes
                     continue
                 # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this chunk
                 _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
@@ -204,10 +236,18 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     _lib.ptr(gbh_acc),
                     L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
+                if nset == 2:
+                    free[i].record(main)  # the trace's last reader (the spikes' was dW_o)
                 if gx is not None:
                     _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
                 if gwh is not None:
                     _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != K - 1, prec, stream)
+            if nset == 2:
+                # every side-stream kernel is behind a ready[] the main stream
+                # waited on; these tensors' last users include the side stream
+                for t_ in (*hs_b, *pre_b, xs, wh, ck_h, bh, wt):
+                    if t_ is not None:
+                        t_.record_stream(side)
             gbh = gbo = None
             if gbh_acc is not None:
                 gbh = torch.empty((H,), device=dev)
