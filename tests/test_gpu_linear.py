@@ -241,13 +241,13 @@ def test_modules_match_functional_paths():
     assert packed(x).data.shape == (8, 4, 1)
 
 
-def test_streamed_synapse_bf16_config_subset():
+def test_streamed_synapse_bf16_batch_subset():
     """LinearSurrogateLIF(784 -> 2048, stream_synapse=True, atan, bf16 GEMM)
     then LinearSurrogateLIFRate(2048 -> 10, atan), CE on spike counts, at
     T=50 and a 32-row batch slice; oracle = fp32 torch path on bf16-rounded
     weights (inputs are exactly 0/1)."""
 
-    _print_case(test="config3_subset")
+    _print_case(test="streamed_synapse_bf16_subset")
     T, B, F, H, O = 50, 32, 784, 2048, 10
     g = seeded(3)
     rate_f = torch.rand(F, generator=g) * 0.2

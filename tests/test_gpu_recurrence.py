@@ -33,10 +33,10 @@ def _print_case(**kw):
 
 
 # ---------------------------------------------------------------- plain LIF
-def test_lif_forward_config1_bit_exact():
+def test_lif_forward_T100_B64_N1024_bit_exact():
     """LIF, hard reset, x ~ N(0.3, 0.5) [100, 64, 1024], beta=0.9 (tau 10), theta=1, v0=0."""
 
-    _print_case(test="lif_config1")
+    _print_case(test="lif_T100_B64_N1024")
     g = seeded(1)
     x = 0.3 + 0.5 * torch.randn(100, 64, 1024, generator=g)
     m0 = torch.zeros(64, 1024)
