@@ -666,8 +666,11 @@ __global__ __launch_bounds__(256) void gemm_smallk(GemmArgs g) {
   // TB (B stored [N, K]): the workgroup's 256 columns x K, k-major
   __shared__ __attribute__((aligned(16))) float bt[TB ? KMAX : 1][TB ? 256 : 4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
-  const int64_t r0 = (static_cast<int64_t>(blockIdx.y) * 4 + w) * RW;
+  // one-dimensional grid: column group fastest, then row group
+  const int64_t cgroups = (g.N + 255) / 256;
+  const int64_t cg = static_cast<int64_t>(blockIdx.x) % cgroups, rg = static_cast<int64_t>(blockIdx.x) / cgroups;
+  const int64_t c0 = cg * 256 + 4 * lane;
+  const int64_t r0 = (rg * 4 + w) * RW;
   const int K = static_cast<int>(g.K);
   // the wave's block of A first (rows clamped into range, so a wave past
   // the last row loads valid memory and discards it)
@@ -684,7 +687,7 @@ __global__ __launch_bounds__(256) void gemm_smallk(GemmArgs g) {
   if constexpr (TB) {
     // B[n * ldb + k] for the 256 columns from n_begin, read in memory order
     // (contiguous when ldb == K), stored k-major; zero past N
-    const int64_t n_begin = static_cast<int64_t>(blockIdx.x) * 256;
+    const int64_t n_begin = cg * 256;
     const float *B = static_cast<const float *>(g.B);
     constexpr int PER = KMAX;  // 256 * K <= 256 * KMAX elements, PER per thread at most
     float v[PER];
@@ -1939,10 +1942,12 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     }
     return MYELIN_OK;
   }
-  if (!half && g.K <= 32 && cdiv(g.M, 4 * MYELIN_SMALLK_RW) <= 65535) {
+  if (!half && g.K <= 32) {
     // tiny K (dS = G_o W_o^T): one pass over the output
+    const int64_t wgs = cdiv(g.N, 256) * cdiv(g.M, 4 * MYELIN_SMALLK_RW);
+    if (wgs > 0x7fffffff) return myelin::invalid("gemm: output too large (%lld x %lld)", (long long)g.M, (long long)g.N);
     g.splits = 1;
-    const dim3 grid(static_cast<unsigned>(cdiv(g.N, 256)), static_cast<unsigned>(cdiv(g.M, 4 * MYELIN_SMALLK_RW)));
+    const dim3 grid(static_cast<unsigned>(wgs));
     if (bits)
       launch_smallk<PREC, true>(g, ta, tb, grid, s);
     else
