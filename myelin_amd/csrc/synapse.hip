@@ -1,22 +1,28 @@
-// Streamed synapse x_t @ W fused ahead of the LIF update, and the GEMMs of
-// its backward, for gfx950.
+// Streamed synapse x_t @ W fused ahead of the LIF update, and the GEMMs and
+// reverse recurrences of its backward, for gfx950.  In file order:
 //
-// MFMA tiles: a workgroup of 4 waves computes a 64 x 64 output tile, each
-// wave one 32 x 32 quarter with v_mfma_f32_32x32x16_bf16 (bf16 inputs,
-// fp32 accumulate) or v_mfma_f32_32x32x2f32 (fp32).  Operand fragments, per
-// lane l of a wave:
+//  * gemm_kernel: 64 x 64 output tiles, 4 waves each owning a 32 x 32
+//    quarter (v_mfma_f32_32x32x16_bf16 with fp32 accumulate, or
+//    v_mfma_f32_32x32x2f32), operands staged through LDS; A may also be
+//    packed spike bits.
+//  * gemm_narrow / gemm_smallk: the readout shapes -- at most 32 output
+//    columns (A streamed once straight into MFMA fragments) or K at most 32
+//    (vector-ALU FMAs, 16-byte row stores).
+//  * gemm_big: 128 x 128 tiles (each wave 2 x 2 MFMA blocks), register-
+//    prefetched stages, XCD-grouped tile order; fp32 or bf16 operands.
+//  * linear_lif_fwd / linear_lif_fwd_big: the current tile of a batch-row
+//    block computed per time chunk, parked in LDS and consumed by the LIF
+//    recurrence in registers, so currents never reach HBM.
+//  * linear_pre_bwd (reverse recurrence -> G = dL/dI), col_sum (bias
+//    gradient), lif_currents_fwd (the recurrence over precomputed currents),
+//    bf16 operand copies, then the C ABI.
+//
+// MFMA operand fragments, per lane l of a wave (32 x 32 tiles):
 //   A (32 x K-step): row l % 32, k = (l / 32) * KV + [0, KV)   (KV = 8 bf16 | 1 f32)
 //   B (K-step x 32): col l % 32, same k
 //   D (32 x 32):     col l % 32, row 8*(r/4) + 4*(l/32) + r%4 for acc register r
 // Tiles stage through LDS k-contiguous ([row][k] for A, [col][k] for B), so a
 // bf16 fragment is one 16-byte LDS read.
-//
-// linear_lif_fwd: the workgroup owns 8 batch rows x 64 neurons and walks the
-// time axis in chunks of 8 steps.  Per chunk it computes the 64 x 64 current
-// tile (rows = 8 steps x 8 batch rows) over the full input width, parks it
-// in LDS, and runs the 8 recurrence steps for its 512 neurons in registers;
-// membrane (and spike counts) stay in registers across chunks, so currents
-// never go to HBM.
 
 #include <type_traits>
 
