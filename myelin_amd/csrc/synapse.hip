@@ -45,7 +45,7 @@ struct Prec<0> {  // fp32 MFMA
   static constexpr int KS = 32;  // k per LDS stage
   static constexpr int KV = 1;   // k per lane per MFMA
   static constexpr int KM = 2;   // k per MFMA
-  static constexpr int PAD = 1;
+  static constexpr int PAD = 4;  // rows of 36 floats: 16-byte fragment reads hit 64 distinct banks
 };
 template <>
 struct Prec<1> {  // bf16 MFMA, fp32 accumulate
@@ -72,27 +72,40 @@ __device__ __forceinline__ typename Prec<PREC>::T cvt(float v) {
     return v;
 }
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
 // One wave's MFMA over one LDS stage: acc += A[wm rows] x B[wn cols].
+// fp32 fragments are read 16 bytes at a time: for each group of 8 k, lane l
+// reads k0 + 4*(l/32) + [0, 4) and the i-th v_mfma_f32_32x32x2f32 takes
+// element i (lanes < 32: k0 + i, lanes >= 32: k0 + 4 + i), so one LDS read
+// feeds four MFMAs without bank conflicts.  Every fp32 tile path uses this
+// k order, so all of them produce the same sums.
 template <int PREC>
 __device__ __forceinline__ void mfma_stage(const Stage<PREC> &st, int wm, int wn, int lane, f32x16 &acc) {
   constexpr int KS = Prec<PREC>::KS, KM = Prec<PREC>::KM, KV = Prec<PREC>::KV;
-  const int r = 32 * wm + (lane & 31), c = 32 * wn + (lane & 31), kq = (lane >> 5) * KV;
+  const int r = 32 * wm + (lane & 31), c = 32 * wn + (lane & 31);
+  if constexpr (PREC == 1) {
+    const int kq = (lane >> 5) * KV;
 #pragma unroll
-  for (int kk = 0; kk < KS; kk += KM) {
-    if constexpr (PREC == 1) {
+    for (int kk = 0; kk < KS; kk += KM) {
       const bf16x8 av = *reinterpret_cast<const bf16x8 *>(&st.a[r][kk + kq]);
       const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(&st.b[c][kk + kq]);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
-    } else {
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(st.a[r][kk + kq], st.b[c][kk + kq], acc, 0, 0, 0);
+    }
+  } else {
+    const int kq = (lane >> 5) * 4;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk += 8) {
+      const f4 av = *reinterpret_cast<const f4 *>(&st.a[r][kk + kq]);
+      const f4 bv = *reinterpret_cast<const f4 *>(&st.b[c][kk + kq]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[i], acc, 0, 0, 0);
     }
   }
 }
 
 // row index (within the wave's 32 x 32 quarter) of accumulator register r
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
-
-typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Stages one operand tile (64 rows x KS k) from global memory through
 // registers into LDS.  Each thread owns NV float4 pieces.
@@ -179,12 +192,17 @@ struct TileLoader {
   __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[Stage<PREC>::LD]) const {
 #pragma unroll
     for (int e = 0; e < NV; ++e) {
+      if constexpr (KCONTIG && PREC == 0) {
+        // fp32 rows are 16-byte aligned (36 floats) and koff a multiple of 4
+        *reinterpret_cast<f4 *>(&dst[roff[e]][koff[e]]) = f4{v[e][0], v[e][1], v[e][2], v[e][3]};
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (KCONTIG)
-          dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
-        else
-          dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (KCONTIG)
+            dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
+          else
+            dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+        }
       }
     }
   }
@@ -255,12 +273,17 @@ struct BitLoader {
   __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[Stage<PREC>::LD]) const {
 #pragma unroll
     for (int e = 0; e < NV; ++e) {
+      if constexpr (KCONTIG && PREC == 0) {
+        // fp32 rows are 16-byte aligned (36 floats) and koff a multiple of 4
+        *reinterpret_cast<f4 *>(&dst[roff[e]][koff[e]]) = f4{v[e][0], v[e][1], v[e][2], v[e][3]};
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (KCONTIG)
-          dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
-        else
-          dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (KCONTIG)
+            dst[roff[e]][koff[e] + i] = cvt<PREC>(v[e][i]);
+          else
+            dst[roff[e] + i][koff[e]] = cvt<PREC>(v[e][i]);
+        }
       }
     }
   }
@@ -1031,13 +1054,20 @@ __device__ __forceinline__ void big_mfma(const ST &st, int wm, int wn, int lane,
       acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
       acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
       acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
-    } else {
-      const float a0 = st.a[r][kk + kq], a1 = st.a[r + 32][kk + kq];
-      const float b0 = st.b[c][kk + kq], b1 = st.b[c + 32][kk + kq];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    } else if (kk % 8 == 0) {
+      // 16-byte fragment groups of 8 k, the k order of mfma_stage
+      const int kg = (lane >> 5) * 4;
+      const f4 a0 = *reinterpret_cast<const f4 *>(&st.a[r][kk + kg]);
+      const f4 a1 = *reinterpret_cast<const f4 *>(&st.a[r + 32][kk + kg]);
+      const f4 b0 = *reinterpret_cast<const f4 *>(&st.b[c][kk + kg]);
+      const f4 b1 = *reinterpret_cast<const f4 *>(&st.b[c + 32][kk + kg]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[i], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b1[i], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], b0[i], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], b1[i], acc[1][1], 0, 0, 0);
+      }
     }
   }
 }
