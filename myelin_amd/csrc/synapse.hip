@@ -1503,7 +1503,9 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
   int64_t next_ck = p.t_begin, ck_row = 0;
 
   using S = typename std::conditional<H, uint16_t, float>::type;
-  constexpr int D = 1;  // the recurrence state leaves no room for a second register set
+  // register sets of prefetched stages: a second fits in 256 VGPRs
+  // (2 waves per SIMD, which the LDS allows anyway) only for 8-row bf16
+  constexpr int D = (H && BT == 8) ? 2 : 1;
   // H: wt [N, F] rows are neurons (k-contiguous); else w [F, N], neurons
   // contiguous for a fixed k
   BigLoader<PREC, H, S, D> lb;
