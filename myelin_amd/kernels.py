@@ -18,7 +18,7 @@ from typing import Literal
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.autograd import HipALIFFunction, HipLIFFunction
+from myelin_amd.autograd import BWD_CHUNK, HipALIFFunction, HipLIFFunction
 from myelin_amd.checkpointing import CheckpointSize, resolve_checkpoint_size
 from myelin_amd.neurons import ALIFParams, ALIFState, LIFParams, LIFState
 from myelin_amd.packing import PackedSpikes, packed_last_dim_size
@@ -60,6 +60,16 @@ def _f32(v: float) -> float:
     return float(v)
 
 
+def _direct(*tensors: torch.Tensor) -> bool:
+    """No autograd graph is needed and the tensors are on the current device:
+    the forward can launch directly, without the autograd Function and the
+    device switch (the same entry point and outputs, less host time)."""
+
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return False
+    return tensors[0].device.index == torch.cuda.current_device()
+
+
 def lif_forward(
     inputs: torch.Tensor,
     initial_state: LIFState,
@@ -78,9 +88,18 @@ def lif_forward(
     _check_backend(backend)
     _check_inputs(inputs)
     m0 = _check_state(initial_state.membrane, inputs, "membrane")
+    x = inputs.contiguous()
+    if _direct(x, m0):
+        T, B, N = x.shape
+        m = torch.empty_like(m0)
+        spikes = torch.empty_like(x)
+        _lib.call("myelin_lif_fwd_f32", x.data_ptr(), m0.data_ptr(), m.data_ptr(), spikes.data_ptr(), None, None,
+                  T, B, N, _f32(params.decay), _f32(params.threshold), _f32(params.reset), 0.0,
+                  _lib.RULE_THRESHOLD, BWD_CHUNK, _lib.stream(x.device))
+        return LIFState(membrane=m), spikes
     with torch.cuda.device(inputs.device):
         m, spikes = HipLIFFunction.apply(
-            inputs.contiguous(), m0, _f32(params.decay), _f32(params.threshold), _f32(params.reset),
+            x, m0, _f32(params.decay), _f32(params.threshold), _f32(params.reset),
             0.0, _lib.RULE_THRESHOLD, _lib.SG_NONE,
         )
     return LIFState(membrane=m), spikes
@@ -139,9 +158,19 @@ def alif_forward(
     _check_inputs(inputs)
     m0 = _check_state(initial_state.membrane, inputs, "membrane")
     a0 = _check_state(initial_state.adaptation, inputs, "adaptation")
+    x = inputs.contiguous()
+    if _direct(x, m0, a0):
+        T, B, N = x.shape
+        m, a = torch.empty_like(m0), torch.empty_like(a0)
+        spikes = torch.empty_like(x)
+        _lib.call("myelin_alif_fwd_f32", x.data_ptr(), m0.data_ptr(), a0.data_ptr(), m.data_ptr(), a.data_ptr(),
+                  spikes.data_ptr(), None, None, None, T, B, N, _f32(params.decay), _f32(params.adaptation_decay),
+                  _f32(params.threshold), _f32(params.beta), _f32(params.reset), 0.0, _lib.RULE_THRESHOLD,
+                  BWD_CHUNK, _lib.stream(x.device))
+        return ALIFState(membrane=m, adaptation=a), spikes
     with torch.cuda.device(inputs.device):
         m, a, spikes = HipALIFFunction.apply(
-            inputs.contiguous(), m0, a0, _f32(params.decay), _f32(params.adaptation_decay),
+            x, m0, a0, _f32(params.decay), _f32(params.adaptation_decay),
             _f32(params.threshold), _f32(params.beta), _f32(params.reset), 0.0,
             _lib.RULE_THRESHOLD, _lib.SG_NONE,
         )
