@@ -10,6 +10,9 @@ words, unpack writes 4 elements per lane, counts use popcount.
 
 from __future__ import annotations
 
+import contextlib
+import ctypes
+
 from collections.abc import Sequence
 from dataclasses import dataclass
 from typing import Union
@@ -41,6 +44,15 @@ class PackedSpikes:
         return numel
 
 
+def _device_of(t: torch.Tensor):
+    """The tensor's device as the current device for a launch (no switch
+    when it already is)."""
+
+    if t.device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(t.device)
+
+
 def packed_last_dim_size(size: int) -> int:
     """Words needed for a last dimension of ``size`` (packing.py:36-42)."""
 
@@ -69,7 +81,7 @@ def pack_spikes(spikes: torch.Tensor) -> PackedSpikes:
     n = src.shape[-1]
     rows = src.numel() // n
     words = torch.empty((*src.shape[:-1], packed_last_dim_size(n)), dtype=torch.int32, device=src.device)
-    with torch.cuda.device(src.device):
+    with _device_of(src):
         _lib.call("myelin_pack", _lib.ptr(src), code, _lib.ptr(words), rows, n, _lib.stream(src.device))
     return PackedSpikes(data=words, original_shape=tuple(spikes.shape))
 
@@ -85,7 +97,7 @@ def unpack_spikes(packed: PackedSpikes, *, dtype: torch.dtype = torch.float32) -
     n = shape[-1]
     out = torch.empty(shape, dtype=dtype, device=words.device)
     rows = out.numel() // n
-    with torch.cuda.device(words.device):
+    with _device_of(words):
         _lib.call("myelin_unpack", _lib.ptr(words), _lib.ptr(out), code, rows, n, _lib.stream(words.device))
     return out
 
@@ -136,12 +148,12 @@ def packed_spike_counts(packed: PackedSpikes, dim: CountDim = -1) -> torch.Tenso
     kept = tuple(s for i, s in enumerate(lead) if not (mask >> i) & 1)
     out = torch.empty(kept, dtype=torch.int64, device=packed.data.device)
     words = packed.data.contiguous()
-    lead_arr = (torch.tensor(lead, dtype=torch.int64) if lead else torch.zeros(1, dtype=torch.int64))
+    lead_arr = (ctypes.c_int64 * max(1, len(lead)))(*lead)
     if len(lead) > 8:
         raise ValueError("at most 8 leading dimensions are supported")
-    with torch.cuda.device(words.device):
+    with _device_of(words):
         _lib.call(
-            "myelin_packed_counts", _lib.ptr(words), len(lead), lead_arr.data_ptr(), mask, shape[-1],
+            "myelin_packed_counts", _lib.ptr(words), len(lead), ctypes.addressof(lead_arr), mask, shape[-1],
             _lib.ptr(out), _lib.stream(words.device),
         )
     return out
@@ -170,7 +182,7 @@ def _counts_keep_last(packed: PackedSpikes, dims: tuple[int, ...]) -> torch.Tens
     for d in keep:
         K *= shape[d]
     out = torch.empty((*[shape[d] for d in keep], n), dtype=torch.int64, device=words.device)
-    with torch.cuda.device(words.device):
+    with _device_of(words):
         _lib.call(
             "myelin_packed_counts_keep_last", _lib.ptr(words), R, K, n, _lib.ptr(out),
             _lib.stream(words.device),
@@ -192,7 +204,7 @@ def packed_spike_rate(
     if dtype not in (torch.float32, torch.float64):
         raise ValueError("packed_spike_rate supports dtype float32 or float64 on the HIP path")
     out = torch.empty(counts.shape, dtype=dtype, device=counts.device)
-    with torch.cuda.device(counts.device):
+    with _device_of(counts):
         _lib.call(
             "myelin_counts_to_rate", _lib.ptr(counts), _lib.ptr(out), _lib.DT[dtype], counts.numel(),
             denominator, _lib.stream(counts.device),
