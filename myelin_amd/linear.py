@@ -11,11 +11,14 @@ Saved state:
   autograd.py:445-558): the pre-reset membranes ``[T, B, N]`` -- one tensor
   where the reference keeps pre-reset membranes and spikes;
 * ``checkpoint_size=C`` (autograd.py:588-717) and the rate readout
-  (autograd.py:753-885): chunk-start membranes every C steps only.
+  (autograd.py:753-885): chunk-start membranes every C steps only, except
+  for layers of at most 32 neurons (readouts), which keep the whole trace
+  as the stream path does (a few MB; their backward then recomputes
+  nothing).
 
-Backward, per chunk in reverse time: recompute the chunk's pre-reset trace
-(fused kernel from the chunk-start membrane; skipped for the stream path),
-reverse recurrence -> G = dL/dI ``[C, B, N]`` plus per-(b, n) bias partials,
+Backward, per span of whole chunks in reverse time: recompute the span's
+pre-reset trace from its first chunk-start membrane (skipped when the trace
+is saved), reverse recurrence -> G = dL/dI plus per-(b, n) bias partials,
 then ``dX[t] = G_t @ W^T`` and ``dW += X_t^T G_t`` on MFMA GEMMs,
 ``db = sum_b`` of the bias partials.  Every reduction has a fixed order, so
 gradients are run-to-run deterministic (the reference's Triton path uses
@@ -137,9 +140,22 @@ def _fused_grid(B: int, N: int) -> int:
     return nt * -(-B // 8) if nt * -(-B // 8) >= 512 else nt * -(-B // 4)
 
 
+def _fused(B: int, N: int) -> bool:
+    """The forward takes the fused kernel (else GEMM chunks + recurrence)."""
+
+    return N >= 64 and _fused_grid(B, N) >= 1024
+
+
+def _span(T: int, checkpoint: int, BN: int) -> int:
+    """Steps per backward span of a checkpointed layer: whole chunks, as
+    many as keep a span's trace within _CURRENT_CHUNK_ELEMS."""
+
+    return checkpoint * max(1, min(math.ceil(T / checkpoint), _CURRENT_CHUNK_ELEMS // (checkpoint * BN)))
+
+
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
-             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, cur_out=None,
-             exact=False):
+             spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, exact=False,
+             pre_from=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
@@ -149,9 +165,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     are processed in chunks of up to 2**25 currents: an MFMA GEMM (split-K
     when narrow) writes ``x_t @ W + b`` for the chunk, then the recurrence
     kernel consumes it, carrying the membrane and the spike counts across
-    chunks.  ``pre`` is indexed from t0; checkpoint rows from t0.
-    ``cur_out`` (``[t1 - t0, B, N]``, chunked route only) receives all the
-    currents, for a backward that reuses them instead of recomputing.
+    chunks; with several chunks, each chunk's GEMM runs on a side stream
+    while the previous chunk's recurrence runs.  ``pre`` receives the steps
+    from ``pre_from`` (default t0; the chunked route only) on; checkpoint
+    rows count from t0.
     ``exact``: the GEMM never splits K, so a checkpointed forward and the
     backward's recompute of any chunk of it produce the same currents bit
     for bit (the fused kernel always sums that way).
@@ -160,7 +177,9 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     T, B, F = x.shape
     half = x.dtype == torch.bfloat16
     N = wt.shape[0] if half else w.shape[1]
-    if cur_out is None and N >= 64 and _fused_grid(B, N) >= 1024:
+    if _fused(B, N):
+        if pre_from not in (None, t0):
+            raise ValueError("pre_from is a chunked-route option")
         outs = (_lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
                 _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule)
         if half:
@@ -169,32 +188,65 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
             _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *outs, prec, stream)
         return
     dev = x.device
-    if cur_out is not None:
-        step, cur = t1 - t0, cur_out
-    else:
-        step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
-        cur = torch.empty((step, B, N), dtype=torch.float32, device=dev)
+    step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
+    p0 = t0 if pre_from is None else pre_from  # pre holds the steps from p0 on
+    bounds = sorted({*range(t0, t1, step), t1} | ({p0} if t0 < p0 < t1 else set()))
+    n = len(bounds) - 1
+    # several chunks: each chunk's GEMM runs on the side stream one chunk
+    # ahead of the recurrence, into two alternating currents buffers
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    overlap = n > 1 and main.cuda_stream == stream and side.cuda_stream != stream
+    curs = [torch.empty((step, B, N), dtype=torch.float32, device=dev) for _ in range(2 if overlap else 1)]
     # the membrane carried across chunks lives in m_final (each lane reads
     # its m0 before writing, so m0 may be m_final); a single chunk needs no
     # carry buffer at all
     state = m_final
-    if state is None and step < t1 - t0:
+    if state is None and n > 1:
         state = torch.empty((B, N), dtype=torch.float32, device=dev)
     counts = torch.zeros((B, N), dtype=torch.float32, device=dev) if rates is not None else None
-    for c0 in range(t0, t1, step):
-        c1 = min(c0 + step, t1)
+    if overlap:
+        side.wait_stream(main)
+        done = [torch.cuda.Event(), torch.cuda.Event()]  # GEMM wrote buffer i
+        used = [torch.cuda.Event(), torch.cuda.Event()]  # the recurrence read buffer i
+
+    def gemm(c0, c1, cur, s):
         rows = (c1 - c0) * B
         if half:
-            _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, stream, bias=b, split=not exact)
+            _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, s, bias=b, split=not exact)
         else:
-            _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, stream, bias=b, split=not exact)
+            _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, s, bias=b, split=not exact)
+
+    for c in range(n):
+        c0, c1 = bounds[c], bounds[c + 1]
+        i = c % len(curs)
+        cur = curs[i]
+        if overlap:
+            with torch.cuda.stream(side):
+                if c >= 2:
+                    side.wait_event(used[i])
+                gemm(c0, c1, cur, side.cuda_stream)
+                done[i].record(side)
+            main.wait_event(done[i])
+        else:
+            gemm(c0, c1, cur, stream)
         last = c1 == t1
+        with_pre = pre is not None and c0 >= p0
         _lib.call(
             "myelin_lif_currents_fwd",
-            _lib.ptr(cur), _lib.ptr(m0 if c0 == t0 else state), _lib.ptr(state), _lib.ptr(spikes), _lib.ptr(pre),
-            _lib.ptr(packed), _lib.ptr(rates) if last else None, _lib.ptr(counts), _lib.ptr(ckpt), T, B, N, c0, c1,
-            t0, t0, ckpt_every, decay, threshold, reset, slope, rule, stream,
+            _lib.ptr(cur), _lib.ptr(m0 if c0 == t0 else state), _lib.ptr(state), _lib.ptr(spikes),
+            _lib.ptr(pre) if with_pre else None, _lib.ptr(packed), _lib.ptr(rates) if last else None,
+            _lib.ptr(counts), _lib.ptr(ckpt), T, B, N, c0, c1, p0 if with_pre else t0, t0, ckpt_every, decay,
+            threshold, reset, slope, rule, stream,
         )
+        if overlap:
+            used[i].record(main)
+    if overlap:
+        # the main stream waited on every side GEMM; the inputs' and buffers'
+        # last users include the side stream
+        for t_ in (*curs, x, w, b, wt):
+            if t_ is not None:
+                t_.record_stream(side)
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -212,25 +264,15 @@ def _side_stream(dev: torch.device) -> torch.cuda.Stream:
     return s
 
 
-def _keep_currents(F: int, N: int) -> bool:
-    """A checkpointed layer keeps its forward currents ``[T, B, N]`` (and its
-    backward runs only the recurrence from them, no synapse GEMM) when they
-    are narrow: at most 32 neurons and at most 1/8 of the saved input's
-    bytes -- the readout layers, whose recompute GEMM would re-read the whole
-    input to rebuild a few columns."""
+def _keep_trace(F: int, N: int) -> bool:
+    """A checkpointed layer keeps its whole pre-reset trace ``[T, B, N]``
+    instead of checkpoints (as the uncheckpointed path does), so its
+    backward recomputes nothing, when the trace is narrow: at most 32
+    neurons and at most 1/8 of the saved input's bytes -- the readout
+    layers, whose recompute GEMM would re-read the whole input to rebuild a
+    few columns and whose serial recurrence over T runs on a few waves."""
 
     return N <= 32 and 8 * N <= F
-
-
-def _recompute_pre(cur, m0, pre, T, B, N, t0, t1, decay, threshold, reset, slope, rule, stream):
-    """Pre-reset trace of steps [t0, t1) from saved currents (row 0 = step t0)
-    and the chunk-start membrane ``m0``; ``pre`` rows from t0."""
-
-    _lib.call(
-        "myelin_lif_currents_fwd",
-        _lib.ptr(cur), _lib.ptr(m0), None, None, _lib.ptr(pre), None, None, None, None, T, B, N, t0, t1, t0, t0, 1,
-        decay, threshold, reset, slope, rule, stream,
-    )
 
 
 class HipLinearLIFFunction(torch.autograd.Function):
@@ -248,22 +290,30 @@ class HipLinearLIFFunction(torch.autograd.Function):
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
-        pre = ckpt = cur = None
+        if checkpoint is not None and _keep_trace(F, N):
+            checkpoint = None
+        pre = ckpt = None
+        tail = 0
         if need:
             if checkpoint is None:
                 pre = torch.empty((T, B, N), dtype=x.dtype, device=dev)
             else:
                 ckpt = torch.empty((math.ceil(T / checkpoint), B, N), dtype=x.dtype, device=dev)
-                if _keep_currents(F, N):
-                    cur = torch.empty((T, B, N), dtype=torch.float32, device=dev)
+                if not _fused(B, N):
+                    # the backward starts with the last span, whose trace
+                    # this forward computes anyway: keep it (the buffer the
+                    # backward would fill) instead of recomputing it there
+                    span = _span(T, checkpoint, B * N)
+                    tail = (math.ceil(T / span) - 1) * span
+                    pre = torch.empty((T - tail, B, N), dtype=x.dtype, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1, wt=wt, cur_out=cur, exact=ckpt is not None and cur is None)
+                 ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:
             # the bf16 synapse keeps the bf16 copies of x and W^T (what its GEMMs read)
-            ctx.save_for_backward(xs, w, b, pre, ckpt, wt, cur)
+            ctx.save_for_backward(xs, w, b, pre, ckpt, wt)
         return m_final, out
 
     @staticmethod
@@ -272,22 +322,23 @@ class HipLinearLIFFunction(torch.autograd.Function):
         if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
             return none
         decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
-        xs, w, b, pre, ckpt, wt, cur = ctx.saved_tensors
+        xs, w, b, pre, ckpt, wt = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
         gx, gw, gb = linear_backward(xs, w, b if has_b else None, pre, ckpt, wt, g_m, g_out, decay, threshold,
                                      reset, sid, slope, checkpoint, rate, prec, rule, need_x, need_w,
-                                     need_b and has_b, cur=cur)
+                                     need_b and has_b)
         return gx, gw, gb, None, None, None, None, None, None, None, None, None
 
 
 def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset, sid, slope, checkpoint, rate,
-                    prec, rule, need_x=True, need_w=True, need_b=True, cur=None):
-    """Gradients (dX, dW, db) of the streamed-synapse LIF, chunk by chunk in
-    reverse time: recompute the chunk's pre-reset trace from its checkpoint
-    (``checkpoint=None``: the saved trace ``pre`` covers all T; ``cur``: the
-    forward's saved currents, so no recompute GEMM), reverse the
-    recurrence into G = dL/dI, then ``dX = G W^T`` and ``dW += X^T G`` on
-    the MFMA GEMM and ``db`` as a fixed-order column sum.  ``xs`` is fp32, or
+                    prec, rule, need_x=True, need_w=True, need_b=True):
+    """Gradients (dX, dW, db) of the streamed-synapse LIF, span by span in
+    reverse time: recompute the span's pre-reset trace from its first
+    checkpoint (``checkpoint=None``: the saved trace ``pre`` covers all T;
+    with a checkpoint, ``pre`` if given is the last span's trace, kept by
+    the forward), reverse the recurrence into G = dL/dI, then ``dX = G W^T`` and
+    ``dW += X^T G`` on the MFMA GEMM and ``db`` as a fixed-order column
+    sum.  ``xs`` is fp32, or
     bf16 with ``wt = W^T`` bf16 for the bf16 synapse; ``g_out`` is dL/dspikes
     ``[T, B, N]`` or, with ``rate``, dL/drates ``[B, N]``."""
 
@@ -306,16 +357,25 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         gx = torch.empty((T, B, F), device=dev) if need_x else None
         gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) chunk overwrites it
         gb_acc = torch.zeros((B, N), device=dev) if (need_b and b is not None) else None
-        chunk = T if checkpoint is None else checkpoint
-        G = torch.empty((min(chunk, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
-        scratch = None if checkpoint is None else torch.empty((min(chunk, T), B, N), device=dev)
-        n_chunks = math.ceil(T / chunk)
-        # GEMM recomputes run one chunk ahead on a side stream, into two
-        # alternating trace buffers: chunk k-1's recompute overlaps chunk k's
-        # reverse pass and weight GEMMs (each alone leaves much of the GPU
-        # idle at these sizes).  ready[i]: buffer i holds its chunk's trace;
-        # free[i]: the reverse pass has read buffer i.
-        overlap = checkpoint is not None and cur is None and n_chunks > 1
+        # the reverse pass walks spans of whole checkpoint chunks, as many as
+        # keep a span's trace within _CURRENT_CHUNK_ELEMS: one recompute
+        # (from the span's first checkpoint, which the recurrence carries
+        # through the later ones exactly as the forward did), one reverse
+        # launch and one dX / dW GEMM pair per span instead of per chunk
+        span = T if checkpoint is None else _span(T, checkpoint, BN)
+        per = 1 if checkpoint is None else span // checkpoint  # checkpoint rows per span
+        G = torch.empty((min(span, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
+        n_spans = math.ceil(T / span)
+        tail = pre if checkpoint is not None else None  # the last span's trace, from the forward
+        if tail is not None and tail.shape[0] != T - (n_spans - 1) * span:
+            raise ValueError("the saved trace does not cover the last backward span")
+        recomputes = checkpoint is not None and (tail is None or n_spans > 1)
+        scratch = torch.empty((min(span, T), B, N), device=dev) if recomputes else None
+        # GEMM recomputes run one span ahead on a side stream, into two
+        # alternating trace buffers: span k-1's recompute overlaps span k's
+        # reverse pass and weight GEMMs.  ready[i]: buffer i holds its span's
+        # trace; free[i]: the reverse pass has read buffer i.
+        overlap = checkpoint is not None and n_spans > 1
         if overlap:
             main = torch.cuda.current_stream(dev)
             side = _side_stream(dev)
@@ -327,30 +387,31 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             def recompute(j):
                 i = j % 2
                 with torch.cuda.stream(side):
-                    if j + 2 < n_chunks:
+                    if j + 2 < n_spans:
                         side.wait_event(free[i])
-                    _lif_fwd(xs, w, b, ckpt[j], j * chunk, min(j * chunk + chunk, T), decay, threshold, reset,
+                    _lif_fwd(xs, w, b, ckpt[j * per], j * span, min(j * span + span, T), decay, threshold, reset,
                              slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True)
                     ready[i].record(side)
 
-            recompute(n_chunks - 1)
-        for k in range(n_chunks - 1, -1, -1):
-            t0 = k * chunk
-            t1 = min(t0 + chunk, T)
+            if tail is None:
+                recompute(n_spans - 1)
+        for k in range(n_spans - 1, -1, -1):
+            t0 = k * span
+            t1 = min(t0 + span, T)
             C = t1 - t0
             if checkpoint is None:
                 pre_k = pre
+            elif k == n_spans - 1 and tail is not None:
+                if overlap:
+                    recompute(k - 1)
+                pre_k = tail
             elif overlap:
                 if k > 0:
                     recompute(k - 1)
                 main.wait_event(ready[k % 2])
                 pre_k = bufs[k % 2]
-            elif cur is not None:
-                _recompute_pre(cur[t0:t1], ckpt[k], scratch, T, B, N, t0, t1, decay, threshold, reset, slope, rule,
-                               stream)
-                pre_k = scratch
             else:
-                _lif_fwd(xs, w, b, ckpt[k], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
+                _lif_fwd(xs, w, b, ckpt[k * per], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
                          pre=scratch, wt=wt, exact=True)
                 pre_k = scratch
             _lib.call(
@@ -370,7 +431,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
             if gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_chunks - 1, prec, stream)
+                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream)
         if overlap:
             # every side-stream kernel is behind a ready[] the main stream
             # waited on; the buffers' last users include the side stream

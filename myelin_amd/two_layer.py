@@ -17,17 +17,18 @@ Here both passes walk time in chunks of C steps (the checkpoint size):
   packed variant only their words ``[T, B, ceil(H/32)]``); readout
   ``s_t @ W_o`` + LIF from the carried readout membrane and spike counts.
   Chunk-start membranes of both layers are kept ``[ceil(T/C), B, H + O]``.
-* backward, chunks in reverse: recompute the hidden chunk (pre-reset trace;
-  its spikes, or in the packed variant the stored words read as bits by
-  the readout GEMMs, feed the readout),
-  recompute the readout chunk (from its saved currents when the readout is
-  narrow), reverse the readout recurrence (adjoint
-  carried across chunks), ``dS = G_o @ W_o^T`` for the chunk only, then
-  reverse the hidden recurrence with ``dS`` as its spike gradient.
+* backward, spans of whole chunks in reverse (as many chunks as keep a
+  span's hidden trace within 2**24 elements): recompute the hidden span
+  from its first checkpoint (pre-reset trace; its spikes, or in the packed
+  variant the stored words read as bits by the readout GEMMs, feed the
+  readout), take the readout's trace (saved whole when the readout is
+  narrow, else recomputed), reverse the readout recurrence (adjoint carried
+  across spans), ``dS = G_o @ W_o^T`` for the span only, then reverse the
+  hidden recurrence with ``dS`` as its spike gradient.
 
 So no tensor with T in its shape is written except the input gradient, the
-narrow readout's currents ``[T, B, O]`` and, in the packed variant, the
-packed words -- which its readout GEMMs read directly, so that variant
+narrow readout's pre-reset trace ``[T, B, O]`` and, in the packed variant,
+the packed words -- which its readout GEMMs read directly, so that variant
 never forms dense hidden spikes at all.  The
 arithmetic of each step is that of the one-layer checkpointed path (same
 kernels), so rates and gradients equal those of composing the two
@@ -42,8 +43,16 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _keep_currents, _lif_fwd,
-                               _recompute_pre, _side_stream, _transpose_bf16)
+from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _keep_trace, _lif_fwd, _side_stream,
+                               _transpose_bf16)
+
+# trace budget of a backward span (floats per buffer): the backward walks
+# whole checkpoint chunks, as many at a time as keep each per-span buffer
+# within it.  Half the one-layer budget, since this network is the
+# memory-lean route: at T=2000, B=32, 1024 -> 4096 -> 20 with 45-step chunks,
+# spans of 1 / 2 / 5 chunks measured 19.1 / 17.4 / 16.7 ms per training step
+# at 191 / 303 / 654 MB peak (packed variant).
+_SPAN_ELEMS = 1 << 24
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
@@ -83,8 +92,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         need = any(ctx.needs_input_grad[:5])
         K = math.ceil(T / C)
         L0 = min(C, T)
+        # a narrow readout keeps its whole pre-reset trace [T, B, O] for the
+        # backward, which then recomputes nothing of the readout
+        keep = need and _keep_trace(H, O)
         ck_h = torch.empty((K, B, H), device=dev) if need else None
-        ck_o = torch.empty((K, B, O), device=dev) if need else None
+        ck_o = torch.empty((K, B, O), device=dev) if need and not keep else None
         m_h = torch.zeros((B, H), device=dev)
         m_o = torch.zeros((B, O), device=dev)
         counts = torch.zeros((B, O), device=dev)
@@ -97,10 +109,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         # the packed variant never forms dense hidden spikes: its readout
         # GEMM reads the words
         hs = None if packed_hidden else torch.empty((LG, B, H), device=dev)
-        # a narrow readout keeps all its currents [T, B, O] for the backward
-        # (no readout recompute GEMM there)
-        keep = need and _keep_currents(H, O)
-        cur = torch.empty((T if keep else LG, B, O), device=dev)
+        cur = torch.empty((LG, B, O), device=dev)
+        pre_o = torch.empty((T, B, O), device=dev) if keep else None
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
@@ -114,13 +124,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                      packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
                      ckpt_every=C, wt=wt, exact=need)
             s_in = words[t0:t1] if hs is None else hs[:L]
-            _readout_chunk(cur[t0:t1] if keep else cur[:L], s_in, wo, bo, m_o, m_o, None, counts,
+            _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None if pre_o is None else pre_o[t0:t1], counts,
                            rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
                            stream, exact=need and not keep)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
         if need:
-            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, cur if keep else None)
+            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_o)
         return rates
 
     @staticmethod
@@ -129,7 +139,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         if g_rates is None or not any(ctx.needs_input_grad[:5]):
             return none
         decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
-        xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, cur_o = ctx.saved_tensors
+        xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_all = ctx.saved_tensors
         half = xs.dtype == torch.bfloat16
         need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
         need_hidden = need_x or need_wh or (need_bh and has_bh)
@@ -138,7 +148,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         O = wo.shape[1]
         dev = xs.device
         K = math.ceil(T / C)
-        L0 = min(C, T)
+        # spans of `per` whole chunks (recomputed from the span's first
+        # checkpoints, which the recurrences carry through the later ones
+        # exactly as the forward did)
+        per = max(1, min(K, _SPAN_ELEMS // (C * B * max(H, O))))
+        S = per * C
+        NS = math.ceil(T / S)
+        L0 = min(S, T)
         with torch.cuda.device(dev):
             stream = _lib.stream(dev)
             g_rates = g_rates.float().contiguous()
@@ -146,24 +162,24 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gm_h = torch.zeros((B, H), device=dev) if need_hidden else None
             gx = torch.empty((T, B, F), device=dev) if need_x else None
             whg = _cast_bf16(wh, stream) if (half and need_x) else wh
-            # the first (last-in-time) chunk overwrites the weight gradients
+            # the first (last-in-time) span overwrites the weight gradients
             gwh = torch.empty_like(wh) if need_wh else None
             gwo = torch.empty_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
-            cur = torch.empty((L0, B, O), device=dev) if cur_o is None else None
-            pre_o = torch.empty((L0, B, O), device=dev)
+            cur = torch.empty((L0, B, O), device=dev) if pre_all is None else None
+            pre_o = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             G_o = torch.empty((L0, B, O), device=dev)
             ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
             G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
                    if need_hidden else None)
             # The hidden recompute (its trace, and spikes in the dense
-            # variant) runs one chunk ahead on a side stream into two
-            # alternating buffer sets, overlapping the current chunk's
+            # variant) runs one span ahead on a side stream into two
+            # alternating buffer sets, overlapping the current span's
             # readout and hidden reverse passes and GEMMs.  ready[i]: set i
-            # holds its chunk; free[i]: the chunk using set i is done with it.
+            # holds its span; free[i]: the span using set i is done with it.
             recomputes = need_hidden or words is None
-            nset = 2 if (recomputes and K > 1) else 1
+            nset = 2 if (recomputes and NS > 1) else 1
             hs_b = [None if words is not None else torch.empty((L0, B, H), device=dev) for _ in range(nset)]
             pre_b = [torch.empty((L0, B, H), device=dev) if need_hidden else None for _ in range(nset)]
             main = torch.cuda.current_stream(dev)
@@ -175,26 +191,26 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
 
             def hidden_recompute(j):
                 i = j % nset
-                a0, a1 = j * C, min(j * C + C, T)
+                a0, a1 = j * S, min(j * S + S, T)
                 n = a1 - a0
                 with torch.cuda.stream(side):
-                    if nset == 2 and j + 2 < K:
+                    if nset == 2 and j + 2 < NS:
                         side.wait_event(free[i])
                     pre_j = None if pre_b[i] is None else pre_b[i][:n]
                     if words is not None:
-                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j], 0, n, decay, threshold, reset, slope,
+                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j * per], 0, n, decay, threshold, reset, slope,
                                  _lib.RULE_THRESHOLD, prec, side.cuda_stream, pre=pre_j, wt=wt, exact=True)
                     else:
-                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j], 0, n, decay, threshold, reset, slope,
+                        _lif_fwd(xs[a0:a1], wh, bh, ck_h[j * per], 0, n, decay, threshold, reset, slope,
                                  _lib.RULE_THRESHOLD, prec, side.cuda_stream, spikes=hs_b[i][:n], pre=pre_j, wt=wt,
                                  exact=True)
                     ready[i].record(side)
 
             if recomputes:
-                hidden_recompute(K - 1)
-            for k in range(K - 1, -1, -1):
-                t0 = k * C
-                t1 = min(t0 + C, T)
+                hidden_recompute(NS - 1)
+            for k in range(NS - 1, -1, -1):
+                t0 = k * S
+                t1 = min(t0 + S, T)
                 L = t1 - t0
                 rows = L * B
                 i = k % nset
@@ -204,21 +220,21 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     main.wait_event(ready[i])
                 hs, pre_h = hs_b[i], pre_b[i]
                 s_in = words[t0:t1] if words is not None else hs[:L]
-                if cur_o is not None:
-                    _recompute_pre(cur_o[t0:t1], ck_o[k], pre_o, T, B, O, t0, t1, decay, threshold, reset, slope,
-                                   _lib.RULE_THRESHOLD, stream)
+                if pre_all is not None:
+                    pre_k = pre_all[t0:t1]
                 else:
-                    _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k], None, pre_o[:L], None, None, None, T, t0, t1, C,
-                                   decay, threshold, reset, slope, prec, stream, exact=True)
+                    _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k * per], None, pre_o[:L], None, None, None, T, t0,
+                                   t1, C, decay, threshold, reset, slope, prec, stream, exact=True)
+                    pre_k = pre_o
                 _lib.call(
                     "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_o), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
+                    _lib.ptr(pre_k), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
                     _lib.ptr(gbo_acc),
                     L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
                 if gwo is not None:
                     # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
-                    acc = k != K - 1
+                    acc = k != NS - 1
                     if words is not None:
                         _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, acc, prec, stream,
                               a_bits=True)
@@ -228,7 +244,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     if nset == 2:
                         free[i].record(main)  # dW_o was the last reader of the spikes
                     continue
-                # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this chunk
+                # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this span
                 _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
@@ -241,7 +257,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 if gx is not None:
                     _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
                 if gwh is not None:
-                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != K - 1, prec, stream)
+                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream)
             if nset == 2:
                 # every side-stream kernel is behind a ready[] the main stream
                 # waited on; these tensors' last users include the side stream

@@ -467,3 +467,41 @@ def test_checkpoint_recompute_reproduces_forward_trace_exactly(prec):
     for k in (0, 1, 37, T // C - 1):
         _lif_fwd(xs, w, b, ck[k], k * C, (k + 1) * C, *args, pre=scratch, wt=wt, exact=True)
         assert torch.equal(scratch, pre[k * C:(k + 1) * C]), f"chunk {k}"
+
+
+@pytest.mark.parametrize("C", [5, 6])
+@pytest.mark.parametrize("rate", [False, True])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_small_budget_spans_and_forward_chunks_agree_with_one_span(monkeypatch, C, rate, prec):
+    """With the currents budget shrunk to 20 steps, the forward walks six
+    GEMM chunks (each GEMM on the side stream beside the previous chunk's
+    recurrence) and keeps the last backward span's trace, and the backward
+    walks spans of several chunks (C = 6: 18-step spans, so the kept trace
+    starts inside a forward chunk).  Spikes, rates and dX must equal the
+    one-span run bit for bit; dW and db differ only in summation order."""
+
+    from myelin_amd import linear as L
+
+    _print_case(test="small_budget_spans", C=C, rate=rate, prec=prec)
+    T, B, F, N = 103, 4, 64, 96
+    g = seeded(C * 11 + rate)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float()
+    w = (torch.rand(F, N, generator=g) - 0.45) * 0.5
+    b = torch.rand(N, generator=g) * 0.1
+    go = torch.randn((B, N) if rate else (T, B, N), generator=g)
+    res = []
+    for budget in (None, 20 * B * N):
+        if budget is not None:
+            monkeypatch.setattr(L, "_CURRENT_CHUNK_ELEMS", budget)
+        xd, wd, bd = (t.to(DEV).requires_grad_() for t in (x, w, b))
+        fn = myelin.linear_surrogate_lif_rate_forward if rate else myelin.linear_surrogate_lif_forward
+        kw = {"reduction": "none"} if rate else {}
+        _, out = fn(xd, wd, bd, P, surrogate="atan", surrogate_slope=4.0, checkpoint_size=C,
+                    synapse_precision=prec, **kw)
+        out.backward(go.to(DEV))
+        torch.cuda.synchronize()
+        res.append((to_np(out), to_np(xd.grad), to_np(wd.grad), to_np(bd.grad)))
+    assert 0.0 < res[0][0].mean() < 1.0
+    assert np.array_equal(res[1][0], res[0][0]) and np.array_equal(res[1][1], res[0][1])
+    assert_norm_close(res[1][2], res[0][2], 1e-6, "grad_w across span sizes")
+    assert_norm_close(res[1][3], res[0][3], 1e-6, "grad_b across span sizes")
