@@ -62,6 +62,7 @@ typedef struct ihipStream_t *myelin_stream_t;
 #define MYELIN_DT_I64 5
 #define MYELIN_DT_F64 6
 #define MYELIN_DT_BITS 7 /* packed spike bits: int32 words, bit i of word w = column 32w + i */
+#define MYELIN_DT_BF16X3 8 /* three bf16 planes [3, ...] (hi, mid, lo) whose float sum is exact */
 
 const char *myelin_last_error(void);
 int myelin_abi_version(void);
@@ -231,6 +232,25 @@ int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype,
 int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
                                     int precision);
 
+/*
+ * C (+)= sum over p < parts (1..8) of op(A) op(B_p) (+ bias), B_p = B +
+ * p*b_part, all bf16 operands (alignment as myelin_gemm's bf16 operands,
+ * for every part) on the 128 x 128 bf16 MFMA engine; each part's k range
+ * is summed in turn into the same fp32 accumulators.  With A exactly
+ * representable in bf16 (spikes) and B_p the three planes of
+ * myelin_split_bf16x3, every product is exact and the result is an fp32
+ * GEMM of the unsplit B to fp32 summation accuracy, at bf16 MFMA rate.
+ * Workspace as myelin_gemm_workspace_elems(M, N, K, MYELIN_PREC_BF16).
+ * Replaces: as myelin_gemm_f32 (the fp32 synapse GEMMs when the layer input
+ *   is spikes).
+ */
+int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts,
+                      int64_t b_part, const float *bias, float *C, int64_t M,
+                      int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                      int64_t ldc, int trans_a, int trans_b, int accumulate,
+                      float *workspace, int64_t workspace_elems,
+                      myelin_stream_t stream);
+
 
 /*
  * Streamed synapse fused ahead of the LIF update, over steps
@@ -284,13 +304,34 @@ int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows,
                           int64_t cols, myelin_stream_t stream);
 
 /*
+ * myelin_cast_bf16 that also sets *inexact = 1 (never clears it) when some
+ * element is not a bf16 value the MFMA multiplies exactly (its rounding
+ * changes it, or it is a nonzero denormal).  No counterpart in the
+ * reference.
+ */
+int myelin_cast_bf16_checked(const float *src, uint16_t *dst, int64_t n,
+                             int *inexact, myelin_stream_t stream);
+
+/*
+ * Splits src [rows, cols] fp32 into three bf16 planes hi, mid, lo with
+ * float(hi) + float(mid) + float(lo) == src exactly (hi = bf16(v), mid =
+ * bf16(v - hi), lo = v - hi - mid; exact for |v| >= 2^-110, non-finite v
+ * in hi alone).  Plane p starts at dst + p*rows*cols and is [rows, cols],
+ * or with `transpose` [cols, rows].  No counterpart in the reference.
+ */
+int myelin_split_bf16x3(const float *src, uint16_t *dst, int64_t rows,
+                        int64_t cols, int transpose, myelin_stream_t stream);
+
+/*
  * Reverse recurrence over C steps of a saved pre-reset trace [C, BN]:
  *   d = slope*sigma'(slope*(pre - thr)); gp = gm*((1-s) + (reset-pre)*d)
  *   + g_spike*d; G[j] = gp; gm = gp*decay   (grad_m is in/out)
  * g_spike = grad_spikes[j] (may be NULL) plus grad_rates/T_total (may be
  * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.  G is written
  * as g_dtype MYELIN_DT_F32, or MYELIN_DT_BF16 (round to nearest even, the
- * rounding the bf16 GEMMs apply) when only bf16 GEMMs read it.
+ * rounding the bf16 GEMMs apply) when only bf16 GEMMs read it, or
+ * MYELIN_DT_BF16X3: three bf16 planes [3, C, BN] as myelin_split_bf16x3
+ * writes them, for myelin_gemm_parts.
  * Replaces: the reverse loops of the torch stream / checkpoint / rate
  *   Functions (autograd.py:540-556,694-715,857-883) and
  *   _linear_surrogate_lif_checkpoint_backward_chunk_packed_spikes_kernel

@@ -22,6 +22,7 @@ RULE_THRESHOLD, RULE_SURROGATE = 0, 1
 SG_NONE = 6
 PREC = {"fp32": 0, "bf16": 1}
 DT_BITS = 7  # packed spike bits (int32 words) as a GEMM operand
+DT_BF16X3 = 8  # three bf16 planes summing exactly to an fp32 tensor
 DT = {
     torch.float32: 0,
     torch.float16: 1,
@@ -55,6 +56,9 @@ SIGNATURES: dict[str, list] = {
     "myelin_linear_lif_fwd": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_linear_lif_fwd_bf16": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _P],
     "myelin_cast_bf16": [_P, _P, _I64, _P],
+    "myelin_cast_bf16_checked": [_P, _P, _I64, _P, _P],
+    "myelin_split_bf16x3": [_P, _P, _I64, _I64, _INT, _P],
+    "myelin_gemm_parts": [_P, _P, _INT, _I64, _P, _P] + [_I64] * 6 + [_INT] * 3 + [_P, _I64, _P],
     "myelin_transpose_bf16": [_P, _P, _I64, _I64, _P],
     "myelin_linear_pre_bwd": [_P] * 5 + [_INT, _P] + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],

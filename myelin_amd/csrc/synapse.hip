@@ -334,6 +334,10 @@ struct GemmArgs {
   float *ws;          // [splits, M, N] when split
   int64_t M, N, K, lda, ldb, ldc, kchunk;
   int accumulate, splits;
+  // bf16 operands on the 128 x 128 kernel only: C (+)= sum over p < parts of
+  // op(A) op(B + p * b_part), each part's k range summed in turn
+  int parts = 1;
+  int64_t b_part = 0;
 };
 
 // Writes one wave's 32 x 32 accumulator tile (rows row0 + acc_row(r, lane),
@@ -998,6 +1002,13 @@ struct BigLoader {
   // fast() addresses are valid: the tile has a row (KC) / four columns (MN)
   __device__ __forceinline__ bool fast_ok() const { return KC ? mn_lim >= 1 : mn_lim >= 4; }
 
+  // move to the same tile of another operand laid out like this one, d
+  // elements further on
+  __device__ __forceinline__ void shift(int64_t d) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) q[e] += d;
+  }
+
   template <int d>
   __device__ __forceinline__ void store(typename Prec<PREC>::T (*dst)[BigStage<PREC>::LD]) const {
     if constexpr (KC) {
@@ -1174,8 +1185,9 @@ __device__ __forceinline__ void big_tile(uint32_t bid, uint32_t nblk, uint32_t t
 }
 
 // BM x BN output tile, one wave per 64 x 64 quarter: (BM/64) x (BN/64)
-// waves of 2 x 2 MFMA blocks.
-template <int PREC, bool TA, bool TB, typename S, int BM, int BN>
+// waves of 2 x 2 MFMA blocks.  MP: bf16 operands summing g.parts B parts
+// (a separate instantiation, so the one-part kernels keep their registers).
+template <int PREC, bool TA, bool TB, typename S, int BM, int BN, bool MP = false>
 __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
   constexpr int NT = BM * BN / 64;
   __shared__ BigStage<PREC, BM, BN> st[2];
@@ -1202,7 +1214,16 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
+  if constexpr (MP) {
+    static_assert(sizeof(S) == 2, "B parts are a bf16-operand feature");
+    // the same k range of each B part in turn
+    for (int p = 0; p < g.parts; ++p) {
+      if (p > 0) lb.shift(g.b_part);
+      big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
+    }
+  } else {
+    big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
+  }
 
   // (the per-element form measures faster here than store_acc's)
 #pragma unroll
@@ -1600,12 +1621,40 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
   }
 }
 
+// Three bf16 values whose float sum is exactly v: h = bf16(v) (nearest
+// even), m = bf16(v - h), l = v - h - m.  v - h is exact and has at most 16
+// significant bits, so after m at most 8 remain and l is exact as well (for
+// |v| >= 2^-110; below that l would be subnormal in bf16).  Non-finite v:
+// h carries it, m = l = 0.
+__device__ __forceinline__ void split3(float v, uint16_t &h, uint16_t &m, uint16_t &l) {
+  const __bf16 bh = static_cast<__bf16>(v);
+  if (!__builtin_isfinite(v)) {
+    h = __builtin_bit_cast(uint16_t, bh);
+    m = l = 0;
+    return;
+  }
+  const float r1 = v - static_cast<float>(bh);
+  const __bf16 bm = static_cast<__bf16>(r1);
+  const float r2 = r1 - static_cast<float>(bm);
+  h = __builtin_bit_cast(uint16_t, bh);
+  m = __builtin_bit_cast(uint16_t, bm);
+  l = __builtin_bit_cast(uint16_t, static_cast<__bf16>(r2));
+}
+
+// v is a bf16 value the MFMA multiplies exactly: its bf16 rounding returns
+// it, and it is zero or normal (denormals may be flushed)
+__device__ __forceinline__ bool bf16_exact(float v) {
+  const float a = __builtin_fabsf(v);
+  return static_cast<float>(static_cast<__bf16>(v)) == v && (a == 0.0f || a >= 1.17549435e-38f);
+}
+
 struct PreBwdArgs {
   const float *pre;     // [C, BN]
   const float *gs;      // [C, BN] or null
   const float *grate;   // [BN] or null
   float *gm;            // [BN] in/out
-  void *G;              // [C, BN] float, or bf16 bits when the GEMMs read bf16
+  void *G;              // [C, BN] float, or bf16 bits when the GEMMs read bf16, or three
+                        // bf16 planes [3, C, BN] summing exactly to G
   float *gbias_acc;     // [BN] or null (accumulated)
   int64_t C, BN;
   float decay, thr, reset, slope, rate_denominator;
@@ -1620,7 +1669,7 @@ struct PreBwdArgs {
 // no load is predicated.
 constexpr int kPipe = 16;
 
-template <int SID, bool GS, bool GH>
+template <int SID, bool GS, int GM>
 __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, float pre, float gsv,
                                              float gstep, float &gm, float &gb) {
   const float c = p.slope * (pre - p.thr);
@@ -1630,17 +1679,27 @@ __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int
   float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
   if constexpr (GS) gp = gp + gsv * d;
   if (p.grate != nullptr) gp = gp + gstep * d;
-  if constexpr (GH)
+  if constexpr (GM == 1) {
     static_cast<uint16_t *>(p.G)[j * p.BN + i] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(gp));
-  else
+  } else if constexpr (GM == 2) {
+    uint16_t h, m, l;
+    split3(gp, h, m, l);
+    uint16_t *g16 = static_cast<uint16_t *>(p.G) + j * p.BN + i;
+    const int64_t plane = p.C * p.BN;
+    g16[0] = h;
+    g16[plane] = m;
+    g16[2 * plane] = l;
+  } else {
     static_cast<float *>(p.G)[j * p.BN + i] = gp;
+  }
   gb = gb + gp;
   gm = gp * p.decay;
 }
 
-// reverse time: relative index r = C - 1 - j.  GH: G is written as bf16
-// (rounded as the bf16 GEMMs would round it).
-template <int SID, bool GS, bool GH>
+// reverse time: relative index r = C - 1 - j.  GM: G is written as fp32
+// (0), as bf16 rounded as the bf16 GEMMs would round it (1), or as three
+// bf16 planes whose sum is G exactly (2).
+template <int SID, bool GS, int GM>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= p.BN) return;
@@ -1671,7 +1730,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     }
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      if (u < f) pre_bwd_step<SID, GS, GH>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      if (u < f) pre_bwd_step<SID, GS, GM>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
@@ -1689,7 +1748,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      pre_bwd_step<SID, GS, GH>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      pre_bwd_step<SID, GS, GM>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
@@ -1869,7 +1928,10 @@ void launch_big(const GemmArgs &g, bool half, dim3 grid, hipStream_t s) {
   constexpr int NT = BM * BN / 64;
   if constexpr (PREC == 1) {
     if (half) {
-      gemm_big<1, TA, TB, uint16_t, BM, BN><<<grid, dim3(NT), 0, s>>>(g);
+      if (g.parts > 1)
+        gemm_big<1, TA, TB, uint16_t, BM, BN, true><<<grid, dim3(NT), 0, s>>>(g);
+      else
+        gemm_big<1, TA, TB, uint16_t, BM, BN><<<grid, dim3(NT), 0, s>>>(g);
       return;
     }
   }
@@ -2032,15 +2094,22 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
 }
 
 template <int SID>
-void launch_pre_bwd(const PreBwdArgs &a, bool gs, bool gh, dim3 grid, hipStream_t s) {
-  if (gs && gh)
-    linear_pre_bwd<SID, true, true><<<grid, dim3(256), 0, s>>>(a);
-  else if (gs)
-    linear_pre_bwd<SID, true, false><<<grid, dim3(256), 0, s>>>(a);
-  else if (gh)
-    linear_pre_bwd<SID, false, true><<<grid, dim3(256), 0, s>>>(a);
-  else
-    linear_pre_bwd<SID, false, false><<<grid, dim3(256), 0, s>>>(a);
+void launch_pre_bwd(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
+  if (gs) {
+    if (gm == 2)
+      linear_pre_bwd<SID, true, 2><<<grid, dim3(256), 0, s>>>(a);
+    else if (gm == 1)
+      linear_pre_bwd<SID, true, 1><<<grid, dim3(256), 0, s>>>(a);
+    else
+      linear_pre_bwd<SID, true, 0><<<grid, dim3(256), 0, s>>>(a);
+  } else {
+    if (gm == 2)
+      linear_pre_bwd<SID, false, 2><<<grid, dim3(256), 0, s>>>(a);
+    else if (gm == 1)
+      linear_pre_bwd<SID, false, 1><<<grid, dim3(256), 0, s>>>(a);
+    else
+      linear_pre_bwd<SID, false, 0><<<grid, dim3(256), 0, s>>>(a);
+  }
 }
 
 template <bool PRE, bool SPK>
@@ -2113,6 +2182,34 @@ extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtyp
   hipStream_t s = myelin::as_hip(stream);
   if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s, bits);
   return launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s, bits);
+}
+
+extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts, int64_t b_part, const float *bias,
+                                 float *C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                 int trans_a, int trans_b, int accumulate, float *workspace, int64_t workspace_elems,
+                                 myelin_stream_t stream) {
+  if (parts < 1 || parts > 8) return myelin::invalid("gemm_parts: parts must be in [1, 8]");
+  if (parts > 1 && b_part < 0) return myelin::invalid("gemm_parts: negative part stride");
+  if (M < 0 || N < 0 || K < 0) return myelin::invalid("gemm_parts: negative size");
+  if (M == 0 || N == 0) return MYELIN_OK;
+  if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm_parts: null pointer");
+  if (ldc < N) return myelin::invalid("gemm_parts: ldc < N");
+  if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N)) return myelin::invalid("gemm_parts: bad leading dim");
+  if (workspace_elems < 0) return myelin::invalid("gemm_parts: negative workspace size");
+  // every part must satisfy the bf16 loaders' alignment, as B itself does
+  if (!bf16_aligned(A, lda, !trans_a) || !bf16_aligned(B, ldb, trans_b != 0) ||
+      (parts > 1 && !bf16_aligned(B + b_part, ldb, trans_b != 0)))
+    return myelin::invalid("gemm_parts: bfloat16 operand rows must be 16-byte (k-contiguous) or 8-byte aligned");
+  GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
+  g.parts = parts;
+  g.b_part = b_part;
+  hipStream_t s = myelin::as_hip(stream);
+  if (K == 0) {  // C = (accumulate ? C : 0) + bias
+    g.splits = 0;
+    splitk_reduce<<<dim3(cdiv(M * N, 256)), dim3(256), 0, s>>>(g);
+    return myelin::launched("gemm_parts (K = 0)");
+  }
+  return launch_gemm<1>(g, trans_a, trans_b, true, workspace_elems, s);
 }
 
 extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
@@ -2251,13 +2348,14 @@ extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
                                      int surrogate_id, int rule, myelin_stream_t stream) {
   if (C < 1 || BN < 1) return myelin::invalid("linear_pre_bwd: C and BN must be positive");
   if (pre == nullptr || grad_m == nullptr || G == nullptr) return myelin::invalid("linear_pre_bwd: null pointer");
-  if (g_dtype != MYELIN_DT_F32 && g_dtype != MYELIN_DT_BF16)
-    return myelin::invalid("linear_pre_bwd: G must be float32 or bfloat16");
+  if (g_dtype != MYELIN_DT_F32 && g_dtype != MYELIN_DT_BF16 && g_dtype != MYELIN_DT_BF16X3)
+    return myelin::invalid("linear_pre_bwd: G must be float32, bfloat16 or three bfloat16 planes");
   PreBwdArgs a{pre, grad_spikes, grad_rates, grad_m, G, gbias_acc, C, BN, decay, threshold, reset, slope,
                static_cast<float>(T_total), rule};
   const dim3 grid(cdiv(BN, 256));
   hipStream_t s = myelin::as_hip(stream);
-  const bool gs = grad_spikes != nullptr, gh = g_dtype == MYELIN_DT_BF16;
+  const bool gs = grad_spikes != nullptr;
+  const int gh = g_dtype == MYELIN_DT_BF16X3 ? 2 : g_dtype == MYELIN_DT_BF16 ? 1 : 0;
   switch (surrogate_id) {
     case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, gh, grid, s); break;
     case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, gh, grid, s); break;
@@ -2345,6 +2443,70 @@ __global__ __launch_bounds__(256) void cast_bf16(const float *__restrict__ src, 
   }
 }
 
+// cast_bf16 that also reports whether every element was bf16-exact:
+// inexact[0] is set to 1 by any wave holding an inexact element (and never
+// cleared here)
+__global__ __launch_bounds__(256) void cast_bf16_checked(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                         int64_t n, int *__restrict__ inexact) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  bool bad = false;
+  if (i + 8 <= n) {
+    const f4 a = *reinterpret_cast<const f4 *>(src + i);
+    const f4 b = *reinterpret_cast<const f4 *>(src + i + 4);
+    bad = !(bf16_exact(a.x) && bf16_exact(a.y) && bf16_exact(a.z) && bf16_exact(a.w) && bf16_exact(b.x) &&
+            bf16_exact(b.y) && bf16_exact(b.z) && bf16_exact(b.w));
+    const u4 o{to_bf16(a.x) | (unsigned)to_bf16(a.y) << 16, to_bf16(a.z) | (unsigned)to_bf16(a.w) << 16,
+               to_bf16(b.x) | (unsigned)to_bf16(b.y) << 16, to_bf16(b.z) | (unsigned)to_bf16(b.w) << 16};
+    *reinterpret_cast<u4 *>(dst + i) = o;
+  } else {
+    for (int64_t j = i; j < n; ++j) {
+      bad = bad || !bf16_exact(src[j]);
+      dst[j] = to_bf16(src[j]);
+    }
+  }
+  if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) inexact[0] = 1;
+}
+
+// src [rows, cols] -> three bf16 planes (split3), plane p at dst + p*rows*cols,
+// each [rows, cols] (row-major like src)
+__global__ __launch_bounds__(256) void split_bf16x3(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                    int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint16_t h, m, l;
+  split3(src[i], h, m, l);
+  dst[i] = h;
+  dst[n + i] = m;
+  dst[2 * n + i] = l;
+}
+
+// src [rows, cols] -> three transposed bf16 planes [cols, rows] through a
+// 64 x 64 LDS tile
+__global__ __launch_bounds__(256) void split_bf16x3_t(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                      int64_t rows, int64_t cols) {
+  __shared__ float tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t plane = rows * cols;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
+    tile[ty + 4 * k][tx] = (r < rows && c < cols) ? src[r * cols + c] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < cols && r < rows) {
+      uint16_t h, m, l;
+      split3(tile[tx][ty + 4 * k], h, m, l);
+      dst[c * rows + r] = h;
+      dst[plane + c * rows + r] = m;
+      dst[2 * plane + c * rows + r] = l;
+    }
+  }
+}
+
 // dst[c, r] = bf16(src[r, c]) through a 64 x 64 LDS tile
 __global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
                                                       int64_t rows, int64_t cols) {
@@ -2374,6 +2536,33 @@ extern "C" int myelin_cast_bf16(const float *src, uint16_t *dst, int64_t n, myel
     return myelin::invalid("cast_bf16: src and dst must be 16-byte aligned");
   cast_bf16<<<dim3(cdiv(cdiv(n, 8), 256)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, n);
   return myelin::launched("cast_bf16");
+}
+
+extern "C" int myelin_cast_bf16_checked(const float *src, uint16_t *dst, int64_t n, int *inexact,
+                                        myelin_stream_t stream) {
+  if (n < 0) return myelin::invalid("cast_bf16_checked: negative size");
+  if (n == 0) return MYELIN_OK;
+  if (src == nullptr || dst == nullptr || inexact == nullptr) return myelin::invalid("cast_bf16_checked: null pointer");
+  if (!myelin::aligned(src, 16) || !myelin::aligned(dst, 16))
+    return myelin::invalid("cast_bf16_checked: src and dst must be 16-byte aligned");
+  cast_bf16_checked<<<dim3(cdiv(cdiv(n, 8), 256)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, n, inexact);
+  return myelin::launched("cast_bf16_checked");
+}
+
+extern "C" int myelin_split_bf16x3(const float *src, uint16_t *dst, int64_t rows, int64_t cols, int transpose,
+                                   myelin_stream_t stream) {
+  if (rows < 0 || cols < 0) return myelin::invalid("split_bf16x3: negative size");
+  if (rows == 0 || cols == 0) return MYELIN_OK;
+  if (src == nullptr || dst == nullptr) return myelin::invalid("split_bf16x3: null pointer");
+  hipStream_t s = myelin::as_hip(stream);
+  if (transpose) {
+    if (cdiv(rows, 64) > 65535) return myelin::invalid("split_bf16x3: too many rows");
+    split_bf16x3_t<<<dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0, s>>>(src, dst, rows, cols);
+  } else {
+    if (cdiv(rows * cols, 256) > 0x7fffffff) return myelin::invalid("split_bf16x3: too many elements");
+    split_bf16x3<<<dim3(cdiv(rows * cols, 256)), dim3(256), 0, s>>>(src, dst, rows * cols);
+  }
+  return myelin::launched("split_bf16x3");
 }
 
 extern "C" int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows, int64_t cols,

@@ -74,6 +74,50 @@ def _transpose_bf16(w, stream):
     return out
 
 
+def _gemm_parts(A, B, parts, b_part, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, stream, bias=None,
+                split=True):
+    """C (+)= sum_p op(A) op(B_p) (+ bias), bf16 operands, B_p = B + p*b_part
+    (elements); ``split`` as in _gemm."""
+
+    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, _lib.PREC["bf16"]) if split else 0
+    ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
+    _lib.call("myelin_gemm_parts", _lib.ptr(A), _lib.ptr(B), parts, b_part, _lib.ptr(bias), _lib.ptr(C), M, N, K,
+              lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), _lib.ptr(ws), n_ws, stream)
+
+
+# exact bf16 split of an fp32 synapse: tried for products of at least this
+# many multiply-adds (the input check costs one host synchronisation)
+_SPLIT_MIN_MACS = 1 << 32
+
+
+def _split_synapse(x, w, stream):
+    """The fp32 synapse on the bf16 MFMA, exactly: when every input value is
+    a bf16 value (spikes, small integers), ``x @ W = x @ W_hi + x @ W_mid +
+    x @ W_lo`` with the three bf16 planes of W summing exactly to W, so every
+    product is exact and only the fp32 summation rounds -- at the bf16
+    engine's rate (about 5x the fp32 one per pass).  Returns the bf16 copy
+    of x and the transposed planes ``[3, N, F]``, or None when some input
+    value is not bf16-exact (then the fp32 GEMMs run)."""
+
+    xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=x.device)
+    _lib.call("myelin_cast_bf16_checked", _lib.ptr(x), _lib.ptr(xb), x.numel(), _lib.ptr(flag), stream)
+    if int(flag.item()) != 0:
+        return None
+    F, N = w.shape
+    w3 = torch.empty((3, N, F), dtype=torch.bfloat16, device=w.device)
+    _lib.call("myelin_split_bf16x3", _lib.ptr(w), _lib.ptr(w3), F, N, 1, stream)
+    return xb, w3
+
+
+def _split_eligible(prec: int, T: int, B: int, F: int, N: int) -> bool:
+    """fp32 synapse on the chunked route with rows the bf16 loaders take and
+    enough work to amortise the input check."""
+
+    return (prec == _lib.PREC["fp32"] and not _fused(B, N) and F % 8 == 0 and N % 8 == 0
+            and T * B * F * N >= _SPLIT_MIN_MACS)
+
+
 class HipLinearFunction(torch.autograd.Function):
     """``inputs @ weight + bias`` on the MFMA GEMM (LinearSynapse, modules.py:112-133).
 
@@ -176,10 +220,13 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
 
     T, B, F = x.shape
     half = x.dtype == torch.bfloat16
-    N = wt.shape[0] if half else w.shape[1]
+    parts = half and wt.ndim == 3  # exact split: wt holds the planes [3, N, F]
+    N = wt.shape[-2] if half else w.shape[1]
     if _fused(B, N):
         if pre_from not in (None, t0):
             raise ValueError("pre_from is a chunked-route option")
+        if parts:
+            raise ValueError("the split synapse is a chunked-route option")
         outs = (_lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
                 _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule)
         if half:
@@ -212,7 +259,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
 
     def gemm(c0, c1, cur, s):
         rows = (c1 - c0) * B
-        if half:
+        if parts:
+            _gemm_parts(x[c0:c1], wt, 3, N * F, cur, rows, N, F, F, F, N, False, True, False, s, bias=b,
+                        split=not exact)
+        elif half:
             _gemm(x[c0:c1], wt, cur, rows, N, F, F, F, N, False, True, False, prec, s, bias=b, split=not exact)
         else:
             _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, s, bias=b, split=not exact)
@@ -288,6 +338,10 @@ class HipLinearLIFFunction(torch.autograd.Function):
         need = any(ctx.needs_input_grad[:3])
         half = _half(prec, F, N)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
+        if not half and _split_eligible(prec, T, B, F, N):
+            sp = _split_synapse(x, w, stream)
+            if sp is not None:
+                xs, wt = sp
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
         if checkpoint is not None and _keep_trace(F, N):
@@ -346,7 +400,8 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
     N = w.shape[1]
     BN = B * N
     dev = xs.device
-    half = xs.dtype == torch.bfloat16
+    parts = wt is not None and wt.ndim == 3  # exact split: xs bf16-exact, wt the planes of W
+    half = xs.dtype == torch.bfloat16 and not parts
     with torch.cuda.device(dev):
         stream = _lib.stream(dev)
         wg = _cast_bf16(w, stream) if (half and need_x) else w
@@ -365,6 +420,12 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         span = T if checkpoint is None else _span(T, checkpoint, BN)
         per = 1 if checkpoint is None else span // checkpoint  # checkpoint rows per span
         G = torch.empty((min(span, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
+        # exact split: dW reads G as three bf16 planes [3, C, B, N] (C the
+        # span's steps), written by the reverse pass itself unless dX needs
+        # the fp32 G as well
+        G3 = torch.empty(3 * min(span, T) * BN, dtype=torch.bfloat16, device=dev) if parts and need_w else None
+        if G3 is not None and not need_x:
+            G = G3
         n_spans = math.ceil(T / span)
         tail = pre if checkpoint is not None else None  # the last span's trace, from the forward
         if tail is not None and tail.shape[0] != T - (n_spans - 1) * span:
@@ -417,7 +478,8 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             _lib.call(
                 "myelin_linear_pre_bwd",
                 _lib.ptr(pre_k), _lib.ptr(g_spikes[t0:t1]) if g_spikes is not None else None,
-                _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT[G.dtype], _lib.ptr(gb_acc),
+                _lib.ptr(g_rates), _lib.ptr(gm), _lib.ptr(G), _lib.DT_BF16X3 if G is G3 else _lib.DT[G.dtype],
+                _lib.ptr(gb_acc),
                 C, BN, T, decay, threshold, reset, slope, sid, rule, stream,
             )
             if overlap:
@@ -429,7 +491,12 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             if gx is not None:
                 # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
                 _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
-            if gw is not None:
+            if gw is not None and parts:
+                if G is not G3:
+                    _lib.call("myelin_split_bf16x3", _lib.ptr(G), _lib.ptr(G3), rows, N, 0, stream)
+                _gemm_parts(xs[t0:t1], G3, 3, rows * N, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1,
+                            stream)
+            elif gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
                 _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream)
         if overlap:

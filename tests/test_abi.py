@@ -92,3 +92,27 @@ def test_gemm_workspace_size_is_host_only_and_covers_the_split():
     assert lib.myelin_gemm_workspace_elems(12800, 2048, 784, _lib.PREC["bf16"]) == 0
     assert lib.myelin_gemm_workspace_elems(784, 2048, 100, _lib.PREC["fp32"]) == 0
     assert lib.myelin_gemm_workspace_elems(0, 5, 5, 0) == 0
+
+
+def test_split_synapse_entry_points_validate_on_the_host():
+    with pytest.raises(ValueError, match="parts must be in"):
+        _lib.call("myelin_gemm_parts", 16, 16, 0, 0, None, 16, 4, 4, 4, 4, 4, 4, 0, 0, 0, None, 0, None)
+    with pytest.raises(ValueError, match="parts must be in"):
+        _lib.call("myelin_gemm_parts", 16, 16, 9, 64, None, 16, 4, 4, 4, 4, 4, 4, 0, 0, 0, None, 0, None)
+    with pytest.raises(ValueError, match="16-byte"):  # k-contiguous A rows of 4 bf16 are 8 bytes
+        _lib.call("myelin_gemm_parts", 16, 16, 3, 64, None, 16, 4, 4, 4, 4, 4, 4, 0, 0, 0, None, 0, None)
+    with pytest.raises(ValueError, match="bad leading dim"):
+        _lib.call("myelin_gemm_parts", 16, 16, 3, 64, None, 16, 4, 4, 8, 4, 4, 4, 0, 0, 0, None, 0, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("myelin_cast_bf16_checked", 16, 16, 8, None, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _lib.call("myelin_cast_bf16_checked", 4, 16, 8, 16, None)
+    with pytest.raises(ValueError, match="negative size"):
+        _lib.call("myelin_split_bf16x3", 16, 16, -1, 4, 0, None)
+    with pytest.raises(ValueError, match="G must be float32, bfloat16 or three"):
+        _lib.call("myelin_linear_pre_bwd", 16, None, None, 16, 16, 99, None, 4, 4, 4, 0.9, 1.0, 0.0, 5.0, 1, 0,
+                  None)
+    # empty problems are valid no-ops
+    assert _lib.load().myelin_split_bf16x3(None, None, 0, 5, 1, None) == 0
+    assert _lib.load().myelin_gemm_parts(None, None, 3, 0, None, None, 0, 4, 4, 4, 4, 4, 0, 0, 0, None, 0,
+                                         None) == 0

@@ -1,0 +1,276 @@
+"""GPU parity of the exact bf16 split of the fp32 synapse.
+
+When a layer's input is bf16-exact (spikes), ``x @ W`` runs as
+``x @ W_hi + x @ W_mid + x @ W_lo`` on the bf16 MFMA, with the three planes
+summing exactly to W.  Bars:
+* the planes (W and the reverse pass's G) sum back to the fp32 value bit
+  for bit, and the checked cast flags every non-exact input;
+* the multi-part GEMM within 1e-5 (max-norm relative) of the float64
+  product of the unsplit operands, so within fp32 GEMM accuracy;
+* layers on the split path against the oracle as the fp32 layers are:
+  rasters >= 99.99 % equal, membranes within 1e-5, gradients within 1e-4,
+  and against the fp32-engine run of the same layer within 1e-5;
+* a checkpointed recompute on the split path equals the forward's trace
+  bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import myelin_amd as myelin
+from myelin_amd import _lib
+from myelin_amd import linear as L
+from oracle import torch_ref as R
+from tests.helpers import assert_norm_close, raster_agreement, seeded, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+P = myelin.LIFParams(tau_mem=9.0, threshold=0.7, reset=-0.2)
+
+
+def _print_case(**kw):
+    print("case:", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _planes_sum(planes):
+    """float(hi) + float(mid) + float(lo) in fp32, in that order."""
+
+    f = planes.float()
+    return (f[0] + f[1]) + f[2]
+
+
+@pytest.mark.parametrize("transpose", [0, 1])
+def test_split_planes_sum_back_exactly(transpose):
+    _print_case(test="split_planes", transpose=transpose)
+    g = seeded(31 + transpose)
+    rows, cols = 130, 77
+    w = torch.randn(rows, cols, generator=g) * torch.exp2(torch.randint(-40, 40, (rows, cols), generator=g).float())
+    w[0, :4] = torch.tensor([0.0, -0.0, 1.0, -3.0])
+    wd = w.to(DEV)
+    out = torch.empty(3 * rows * cols, dtype=torch.bfloat16, device=DEV)
+    _lib.call("myelin_split_bf16x3", _lib.ptr(wd), _lib.ptr(out), rows, cols, transpose, _lib.stream(wd.device))
+    planes = out.view(3, cols, rows) if transpose else out.view(3, rows, cols)
+    back = _planes_sum(planes).cpu()
+    assert torch.equal(back.t() if transpose else back, w)
+    # the high plane is the nearest bf16 value, as torch rounds
+    hi = planes[0].cpu()
+    assert torch.equal(hi.t() if transpose else hi, w.to(torch.bfloat16))
+
+
+def test_split_of_non_finite_values_keeps_them_in_the_high_plane():
+    _print_case(test="split_non_finite")
+    w = torch.tensor([[float("inf"), -float("inf"), 2.5, float("nan")]], device=DEV)
+    out = torch.empty(12, dtype=torch.bfloat16, device=DEV)
+    _lib.call("myelin_split_bf16x3", _lib.ptr(w), _lib.ptr(out), 1, 4, 0, _lib.stream(w.device))
+    p = out.view(3, 4).float().cpu()
+    assert p[0, 0] == float("inf") and p[0, 1] == -float("inf") and p[0, 2] == 2.5 and torch.isnan(p[0, 3])
+    assert torch.equal(p[1:, :2], torch.zeros(2, 2))
+
+
+@pytest.mark.parametrize("case", ["spikes", "integers", "odd_integer", "random", "denormal", "nan", "tail"])
+def test_checked_cast_flags_exactly_the_inexact_inputs(case):
+    _print_case(test="checked_cast", case=case)
+    g = seeded(7)
+    n = 4099 if case == "tail" else 4096
+    x = (torch.rand(n, generator=g) < 0.1).float()
+    expect = 0
+    if case == "integers":
+        x = torch.randint(-256, 257, (n,), generator=g).float()  # 8 significant bits: |k| <= 256 are exact
+    elif case == "odd_integer":
+        x[9] = 257.0  # needs 9 significant bits
+        expect = 1
+    elif case == "random":
+        x = torch.randn(n, generator=g)
+        expect = 1
+    elif case == "denormal":
+        x[17] = 1e-40
+        expect = 1
+    elif case == "nan":
+        x[4000] = float("nan")
+        expect = 1
+    elif case == "tail":
+        x[n - 1] = 0.1  # in the scalar tail of the last thread
+        expect = 1
+    xd = x.to(DEV)
+    xb = torch.empty(n, dtype=torch.bfloat16, device=DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.call("myelin_cast_bf16_checked", _lib.ptr(xd), _lib.ptr(xb), n, _lib.ptr(flag), _lib.stream(xd.device))
+    assert int(flag.item()) == expect
+    got, want = xb.cpu(), x.to(torch.bfloat16)
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan) and torch.equal(got[~nan], want[~nan])
+
+
+# bf16 rows: k-contiguous ones a multiple of 8 elements, mn-contiguous ones of 4
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (300, 260, 1000), (136, 132, 72), (64, 200, 3000),
+                                   (1000, 136, 24)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("parts", [1, 3])
+def test_gemm_parts_matches_float64(M, N, K, ta, tb, parts):
+    _print_case(test="gemm_parts", M=M, N=N, K=K, ta=ta, tb=tb, parts=parts)
+    g = seeded(M + 3 * N + 7 * K + parts)
+    A = torch.randn((K, M) if ta else (M, K), generator=g).to(torch.bfloat16)
+    Bs = torch.randn((parts, N, K) if tb else (parts, K, N), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    a64 = (A.t() if ta else A).double()
+    ref = sum(a64 @ (Bs[p].t() if tb else Bs[p]).double() for p in range(parts))
+    stream = _lib.stream(torch.device(DEV))
+    Ad, Bd = A.to(DEV), Bs.to(DEV)
+    for acc in (False, True):
+        for split in (False, True):
+            C = C0.clone().to(DEV)
+            L._gemm_parts(Ad, Bd, parts, Bs[0].numel(), C, M, N, K, M if ta else K, K if tb else N, N, ta, tb, acc,
+                          stream, bias=bias.to(DEV), split=split)
+            want = ref + bias.double() + (C0.double() if acc else 0.0)
+            assert_norm_close(to_np(C), want.numpy(), 1e-5, f"acc={acc} split={split}")
+
+
+def test_gemm_parts_equals_the_concatenated_k_product():
+    """Three parts sum like one product over K' = 3K whose A repeats (each
+    part's k range in turn, K a whole number of 64-wide stages): the same
+    stages in the same order, so bit for bit."""
+
+    _print_case(test="gemm_parts_concat")
+    M, N, K = 512, 384, 512
+    g = seeded(99)
+    A = (torch.rand(M, K, generator=g) < 0.3).to(torch.bfloat16)
+    Bs = torch.randn(3, K, N, generator=g).to(torch.bfloat16)
+    stream = _lib.stream(torch.device(DEV))
+    C1 = torch.empty(M, N, device=DEV)
+    L._gemm_parts(A.to(DEV), Bs.to(DEV), 3, K * N, C1, M, N, K, K, N, N, False, False, False, stream, split=False)
+    A3 = torch.cat([A, A, A], dim=1).to(DEV)
+    C2 = torch.empty(M, N, device=DEV)
+    L._gemm(A3, Bs.reshape(3 * K, N).to(DEV), C2, M, N, 3 * K, 3 * K, N, N, False, False, False,
+            _lib.PREC["bf16"], stream, split=False)
+    assert torch.equal(C1, C2)
+
+
+def test_reverse_pass_planes_sum_to_the_fp32_gradient():
+    _print_case(test="pre_bwd_planes")
+    C, BN = 37, 3000
+    g = seeded(5)
+    pre = (torch.randn(C, BN, generator=g) + 0.7).to(DEV)
+    gs = torch.randn(C, BN, generator=g).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    outs = []
+    for dt in (_lib.DT[torch.float32], _lib.DT_BF16X3):
+        gm = torch.zeros(BN, device=DEV)
+        G = torch.empty(C * BN * (3 if dt == _lib.DT_BF16X3 else 1), device=DEV,
+                        dtype=torch.bfloat16 if dt == _lib.DT_BF16X3 else torch.float32)
+        _lib.call("myelin_linear_pre_bwd", _lib.ptr(pre), _lib.ptr(gs), None, _lib.ptr(gm), _lib.ptr(G), dt, None,
+                  C, BN, C, 0.9, 1.0, 0.0, 5.0, 2, 0, stream)
+        outs.append((G, gm))
+    assert torch.equal(_planes_sum(outs[1][0].view(3, C, BN)), outs[0][0].view(C, BN))
+    assert torch.equal(outs[1][1], outs[0][1])
+
+
+def _flips(r1, r2, T):
+    """Spikes by which two rate tensors (counts / T) differ."""
+
+    return float(np.rint(np.abs(to_np(r1).astype(np.float64) - to_np(r2).astype(np.float64)) * T).sum())
+
+
+def _layer_inputs(T, B, F, N, seed):
+    g = seeded(seed)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float()
+    w = (torch.rand(F, N, generator=g) - 0.45) * 0.5
+    b = torch.rand(N, generator=g) * 0.1
+    return x, w, b, g
+
+
+def _run_layer(x, w, b, go, ck, rate, need_x):
+    xd = x.to(DEV).requires_grad_(need_x)
+    wd, bd = w.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    if rate:
+        st, out = myelin.linear_surrogate_lif_rate_forward(xd, wd, bd, P, surrogate="atan", surrogate_slope=4.0,
+                                                           checkpoint_size=ck, reduction="none")
+    else:
+        st, out = myelin.linear_surrogate_lif_forward(xd, wd, bd, P, surrogate="atan", surrogate_slope=4.0,
+                                                      checkpoint_size=ck)
+    out.backward(go.to(DEV))
+    return (to_np(out), to_np(st.membrane), None if not need_x else to_np(xd.grad), to_np(wd.grad),
+            to_np(bd.grad))
+
+
+@pytest.mark.parametrize("ck,rate", [(None, False), (5, False), (7, True)])
+@pytest.mark.parametrize("need_x", [False, True])
+def test_split_layer_matches_oracle_and_fp32_engine(monkeypatch, ck, rate, need_x):
+    """A 64 -> 72 layer on binary inputs, split path forced on (no minimum
+    size): against the CPU oracle at the fp32 bars, and against the same
+    layer on the fp32 engine."""
+
+    _print_case(test="split_layer", ck=ck, rate=rate, need_x=need_x)
+    T, B, F, N = 37, 5, 64, 72
+    x, w, b, g = _layer_inputs(T, B, F, N, 40 + (ck or 0) + rate)
+    go = torch.randn((B, N) if rate else (T, B, N), generator=g)
+    calls = []
+    real = L._split_synapse
+    monkeypatch.setattr(L, "_split_synapse", lambda *a: calls.append(1) or real(*a))
+    monkeypatch.setattr(L, "_SPLIT_MIN_MACS", 0)
+    got = _run_layer(x, w, b, go, ck, rate, need_x)
+    assert calls, "the split path did not run"
+    monkeypatch.setattr(L, "_SPLIT_MIN_MACS", 1 << 62)
+    fp32 = _run_layer(x, w, b, go, ck, rate, need_x)
+    if rate:
+        assert _flips(got[0], fp32[0], T) <= 1e-4 * T * B * N
+    else:
+        assert raster_agreement(got[0], fp32[0]) >= 0.9999
+    for i, what in ((1, "membrane"), (3, "grad_w"), (4, "grad_b")) + (((2, "grad_x"),) if need_x else ()):
+        assert_norm_close(got[i], fp32[i], 1e-5, f"{what} vs fp32 engine")
+    xr, wr, br = (t.clone().requires_grad_() for t in (x, w, b))
+    if rate:
+        mT, r = R.linear_surrogate_lif_rate(xr, wr, br, 9.0, 0.7, -0.2, "atan", 4.0, ck, "none")
+        r.backward(go)
+        assert _flips(got[0], r.detach(), T) <= 1e-4 * T * B * N
+    else:
+        if ck is None:
+            mT, s = R.linear_surrogate_lif_stream(xr, wr, br, 9.0, 0.7, -0.2, "atan", 4.0)
+        else:
+            mT, s = R.linear_surrogate_lif_checkpoint(xr, wr, br, 9.0, 0.7, -0.2, "atan", 4.0, ck)
+        s.backward(go)
+        assert raster_agreement(got[0], s) >= 0.9999
+    assert_norm_close(got[1], mT.detach(), 1e-5, "membrane vs oracle")
+    assert_norm_close(got[3], wr.grad, 1e-4, "grad_w vs oracle")
+    assert_norm_close(got[4], br.grad, 1e-4, "grad_b vs oracle")
+    if need_x:
+        assert_norm_close(got[2], xr.grad, 1e-4, "grad_x vs oracle")
+
+
+def test_non_exact_inputs_fall_back_to_the_fp32_engine(monkeypatch):
+    _print_case(test="split_fallback")
+    T, B, F, N = 21, 4, 64, 72
+    x, w, b, g = _layer_inputs(T, B, F, N, 77)
+    x[3, 1, 5] = 0.3  # not a bf16 value
+    go = torch.randn(T, B, N, generator=g)
+    monkeypatch.setattr(L, "_SPLIT_MIN_MACS", 0)
+    got = _run_layer(x, w, b, go, 4, False, True)
+    monkeypatch.setattr(L, "_SPLIT_MIN_MACS", 1 << 62)
+    fp32 = _run_layer(x, w, b, go, 4, False, True)
+    for a, c in zip(got, fp32):
+        assert np.array_equal(a, c)
+
+
+def test_split_recompute_reproduces_forward_trace_exactly(monkeypatch):
+    """The checkpointed backward's recompute on the split path (unsplit K,
+    chunk rows only) equals the forward's trace bit for bit."""
+
+    _print_case(test="split_recompute_exact")
+    T, B, F, N, C = 512, 8, 256, 1024, 16
+    g = seeded(17)
+    x = (torch.rand(T, B, F, generator=g) < 0.2).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.4) * 0.2).to(DEV)
+    b = (torch.rand(N, generator=g) * 0.05).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    xb, w3 = L._split_synapse(x, w, stream)
+    args = (0.95, 1.0, 0.0, 5.0, _lib.RULE_THRESHOLD, _lib.PREC["fp32"], stream)
+    pre = torch.empty(T, B, N, device=DEV)
+    ck = torch.empty(T // C, B, N, device=DEV)
+    L._lif_fwd(xb, w, b, None, 0, T, *args, pre=pre, ckpt=ck, ckpt_every=C, wt=w3, exact=True)
+    scratch = torch.empty(C, B, N, device=DEV)
+    for k in (0, 1, 17, T // C - 1):
+        L._lif_fwd(xb, w, b, ck[k], k * C, (k + 1) * C, *args, pre=scratch, wt=w3, exact=True)
+        assert torch.equal(scratch, pre[k * C:(k + 1) * C]), f"chunk {k}"
