@@ -43,8 +43,8 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _half, _keep_trace, _lif_fwd, _side_stream,
-                               _transpose_bf16)
+from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _gemm_parts, _half, _keep_trace, _lif_fwd,
+                               _side_stream, _split_eligible, _split_synapse, _transpose_bf16)
 
 # trace budget of a backward span (floats per buffer): the backward walks
 # whole checkpoint chunks, as many at a time as keep each per-span buffer
@@ -115,6 +115,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(wh, stream)) if half else (x, None)
+        # spike inputs: the hidden synapse on the exact bf16 split
+        if not half and _split_eligible(prec, T, B, F, H):
+            sp = _split_synapse(x, wh, stream)
+            if sp is not None:
+                xs, wt = sp
         for k in range(0, K, G):
             t0 = k * C
             t1 = min(t0 + G * C, T)
@@ -140,7 +145,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             return none
         decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
         xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_all = ctx.saved_tensors
-        half = xs.dtype == torch.bfloat16
+        parts = wt is not None and wt.ndim == 3  # exact split of the hidden synapse
+        half = xs.dtype == torch.bfloat16 and not parts
         need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
         need_hidden = need_x or need_wh or (need_bh and has_bh)
         T, B, F = xs.shape
@@ -173,6 +179,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
             G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
                    if need_hidden else None)
+            # exact split: dW_h reads G_h as three bf16 planes [3, L, B, H],
+            # written by the reverse pass itself unless dX needs the fp32 G_h
+            G3 = torch.empty(3 * L0 * B * H, dtype=torch.bfloat16, device=dev) if parts and need_wh else None
+            if G3 is not None and not need_x:
+                G_h = G3
             # The hidden recompute (its trace, and spikes in the dense
             # variant) runs one span ahead on a side stream into two
             # alternating buffer sets, overlapping the current span's
@@ -248,7 +259,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
                 _lib.call(
                     "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h), _lib.DT[G_h.dtype],
+                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h),
+                    _lib.DT_BF16X3 if G_h is G3 else _lib.DT[G_h.dtype],
                     _lib.ptr(gbh_acc),
                     L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
                 )
@@ -257,7 +269,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 if gx is not None:
                     _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
                 if gwh is not None:
-                    _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream)
+                    if parts:
+                        if G_h is not G3:
+                            _lib.call("myelin_split_bf16x3", _lib.ptr(G_h), _lib.ptr(G3), rows, H, 0, stream)
+                        _gemm_parts(xs[t0:t1], G3, 3, rows * H, gwh, F, H, rows, F, H, H, True, False, k != NS - 1,
+                                    stream)
+                    else:
+                        _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream)
             if nset == 2:
                 # every side-stream kernel is behind a ready[] the main stream
                 # waited on; these tensors' last users include the side stream

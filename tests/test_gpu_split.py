@@ -274,3 +274,49 @@ def test_split_recompute_reproduces_forward_trace_exactly(monkeypatch):
     for k in (0, 1, 17, T // C - 1):
         L._lif_fwd(xb, w, b, ck[k], k * C, (k + 1) * C, *args, pre=scratch, wt=w3, exact=True)
         assert torch.equal(scratch, pre[k * C:(k + 1) * C]), f"chunk {k}"
+
+
+@pytest.mark.parametrize("variant", ["recompute", "packed"])
+@pytest.mark.parametrize("need_x", [False, True])
+def test_two_layer_hidden_split_matches_fp32_engine_and_oracle(monkeypatch, variant, need_x):
+    """The two-layer network's hidden synapse on the split path (binary
+    inputs, forced on): rates and gradients against the fp32-engine run and
+    the oracle."""
+
+    from myelin_amd import two_layer as TL
+
+    _print_case(test="two_layer_split", variant=variant, need_x=need_x)
+    T, B, F, H, O, C = 23, 4, 64, 136, 10, 4
+    g = seeded(61 + need_x)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float()
+    wh = (torch.rand(F, H, generator=g) - 0.4) * 0.5
+    bh = torch.rand(H, generator=g) * 0.1
+    wo = (torch.rand(H, O, generator=g) - 0.4) * 0.4
+    bo = torch.rand(O, generator=g) * 0.1
+    grate = torch.randn(B, O, generator=g)
+    fn = {"recompute": myelin.two_layer_surrogate_lif_rate_recompute_forward,
+          "packed": myelin.two_layer_surrogate_lif_rate_packed_hidden_forward}[variant]
+    p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
+    calls = []
+    real = TL._split_synapse
+    monkeypatch.setattr(TL, "_split_synapse", lambda *a: calls.append(1) or real(*a))
+    res = []
+    for min_macs in (0, 1 << 62):
+        monkeypatch.setattr(L, "_SPLIT_MIN_MACS", min_macs)
+        leaves = [x.to(DEV).requires_grad_(need_x)] + [t.to(DEV).requires_grad_() for t in (wh, bh, wo, bo)]
+        r = fn(*leaves, p, surrogate="fast_sigmoid", surrogate_slope=5.0, checkpoint_size=C)
+        r.backward(grate.to(DEV))
+        res.append([to_np(r)] + [None if t.grad is None else to_np(t.grad) for t in leaves])
+    assert len(calls) == 1, "the split path ran once (the first run)"
+    assert _flips(res[0][0], res[1][0], T) <= 1e-4 * T * B * O
+    for name, a, b in zip(("x", "wh", "bh", "wo", "bo"), res[0][1:], res[1][1:]):
+        if a is not None:
+            assert_norm_close(a, b, 1e-5, f"grad_{name} vs fp32 engine")
+    lv = [x.clone().requires_grad_(need_x)] + [t.clone().requires_grad_() for t in (wh, bh, wo, bo)]
+    rr = R.two_layer_rate(*lv, 8.0, 0.7, -0.2, "fast_sigmoid", 5.0, C)
+    rr.backward(grate)
+    assert _flips(res[0][0], rr.detach(), T) <= 1e-4 * T * B * O
+    if np.array_equal(res[0][0], rr.detach().numpy()):
+        for name, a, t in zip(("x", "wh", "bh", "wo", "bo"), res[0][1:], lv):
+            if a is not None:
+                assert_norm_close(a, t.grad, 1e-4, f"grad_{name} vs oracle")
