@@ -864,8 +864,9 @@ struct BigLoader {
   static constexpr int MNB = ROWS / 4 * 8;
   static_assert(KC ? (ROWS * KS / KQ) % NT == 0 : NT % MNB == 0 || MNB % NT == 0, "thread mapping");
   static_assert(KC || MNB <= NT, "one MN block per thread at most");
-  // register set: fp32 -> 4*KQ floats; bf16 KC -> 4 x u4; bf16 MN -> 8 x u2
-  static constexpr int NW = H ? (KC ? 16 : 16) : 4 * KQ;
+  // register set: KC -> per piece one u4 (bf16 in memory) or KQ words (fp32
+  // in memory); MN -> 8 x u2 (bf16) or 4*KQ floats (fp32)
+  static constexpr int NW = KC ? NP * (H ? 4 : KQ) : (H ? 16 : 4 * KQ);
   unsigned int v[D][NW];
   const S *q[NP];      // KC: piece row + its k offset; MN: k row kk, column mn
   int kk[NP];          // k offset of the piece (KC) / of the thread's k rows (MN)
@@ -1050,51 +1051,46 @@ struct BigLoader {
   }
 };
 
-template <int PREC, class ST>
-__device__ __forceinline__ void big_mfma(const ST &st, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
+// One stage of a wave's WM x WN blocks of 32 x 32 (rows 32*WM*wm + 32*i,
+// columns 32*WN*wn + 32*j): per k step, WM + WN fragment reads feed WM*WN
+// MFMAs.
+template <int PREC, class ST, int WM, int WN>
+__device__ __forceinline__ void big_mfma(const ST &st, int wm, int wn, int lane, f32x16 (&acc)[WM][WN]) {
   constexpr int KS = Prec<PREC>::KS, KM = Prec<PREC>::KM, KV = Prec<PREC>::KV;
-  const int r = 64 * wm + (lane & 31), c = 64 * wn + (lane & 31), kq = (lane >> 5) * KV;
+  const int r = 32 * WM * wm + (lane & 31), c = 32 * WN * wn + (lane & 31), kq = (lane >> 5) * KV;
 #pragma unroll
   for (int kk = 0; kk < KS; kk += KM) {
     if constexpr (PREC == 1) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(&st.a[r][kk + kq]);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(&st.a[r + 32][kk + kq]);
-      const bf16x8 b0 = *reinterpret_cast<const bf16x8 *>(&st.b[c][kk + kq]);
-      const bf16x8 b1 = *reinterpret_cast<const bf16x8 *>(&st.b[c + 32][kk + kq]);
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+      bf16x8 a[WM], b[WN];
+#pragma unroll
+      for (int i = 0; i < WM; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(&st.a[r + 32 * i][kk + kq]);
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b[j] = *reinterpret_cast<const bf16x8 *>(&st.b[c + 32 * j][kk + kq]);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     } else if (kk % 8 == 0) {
       // 16-byte fragment groups of 8 k, the k order of mfma_stage
       const int kg = (lane >> 5) * 4;
-      const f4 a0 = *reinterpret_cast<const f4 *>(&st.a[r][kk + kg]);
-      const f4 a1 = *reinterpret_cast<const f4 *>(&st.a[r + 32][kk + kg]);
-      const f4 b0 = *reinterpret_cast<const f4 *>(&st.b[c][kk + kg]);
-      const f4 b1 = *reinterpret_cast<const f4 *>(&st.b[c + 32][kk + kg]);
+      f4 a[WM], b[WN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[i], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b1[i], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], b0[i], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], b1[i], acc[1][1], 0, 0, 0);
-      }
+      for (int i = 0; i < WM; ++i) a[i] = *reinterpret_cast<const f4 *>(&st.a[r + 32 * i][kk + kg]);
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b[j] = *reinterpret_cast<const f4 *>(&st.b[c + 32 * j][kk + kg]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
     }
   }
 }
 
-// acc += A[128 x (kb..ke)] B[(kb..ke) x 128] over LDS double buffers.
-// The full KS-wide stages run with unguarded loads only, so the loop body
-// is straight-line and the compiler's wait counts stay exact: with DEPTH 2
-// register sets a stage's loads are issued two stages before it is stored
-// to LDS (two MFMA stages hide their latency; fetches past the last full
-// stage re-read it).  A partial last stage is then loaded with guards and
-// applied, so the k order is the same as in every other path.  DEPTH 1
-// (fp32 operands of the bf16 MFMA, 64 registers per set): one stage ahead.
-// Operands too narrow for clamped fast loads take guarded stages only.
-template <int PREC, int DEPTH, class LA, class LB, class ST>
+template <int PREC, int DEPTH, class LA, class LB, class ST, int WM, int WN>
 __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke, ST (&st)[2], int wm, int wn,
-                                          int lane, f32x16 (&acc)[2][2]) {
+                                          int lane, f32x16 (&acc)[WM][WN]) {
   constexpr int KS = Prec<PREC>::KS;
   if (kb >= ke) return;
   const int64_t nfull = (ke - kb) / KS;
@@ -1111,7 +1107,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         const int buf = sg & 1;
         la.template fast<0>(kof(sg + 1));
         lb.template fast<0>(kof(sg + 1));
-        big_mfma<PREC, ST>(st[buf], wm, wn, lane, acc);
+        big_mfma<PREC, ST, WM, WN>(st[buf], wm, wn, lane, acc);
         if (sg + 1 < nfull) {
           la.template store<0>(st[buf ^ 1].a);
           lb.template store<0>(st[buf ^ 1].b);
@@ -1126,7 +1122,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         // stage sg in st[0]; set 1 holds stage sg + 1; fetch sg + 2 into set 0
         la.template fast<0>(kof(sg + 2));
         lb.template fast<0>(kof(sg + 2));
-        big_mfma<PREC, ST>(st[0], wm, wn, lane, acc);
+        big_mfma<PREC, ST, WM, WN>(st[0], wm, wn, lane, acc);
         if (sg + 1 < nfull) {
           la.template store<1>(st[1].a);
           lb.template store<1>(st[1].b);
@@ -1136,7 +1132,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
         // stage sg + 1 in st[1]; set 0 holds stage sg + 2; fetch sg + 3 into set 1
         la.template fast<1>(kof(sg + 3));
         lb.template fast<1>(kof(sg + 3));
-        big_mfma<PREC, ST>(st[1], wm, wn, lane, acc);
+        big_mfma<PREC, ST, WM, WN>(st[1], wm, wn, lane, acc);
         if (sg + 2 < nfull) {
           la.template store<0>(st[0].a);
           lb.template store<0>(st[0].b);
@@ -1154,7 +1150,7 @@ __device__ __forceinline__ void big_kloop(LA &la, LB &lb, int64_t kb, int64_t ke
     la.template store<0>(st[0].a);
     lb.template store<0>(st[0].b);
     __syncthreads();
-    big_mfma<PREC, ST>(st[0], wm, wn, lane, acc);
+    big_mfma<PREC, ST, WM, WN>(st[0], wm, wn, lane, acc);
     __syncthreads();
   }
 }
@@ -1184,15 +1180,21 @@ __device__ __forceinline__ void big_tile(uint32_t bid, uint32_t nblk, uint32_t t
   tn = __builtin_amdgcn_readfirstlane(in / gs);
 }
 
-// BM x BN output tile, one wave per 64 x 64 quarter: (BM/64) x (BN/64)
-// waves of 2 x 2 MFMA blocks.  MP: bf16 operands summing g.parts B parts
-// (a separate instantiation, so the one-part kernels keep their registers).
-template <int PREC, bool TA, bool TB, typename S, int BM, int BN, bool MP = false>
-__global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big(GemmArgs g) {
-  constexpr int NT = BM * BN / 64;
+// BM x BN output tile; each wave owns WM x WN blocks of 32 x 32 (the
+// launched kernels: 2 x 2, one wave per 64 x 64 quarter).  MP: bf16 operands
+// summing g.parts B parts (a separate instantiation, so the one-part kernels
+// keep their registers).  Wave tiles above 2 x 2 would run one wave per SIMD
+// with up to 512 registers; a 256 x 128 tile of four 128 x 64 waves
+// measured slower than this one (612 against 703 TFLOP/s at 8192 x 4096 x
+// 3072 bf16), so none is launched.
+template <int PREC, bool TA, bool TB, typename S, int BM, int BN, bool MP = false, int WM = 2, int WN = 2>
+__global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN)))
+__attribute__((amdgpu_waves_per_eu(WM * WN > 4 ? 1 : 2))) void gemm_big(GemmArgs g) {
+  constexpr int WGN = BN / (32 * WN);  // waves across the tile's columns
+  constexpr int NT = 64 * (BM / (32 * WM)) * WGN;
   __shared__ BigStage<PREC, BM, BN> st[2];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / (BN / 64), wn = w % (BN / 64);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / WGN, wn = w % WGN;
   const uint32_t tiles_m = static_cast<uint32_t>((g.M + BM - 1) / BM);
   const uint32_t tiles_n = static_cast<uint32_t>((g.N + BN - 1) / BN);
   int64_t tm, tn;
@@ -1207,11 +1209,11 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
   la.init(tid, g.A, m0, g.M, g.lda);
   lb.init(tid, g.B, n0, g.N, g.ldb);
 
-  f32x16 acc[2][2];
+  f32x16 acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   if constexpr (MP) {
@@ -1227,14 +1229,14 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
 
   // (the per-element form measures faster here than store_acc's)
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + 64 * wn + 32 * j + (lane & 31);
+  for (int j = 0; j < WN; ++j) {
+    const int64_t col = n0 + 32 * WN * wn + 32 * j + (lane & 31);
     if (col >= g.N) continue;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + 64 * wm + 32 * i + acc_row(r, lane);
+        const int64_t row = m0 + 32 * WM * wm + 32 * i + acc_row(r, lane);
         if (row >= g.M) continue;
         if (g.splits > 1) {
           g.ws[(static_cast<int64_t>(blockIdx.y) * g.M + row) * g.N + col] = acc[i][j][r];

@@ -320,3 +320,30 @@ def test_two_layer_hidden_split_matches_fp32_engine_and_oracle(monkeypatch, vari
         for name, a, t in zip(("x", "wh", "bh", "wo", "bo"), res[0][1:], lv):
             if a is not None:
                 assert_norm_close(a, t.grad, 1e-4, f"grad_{name} vs oracle")
+
+
+@pytest.mark.parametrize("parts", [1, 3])
+def test_parts_products_do_not_depend_on_the_rows_computed(parts):
+    """A 128-row slice of a three-part bf16 product (K = 1000, ending in a
+    partial stage, no K split) equals the same rows of the 8192-row product
+    bit for bit, as a checkpointed recompute needs; and the product is
+    within 1e-5 of float64."""
+
+    _print_case(test="parts_rows", parts=parts)
+    M, N, K = 8192, 1024, 1000
+    g = seeded(123 + parts)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    Bs = torch.randn(parts, N, K, generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g)
+    Ad, Bd, bd = A.to(DEV), Bs.to(DEV), bias.to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    full = torch.empty(M, N, device=DEV)
+    L._gemm_parts(Ad, Bd, parts, N * K, full, M, N, K, K, K, N, False, True, False, stream, bias=bd, split=False)
+    for r0 in (0, 4000, M - 128):
+        sub = torch.empty(128, N, device=DEV)
+        L._gemm_parts(Ad[r0:r0 + 128], Bd, parts, N * K, sub, 128, N, K, K, K, N, False, True, False, stream,
+                      bias=bd, split=False)
+        assert torch.equal(full[r0:r0 + 128], sub), f"rows {r0}"
+    rows = torch.tensor([0, 1, 255, 256, 4097, M - 1])
+    ref = sum(A[rows].double() @ Bs[p].double().t() for p in range(parts)) + bias.double()
+    assert_norm_close(to_np(full[rows.to(DEV)]), ref.numpy(), 1e-5, "parts product vs float64")
