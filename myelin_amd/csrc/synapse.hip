@@ -689,13 +689,14 @@ __device__ __forceinline__ float round_in(float v) {
 // precision's input type, summed in k order with fused multiply-adds (bf16
 // products are exact in fp32).  VC: C rows allow 16-byte stores.
 #ifndef MYELIN_SMALLK_RW
-#define MYELIN_SMALLK_RW 16  // rows per wave of the small-K kernel
+#define MYELIN_SMALLK_RW 32  // rows per wave of the small-K kernel
 #endif
 
 template <int PREC, bool TA, bool TB, bool PA, int KMAX, bool VC>
 __global__ __launch_bounds__(256) void gemm_smallk(GemmArgs g) {
   constexpr int RW = MYELIN_SMALLK_RW;     // rows per wave
   constexpr int SLOTS = RW * KMAX / 64;    // A values per lane
+  static_assert(RW * KMAX % 64 == 0, "the wave's A block fills whole slots");
   // TB (B stored [N, K]): the workgroup's 256 columns x K, k-major
   __shared__ __attribute__((aligned(16))) float bt[TB ? KMAX : 1][TB ? 256 : 4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -2008,13 +2009,18 @@ void launch_smallk_c(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s
     launch_smallk_k<PREC, PA, KMAX, false>(g, ta, tb, grid, s);
 }
 
-// K <= 32, unrolled to the next multiple of 8
+// K <= 32, unrolled to the next multiple of 4 from 8 up to 24, else 32
+// (the padded k cost full multiply-adds: the kernel is bound by them)
 template <int PREC, bool PA>
 void launch_smallk(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) {
   if (g.K <= 8)
     launch_smallk_c<PREC, PA, 8>(g, ta, tb, grid, s);
+  else if (g.K <= 12)
+    launch_smallk_c<PREC, PA, 12>(g, ta, tb, grid, s);
   else if (g.K <= 16)
     launch_smallk_c<PREC, PA, 16>(g, ta, tb, grid, s);
+  else if (g.K <= 20)
+    launch_smallk_c<PREC, PA, 20>(g, ta, tb, grid, s);
   else if (g.K <= 24)
     launch_smallk_c<PREC, PA, 24>(g, ta, tb, grid, s);
   else
