@@ -1672,9 +1672,11 @@ struct PreBwdArgs {
 // no load is predicated.
 constexpr int kPipe = 16;
 
-template <int SID, bool GS, int GM>
-__device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, float pre, float gsv,
-                                             float gstep, float &gm, float &gb) {
+// One reverse step of one neuron: gp = dL/dI_j (reference op order), then
+// the carried gm = gp * decay; gb accumulates gp.
+template <int SID, bool GS>
+__device__ __forceinline__ float pre_bwd_gp(const PreBwdArgs &p, float pre, float gsv, float gstep, float &gm,
+                                            float &gb) {
   const float c = p.slope * (pre - p.thr);
   const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (pre >= p.thr) : (c >= 0.0f);
   const float s = sp ? 1.0f : 0.0f;
@@ -1682,58 +1684,115 @@ __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int
   float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
   if constexpr (GS) gp = gp + gsv * d;
   if (p.grate != nullptr) gp = gp + gstep * d;
-  if constexpr (GM == 1) {
-    static_cast<uint16_t *>(p.G)[j * p.BN + i] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(gp));
-  } else if constexpr (GM == 2) {
-    uint16_t h, m, l;
-    split3(gp, h, m, l);
-    uint16_t *g16 = static_cast<uint16_t *>(p.G) + j * p.BN + i;
-    const int64_t plane = p.C * p.BN;
-    g16[0] = h;
-    g16[plane] = m;
-    g16[2 * plane] = l;
-  } else {
-    static_cast<float *>(p.G)[j * p.BN + i] = gp;
-  }
   gb = gb + gp;
   gm = gp * p.decay;
+  return gp;
+}
+
+template <int V>
+struct PreVec;
+template <>
+struct PreVec<1> {
+  using T = float;
+  static __device__ __forceinline__ float at(float v, int) { return v; }
+};
+template <>
+struct PreVec<2> {
+  using T = float2;
+  static __device__ __forceinline__ float at(float2 v, int e) { return e ? v.y : v.x; }
+};
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+
+// G[j, i .. i+V) = gp: fp32 (GM 0), bf16 (GM 1) or three bf16 planes (GM 2),
+// one store per plane covering the lane's V neurons
+template <int GM, int V>
+__device__ __forceinline__ void store_g(const PreBwdArgs &p, int64_t i, int64_t j, const float (&gp)[V]) {
+  const int64_t at = j * p.BN + i;
+  if constexpr (GM == 0) {
+    if constexpr (V == 2)
+      *reinterpret_cast<float2 *>(static_cast<float *>(p.G) + at) = float2{gp[0], gp[1]};
+    else
+      static_cast<float *>(p.G)[at] = gp[0];
+  } else if constexpr (GM == 1) {
+    if constexpr (V == 2)
+      *reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(p.G) + at) =
+          bf16_bits(gp[0]) | static_cast<uint32_t>(bf16_bits(gp[1])) << 16;
+    else
+      static_cast<uint16_t *>(p.G)[at] = bf16_bits(gp[0]);
+  } else {
+    uint16_t h[V], m[V], l[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) split3(gp[e], h[e], m[e], l[e]);
+    uint16_t *g16 = static_cast<uint16_t *>(p.G) + at;
+    const int64_t plane = p.C * p.BN;
+    if constexpr (V == 2) {
+      *reinterpret_cast<uint32_t *>(g16) = h[0] | static_cast<uint32_t>(h[1]) << 16;
+      *reinterpret_cast<uint32_t *>(g16 + plane) = m[0] | static_cast<uint32_t>(m[1]) << 16;
+      *reinterpret_cast<uint32_t *>(g16 + 2 * plane) = l[0] | static_cast<uint32_t>(l[1]) << 16;
+    } else {
+      g16[0] = h[0];
+      g16[plane] = m[0];
+      g16[2 * plane] = l[0];
+    }
+  }
+}
+
+template <int SID, bool GS, int GM, int V, typename VT>
+__device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, VT pre, VT gsv,
+                                             const float (&gstep)[V], float (&gm)[V], float (&gb)[V]) {
+  float gp[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e)
+    gp[e] = pre_bwd_gp<SID, GS>(p, PreVec<V>::at(pre, e), PreVec<V>::at(gsv, e), gstep[e], gm[e], gb[e]);
+  store_g<GM, V>(p, i, j, gp);
 }
 
 // reverse time: relative index r = C - 1 - j.  GM: G is written as fp32
 // (0), as bf16 rounded as the bf16 GEMMs would round it (1), or as three
-// bf16 planes whose sum is G exactly (2).
-template <int SID, bool GS, int GM>
+// bf16 planes whose sum is G exactly (2).  V neurons per lane (V = 2: BN
+// even and every operand 8-byte aligned, so each step is one 8-byte load
+// per operand and one store per plane).
+template <int SID, bool GS, int GM, int V>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  using VT = typename PreVec<V>::T;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (i >= p.BN) return;
-  const int64_t C = p.C;
-  float gm = p.gm[i];
-  const float gstep = p.grate != nullptr ? p.grate[i] / p.rate_denominator : 0.0f;
-  float gb = 0.0f;
-  const float *pre = p.pre + i;
-  const float *gs = GS ? p.gs + i : nullptr;
+  const int64_t C = p.C, row = p.BN / V;
+  float gm[V], gstep[V], gb[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    gm[e] = p.gm[i + e];
+    gstep[e] = p.grate != nullptr ? p.grate[i + e] / p.rate_denominator : 0.0f;
+    gb[e] = 0.0f;
+  }
+  const VT *pre = reinterpret_cast<const VT *>(p.pre + i);
+  const VT *gs = GS ? reinterpret_cast<const VT *>(p.gs + i) : nullptr;
+  const VT zero{};
   const int64_t nblk = (C + kPipe - 1) / kPipe;
   const int64_t f = C - (nblk - 1) * kPipe;
-  float pv[kPipe], gv[kPipe];
+  VT pv[kPipe], gv[kPipe];
 #pragma unroll
   for (int u = 0; u < kPipe; ++u) {
     const int64_t j = C - 1 - (u < f ? u : f - 1);
-    pv[u] = pre[j * p.BN];
-    if constexpr (GS) gv[u] = gs[j * p.BN];
+    pv[u] = pre[j * row];
+    if constexpr (GS) gv[u] = gs[j * row];
   }
   // block 0 (f steps), prefetching block 1 (or re-reading block 0 when alone)
   {
     const int64_t r0 = nblk > 1 ? f : 0;
-    float np[kPipe], ng[kPipe];
+    VT np[kPipe], ng[kPipe];
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       const int64_t r = r0 + u < C ? r0 + u : C - 1;
-      np[u] = pre[(C - 1 - r) * p.BN];
-      if constexpr (GS) ng[u] = gs[(C - 1 - r) * p.BN];
+      np[u] = pre[(C - 1 - r) * row];
+      if constexpr (GS) ng[u] = gs[(C - 1 - r) * row];
     }
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      if (u < f) pre_bwd_step<SID, GS, GM>(p, i, C - 1 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      if (u < f) pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
@@ -1742,24 +1801,27 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   }
   for (int64_t r0 = f; r0 < C; r0 += kPipe) {
     const int64_t rn = r0 + kPipe < C ? r0 + kPipe : r0;
-    float np[kPipe], ng[kPipe];
+    VT np[kPipe], ng[kPipe];
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
-      np[u] = pre[(C - 1 - rn - u) * p.BN];
-      if constexpr (GS) ng[u] = gs[(C - 1 - rn - u) * p.BN];
+      np[u] = pre[(C - 1 - rn - u) * row];
+      if constexpr (GS) ng[u] = gs[(C - 1 - rn - u) * row];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      pre_bwd_step<SID, GS, GM>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : 0.0f, gstep, gm, gb);
+      pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) {
       pv[u] = np[u];
       if constexpr (GS) gv[u] = ng[u];
     }
   }
-  p.gm[i] = gm;
-  if (p.gbias_acc != nullptr) p.gbias_acc[i] = p.gbias_acc[i] + gb;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    p.gm[i + e] = gm[e];
+    if (p.gbias_acc != nullptr) p.gbias_acc[i + e] = p.gbias_acc[i + e] + gb[e];
+  }
 }
 
 // out[n] (+)= sum_r in[r, n].  A block of 16 waves takes 64 columns; wave
@@ -2101,23 +2163,39 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   return MYELIN_OK;
 }
 
-template <int SID>
-void launch_pre_bwd(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
+template <int SID, int V>
+void launch_pre_bwd_v(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
   if (gs) {
     if (gm == 2)
-      linear_pre_bwd<SID, true, 2><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 2, V><<<grid, dim3(256), 0, s>>>(a);
     else if (gm == 1)
-      linear_pre_bwd<SID, true, 1><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 1, V><<<grid, dim3(256), 0, s>>>(a);
     else
-      linear_pre_bwd<SID, true, 0><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 0, V><<<grid, dim3(256), 0, s>>>(a);
   } else {
     if (gm == 2)
-      linear_pre_bwd<SID, false, 2><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 2, V><<<grid, dim3(256), 0, s>>>(a);
     else if (gm == 1)
-      linear_pre_bwd<SID, false, 1><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 1, V><<<grid, dim3(256), 0, s>>>(a);
     else
-      linear_pre_bwd<SID, false, 0><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 0, V><<<grid, dim3(256), 0, s>>>(a);
   }
+}
+
+// two neurons per lane where BN is even, every operand is 8-byte aligned and
+// the grid stays wide (>= 512 waves): on a few waves the serial walk is the
+// cost, and two neurons per lane double it (640 neurons x 2000 steps: 164
+// -> 278 us), while wide grids gain from the 8-byte accesses (131072 x
+// 225: 74 -> 68 us; 524288 x 256: 333 -> 315 us)
+template <int SID>
+void launch_pre_bwd(const PreBwdArgs &a, bool gs, int gm, hipStream_t s) {
+  const bool v2 = a.BN >= 65536 && a.BN % 2 == 0 && myelin::aligned(a.pre, 8) && myelin::aligned(a.gs, 8) &&
+                  myelin::aligned(a.gm, 8) && myelin::aligned(a.grate, 8) && myelin::aligned(a.gbias_acc, 8) &&
+                  myelin::aligned(a.G, gm == 0 ? 8 : 4);
+  if (v2)
+    launch_pre_bwd_v<SID, 2>(a, gs, gm, dim3(cdiv(a.BN / 2, 256)), s);
+  else
+    launch_pre_bwd_v<SID, 1>(a, gs, gm, dim3(cdiv(a.BN, 256)), s);
 }
 
 template <bool PRE, bool SPK>
@@ -2360,17 +2438,17 @@ extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
     return myelin::invalid("linear_pre_bwd: G must be float32, bfloat16 or three bfloat16 planes");
   PreBwdArgs a{pre, grad_spikes, grad_rates, grad_m, G, gbias_acc, C, BN, decay, threshold, reset, slope,
                static_cast<float>(T_total), rule};
-  const dim3 grid(cdiv(BN, 256));
+  if (cdiv(BN, 256) > 0x7fffffff) return myelin::invalid("linear_pre_bwd: BN too large");
   hipStream_t s = myelin::as_hip(stream);
   const bool gs = grad_spikes != nullptr;
   const int gh = g_dtype == MYELIN_DT_BF16X3 ? 2 : g_dtype == MYELIN_DT_BF16 ? 1 : 0;
   switch (surrogate_id) {
-    case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, gh, grid, s); break;
-    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, gh, grid, s); break;
-    case MYELIN_SG_ATAN: launch_pre_bwd<MYELIN_SG_ATAN>(a, gs, gh, grid, s); break;
-    case MYELIN_SG_TRIANGULAR: launch_pre_bwd<MYELIN_SG_TRIANGULAR>(a, gs, gh, grid, s); break;
-    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd<MYELIN_SG_SUPERSPIKE>(a, gs, gh, grid, s); break;
-    case MYELIN_SG_MULTI_GAUSSIAN: launch_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN>(a, gs, gh, grid, s); break;
+    case MYELIN_SG_SIGMOID: launch_pre_bwd<MYELIN_SG_SIGMOID>(a, gs, gh, s); break;
+    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd<MYELIN_SG_FAST_SIGMOID>(a, gs, gh, s); break;
+    case MYELIN_SG_ATAN: launch_pre_bwd<MYELIN_SG_ATAN>(a, gs, gh, s); break;
+    case MYELIN_SG_TRIANGULAR: launch_pre_bwd<MYELIN_SG_TRIANGULAR>(a, gs, gh, s); break;
+    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd<MYELIN_SG_SUPERSPIKE>(a, gs, gh, s); break;
+    case MYELIN_SG_MULTI_GAUSSIAN: launch_pre_bwd<MYELIN_SG_MULTI_GAUSSIAN>(a, gs, gh, s); break;
     default: return myelin::invalid("linear_pre_bwd: unknown surrogate id %d", surrogate_id);
   }
   return myelin::launched("linear_pre_bwd");

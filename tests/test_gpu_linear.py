@@ -505,3 +505,38 @@ def test_small_budget_spans_and_forward_chunks_agree_with_one_span(monkeypatch, 
     assert np.array_equal(res[1][0], res[0][0]) and np.array_equal(res[1][1], res[0][1])
     assert_norm_close(res[1][2], res[0][2], 1e-6, "grad_w across span sizes")
     assert_norm_close(res[1][3], res[0][3], 1e-6, "grad_b across span sizes")
+
+
+@pytest.mark.parametrize("gdt", ["fp32", "bf16", "planes"])
+@pytest.mark.parametrize("with_gs", [False, True])
+def test_reverse_pass_two_neurons_per_lane_equals_one(gdt, with_gs):
+    """linear_pre_bwd takes two neurons per lane on wide grids (>= 65536
+    neurons) when every operand is 8-byte aligned; the same data one float
+    off that alignment runs one neuron per lane.  G, the carried gradient
+    and the bias partials agree bit for bit."""
+
+    _print_case(test="pre_bwd_lanes", gdt=gdt, with_gs=with_gs)
+    C, BN = 37, 66002
+    g = seeded(41)
+    pre = torch.randn(C * BN, generator=g) + 0.8
+    gs = torch.randn(C * BN, generator=g)
+    grate = torch.randn(BN, generator=g)
+    gm0 = torch.randn(BN, generator=g)
+    dt = {"fp32": _lib.DT[torch.float32], "bf16": _lib.DT[torch.bfloat16], "planes": _lib.DT_BF16X3}[gdt]
+    gdtype = torch.float32 if gdt == "fp32" else torch.bfloat16
+    glen = C * BN * (3 if gdt == "planes" else 1)
+    stream = _lib.stream(torch.device(DEV))
+    outs = []
+    for off in (0, 1):
+        def place(t, dtype=torch.float32):
+            buf = torch.zeros(t.numel() + 2, dtype=dtype, device=DEV)
+            buf[off:off + t.numel()] = t.to(DEV, dtype)
+            return buf[off:off + t.numel()]
+        p_, s_, r_, m_ = place(pre), place(gs), place(grate), place(gm0)
+        gb = place(torch.zeros(BN))
+        G = place(torch.zeros(glen), gdtype)
+        _lib.call("myelin_linear_pre_bwd", _lib.ptr(p_), _lib.ptr(s_) if with_gs else None, _lib.ptr(r_),
+                  _lib.ptr(m_), _lib.ptr(G), dt, _lib.ptr(gb), C, BN, 50, 0.9, 1.0, -0.1, 4.0, 2, 0, stream)
+        outs.append((G.cpu(), m_.cpu(), gb.cpu()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
