@@ -1858,37 +1858,53 @@ struct CurArgs {
   int rule;
 };
 
-// One step of the currents recurrence for lane (b, n); output stores are
-// chosen at compile time (PRE: pre-reset membrane, SPK: dense spikes, PK:
-// ballot-packed words), checkpoints and counts at run time.
-template <bool PRE, bool SPK, bool PK>
-__device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, bool act, int64_t flat, int64_t BN,
-                                         int64_t gid, int lane, float &m, float &cnt, int64_t &ck_row,
-                                         int64_t &next_ck) {
-  if (p.ckpt != nullptr && t == next_ck) {
-    if (act) p.ckpt[ck_row * BN + flat] = m;
-    ++ck_row;
-    next_ck += p.ckpt_every;
+// Output cursors of one lane of the currents recurrence: each points at the
+// lane's element of the current step and advances one step at a time, so a
+// step does no index arithmetic.
+struct CurCursor {
+  float *pre, *spk, *ck;
+  int32_t *pk;
+  int64_t next_ck;
+};
+
+// One step of the currents recurrence for lane (b, n); the outputs (PRE:
+// pre-reset membrane, SPK: dense spikes, PK: ballot-packed words, CK:
+// checkpoints) and the spike rule are chosen at compile time, so a step is
+// its arithmetic and its stores.
+template <bool PRE, bool SPK, bool PK, int RULE, bool CK>
+__device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, bool act, int64_t BN, int64_t gw,
+                                         int lane, float &m, float &cnt, CurCursor &o) {
+  if constexpr (CK) {
+    if (t == o.next_ck) {
+      if (act) *o.ck = m;
+      o.ck += BN;
+      o.next_ck += p.ckpt_every;
+    }
   }
   float mp = m * p.decay;
   mp = mp + c;
-  const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (mp >= p.thr) : (p.slope * (mp - p.thr) >= 0.0f);
+  bool sp;
+  if constexpr (RULE == MYELIN_RULE_THRESHOLD)
+    sp = mp >= p.thr;
+  else
+    sp = p.slope * (mp - p.thr) >= 0.0f;
   if (act) {
-    if constexpr (PRE) p.pre[(t - p.pre_origin) * BN + flat] = mp;
-    if constexpr (SPK) p.spikes[t * BN + flat] = sp ? 1.0f : 0.0f;
+    if constexpr (PRE) *o.pre = mp;
+    if constexpr (SPK) *o.spk = sp ? 1.0f : 0.0f;
   }
+  if constexpr (PRE) o.pre += BN;
+  if constexpr (SPK) o.spk += BN;
   m = sp ? p.reset : mp;
   cnt = cnt + (sp ? 1.0f : 0.0f);
   if constexpr (PK) {
     const uint64_t bits = __ballot(act && sp);
-    const int64_t gw = (gid - lane) >> 5;  // the wave's first word
-    int32_t *row = p.packed + t * p.B * p.W;
-    if (lane == 0 && gw < p.B * p.W) row[gw] = static_cast<int32_t>(bits & 0xffffffffu);
-    if (lane == 32 && gw + 1 < p.B * p.W) row[gw + 1] = static_cast<int32_t>(bits >> 32);
+    if (lane == 0 && gw < p.B * p.W) o.pk[gw] = static_cast<int32_t>(bits & 0xffffffffu);
+    if (lane == 32 && gw + 1 < p.B * p.W) o.pk[gw + 1] = static_cast<int32_t>(bits >> 32);
+    o.pk += p.B * p.W;
   }
 }
 
-template <bool PRE, bool SPK, bool PK>
+template <bool PRE, bool SPK, bool PK, int RULE, bool CK>
 __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t g = gid >> 5;
@@ -1896,16 +1912,24 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const int64_t b = g / p.W;
   const int64_t n = (g - b * p.W) * 32 + bit;
   const bool act = (b < p.B) && (n < p.N);
-  const int64_t flat = b * p.N + n, BN = p.B * p.N;
+  const int64_t flat = act ? b * p.N + n : 0, BN = p.B * p.N;
   const int lane = static_cast<int>(threadIdx.x & 63);
+  const int64_t gw = (gid - lane) >> 5;  // the wave's first packed word
   float m = (act && p.m0 != nullptr) ? p.m0[flat] : 0.0f;
   float cnt = (act && p.counts != nullptr) ? p.counts[flat] : 0.0f;
   // checkpoint rows are counted from ck_origin: row k holds the state before
-  // step ck_origin + k*ckpt_every
-  int64_t ck_row = (p.t_begin - p.ck_origin + p.ckpt_every - 1) / p.ckpt_every;
-  int64_t next_ck = p.ck_origin + ck_row * p.ckpt_every;
-  // inactive lanes read element 0 and store nothing
-  const float *cur = p.cur + (act ? flat : 0);
+  // step ck_origin + k*ckpt_every.  Inactive lanes point at element 0 and
+  // store nothing.
+  CurCursor o{};
+  if constexpr (PRE) o.pre = p.pre + (p.t_begin - p.pre_origin) * BN + flat;
+  if constexpr (SPK) o.spk = p.spikes + p.t_begin * BN + flat;
+  if constexpr (PK) o.pk = p.packed + p.t_begin * p.B * p.W;
+  if constexpr (CK) {
+    const int64_t ck_row = (p.t_begin - p.ck_origin + p.ckpt_every - 1) / p.ckpt_every;
+    o.ck = p.ckpt + ck_row * BN + flat;
+    o.next_ck = p.ck_origin + ck_row * p.ckpt_every;
+  }
+  const float *cur = p.cur + flat;
   const int64_t L = p.t_end - p.t_begin;
   const int64_t nblk = (L + kPipe - 1) / kPipe;
   const int64_t f = L - (nblk - 1) * kPipe;
@@ -1919,8 +1943,7 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
     for (int u = 0; u < kPipe; ++u) nc[u] = cur[(r0 + u < L ? r0 + u : L - 1) * BN];
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      if (u < f)
-        cur_step<PRE, SPK, PK>(p, p.t_begin + u, cv[u], act, flat, BN, gid, lane, m, cnt, ck_row, next_ck);
+      if (u < f) cur_step<PRE, SPK, PK, RULE, CK>(p, p.t_begin + u, cv[u], act, BN, gw, lane, m, cnt, o);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) cv[u] = nc[u];
   }
@@ -1932,7 +1955,7 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u)
-      cur_step<PRE, SPK, PK>(p, p.t_begin + r0 + u, cv[u], act, flat, BN, gid, lane, m, cnt, ck_row, next_ck);
+      cur_step<PRE, SPK, PK, RULE, CK>(p, p.t_begin + r0 + u, cv[u], act, BN, gw, lane, m, cnt, o);
 #pragma unroll
     for (int u = 0; u < kPipe; ++u) cv[u] = nc[u];
   }
@@ -2198,12 +2221,28 @@ void launch_pre_bwd(const PreBwdArgs &a, bool gs, int gm, hipStream_t s) {
     launch_pre_bwd_v<SID, 1>(a, gs, gm, dim3(cdiv(a.BN, 256)), s);
 }
 
+template <bool PRE, bool SPK, bool PK>
+void launch_cur_rule(const CurArgs &a, dim3 grid, hipStream_t s) {
+  const bool ck = a.ckpt != nullptr;
+  if (a.rule == MYELIN_RULE_THRESHOLD) {
+    if (ck)
+      lif_currents_fwd<PRE, SPK, PK, MYELIN_RULE_THRESHOLD, true><<<grid, dim3(256), 0, s>>>(a);
+    else
+      lif_currents_fwd<PRE, SPK, PK, MYELIN_RULE_THRESHOLD, false><<<grid, dim3(256), 0, s>>>(a);
+  } else {
+    if (ck)
+      lif_currents_fwd<PRE, SPK, PK, MYELIN_RULE_SURROGATE, true><<<grid, dim3(256), 0, s>>>(a);
+    else
+      lif_currents_fwd<PRE, SPK, PK, MYELIN_RULE_SURROGATE, false><<<grid, dim3(256), 0, s>>>(a);
+  }
+}
+
 template <bool PRE, bool SPK>
 void launch_cur_pk(const CurArgs &a, bool pk, dim3 grid, hipStream_t s) {
   if (pk)
-    lif_currents_fwd<PRE, SPK, true><<<grid, dim3(256), 0, s>>>(a);
+    launch_cur_rule<PRE, SPK, true>(a, grid, s);
   else
-    lif_currents_fwd<PRE, SPK, false><<<grid, dim3(256), 0, s>>>(a);
+    launch_cur_rule<PRE, SPK, false>(a, grid, s);
 }
 
 void launch_currents(const CurArgs &a, dim3 grid, hipStream_t s) {
