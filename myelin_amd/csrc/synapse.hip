@@ -2011,6 +2011,31 @@ bool bf16_aligned(const void *q, int64_t ld, bool kcontig) {
   return kcontig ? (myelin::aligned(q, 16) && ld % 8 == 0) : (myelin::aligned(q, 8) && ld % 4 == 0);
 }
 
+#ifndef MYELIN_TALL_MIN_K
+#define MYELIN_TALL_MIN_K 2048  // k (all parts) from which bf16 k-contiguous products take 256 x 128 tiles
+#endif
+
+// bf16 operands, both k-contiguous, long K: 256 x 128 tiles of eight 64 x 64
+// waves (two per SIMD, one workgroup per CU, 110 KB of LDS).  A stage's
+// operand bytes from L2 per flop are 3/4 of the 128 x 128 tiles', which
+// pays on long K when the tiles fill whole rounds of 256 CUs: at 4096
+// columns and K = 3 x 1024, 8192 rows (4 rounds) 274 -> 242 us and 7200
+// rows (3.6) 251 -> 235 us, but 6400 rows (3.1: a last round 1/8 full)
+// 209 -> 224 us.  So they run when the last round is at least half full.
+// Short K (784, 12 stages) measured slower (137 vs 113 us).
+bool use_tall(const GemmArgs &g, int ta, int tb, bool half) {
+  if (!half || ta || !tb || g.M < 256 || g.K * g.parts < MYELIN_TALL_MIN_K) return false;
+  const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);
+  return tiles >= 256 && (tiles % 256 == 0 || tiles % 256 >= 128);
+}
+
+void launch_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (g.parts > 1)
+    gemm_big<1, false, true, uint16_t, 256, 128, true><<<grid, dim3(512), 0, s>>>(g);
+  else
+    gemm_big<1, false, true, uint16_t, 256, 128><<<grid, dim3(512), 0, s>>>(g);
+}
+
 template <int PREC, bool TA, bool TB, int BM, int BN>
 void launch_big(const GemmArgs &g, bool half, dim3 grid, hipStream_t s) {
   constexpr int NT = BM * BN / 64;
@@ -2148,6 +2173,16 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     return myelin::launched("gemm (small K)");
   }
   const bool big = !bits && (half || use_big(g));
+  if constexpr (PREC == 1) {
+    if (!bits && use_tall(g, ta, tb, half)) {
+      const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);
+      if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
+      g.kchunk = cdiv(g.K, Prec<1>::KS) * Prec<1>::KS;  // no K split
+      g.splits = 1;
+      launch_tall(g, dim3(static_cast<unsigned>(tiles)), s);
+      return myelin::launched("gemm (256 x 128 tiles)");
+    }
+  }
   const int64_t edge = big ? kBig : kTile;
   const int64_t tiles = cdiv(g.N, edge) * cdiv(g.M, edge);
   if (!big && cdiv(g.M, kTile) > 65535) return myelin::invalid("gemm: M too large (%lld)", (long long)g.M);
