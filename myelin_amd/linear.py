@@ -27,6 +27,7 @@ fp32 atomics, triton/lif.py:1336-1348).
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Any
 
@@ -90,24 +91,43 @@ def _gemm_parts(A, B, parts, b_part, C, M, N, K, lda, ldb, ldc, trans_a, trans_b
 _SPLIT_MIN_MACS = 1 << 32
 
 
-def _split_synapse(x, w, stream):
+class _Split:
     """The fp32 synapse on the bf16 MFMA, exactly: when every input value is
     a bf16 value (spikes, small integers), ``x @ W = x @ W_hi + x @ W_mid +
     x @ W_lo`` with the three bf16 planes of W summing exactly to W, so every
     product is exact and only the fp32 summation rounds -- at the bf16
-    engine's rate (about 5x the fp32 one per pass).  Returns the bf16 copy
-    of x and the transposed planes ``[3, N, F]``, or None when some input
-    value is not bf16-exact (then the fp32 GEMMs run)."""
+    engine's rate (about 5x the fp32 one per pass).
 
-    xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
-    flag = torch.zeros(1, dtype=torch.int32, device=x.device)
-    _lib.call("myelin_cast_bf16_checked", _lib.ptr(x), _lib.ptr(xb), x.numel(), _lib.ptr(flag), stream)
-    if int(flag.item()) != 0:
-        return None
-    F, N = w.shape
-    w3 = torch.empty((3, N, F), dtype=torch.bfloat16, device=w.device)
-    _lib.call("myelin_split_bf16x3", _lib.ptr(w), _lib.ptr(w3), F, N, 1, stream)
-    return xb, w3
+    Construction launches the checked bf16 copy of x (``xb``), the split of
+    W into transposed planes ``w3 [3, N, F]`` and an asynchronous copy of
+    the check's flag to pinned host memory, without waiting.  ``exact()``
+    waits for the flag alone (not for later work on the stream) and caches
+    the answer; when it is False the fp32 GEMMs must run instead."""
+
+    def __init__(self, x, w, stream):
+        self.xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        flag = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _lib.call("myelin_cast_bf16_checked", _lib.ptr(x), _lib.ptr(self.xb), x.numel(), _lib.ptr(flag), stream)
+        self._host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self._host.copy_(flag, non_blocking=True)
+        self._ready = torch.cuda.Event()
+        self._ready.record(torch.cuda.current_stream(x.device))
+        F, N = w.shape
+        self.w3 = torch.empty((3, N, F), dtype=torch.bfloat16, device=w.device)
+        _lib.call("myelin_split_bf16x3", _lib.ptr(w), _lib.ptr(self.w3), F, N, 1, stream)
+        self._exact = None
+
+    def exact(self) -> bool:
+        if self._exact is None:
+            self._ready.synchronize()
+            self._exact = int(self._host[0]) == 0
+        return self._exact
+
+
+def _split_synapse(x, w, stream):
+    """Start the exact split of ``x @ W`` (see _Split)."""
+
+    return _Split(x, w, stream)
 
 
 def _split_eligible(prec: int, T: int, B: int, F: int, N: int) -> bool:
@@ -199,7 +219,7 @@ def _span(T: int, checkpoint: int, BN: int) -> int:
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
              spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, exact=False,
-             pre_from=None):
+             pre_from=None, split=None, x32=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
@@ -216,6 +236,12 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     ``exact``: the GEMM never splits K, so a checkpointed forward and the
     backward's recompute of any chunk of it produce the same currents bit
     for bit (the fused kernel always sums that way).
+    ``split`` (a _Split whose ``xb`` / ``w3`` are passed as x / wt, with
+    ``x32`` the same steps of the fp32 input): the first chunk's GEMM is
+    launched on the split before ``split.exact()`` is asked, so the GPU
+    works while the host waits for the check; if the input is not
+    bf16-exact that GEMM is redone on the fp32 engine into the same buffer
+    and every later chunk takes the fp32 engine.
     """
 
     T, B, F = x.shape
@@ -225,7 +251,7 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     if _fused(B, N):
         if pre_from not in (None, t0):
             raise ValueError("pre_from is a chunked-route option")
-        if parts:
+        if parts or split is not None:
             raise ValueError("the split synapse is a chunked-route option")
         outs = (_lib.ptr(b), _lib.ptr(m0), _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(packed),
                 _lib.ptr(rates), _lib.ptr(ckpt), T, B, F, N, t0, t1, ckpt_every, decay, threshold, reset, slope, rule)
@@ -267,19 +293,27 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
         else:
             _gemm(x[c0:c1], w, cur, rows, N, F, F, N, N, False, False, False, prec, s, bias=b, split=not exact)
 
+    def fallback():
+        # the input was not bf16-exact: the fp32 engine from here on
+        nonlocal x, wt, half, parts
+        x, wt, half, parts = x32, None, False, False
+
     for c in range(n):
         c0, c1 = bounds[c], bounds[c + 1]
         i = c % len(curs)
         cur = curs[i]
-        if overlap:
-            with torch.cuda.stream(side):
-                if c >= 2:
-                    side.wait_event(used[i])
-                gemm(c0, c1, cur, side.cuda_stream)
+        s_ = side.cuda_stream if overlap else stream
+        with torch.cuda.stream(side) if overlap else contextlib.nullcontext():
+            if overlap and c >= 2:
+                side.wait_event(used[i])
+            gemm(c0, c1, cur, s_)
+            if c == 0 and split is not None and not split.exact():
+                fallback()
+                gemm(c0, c1, cur, s_)
+            if overlap:
                 done[i].record(side)
+        if overlap:
             main.wait_event(done[i])
-        else:
-            gemm(c0, c1, cur, stream)
         last = c1 == t1
         with_pre = pre is not None and c0 >= p0
         _lib.call(
@@ -294,7 +328,7 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     if overlap:
         # the main stream waited on every side GEMM; the inputs' and buffers'
         # last users include the side stream
-        for t_ in (*curs, x, w, b, wt):
+        for t_ in (*curs, x, w, b, wt, x32, *(() if split is None else (split.xb, split.w3))):
             if t_ is not None:
                 t_.record_stream(side)
 
@@ -338,10 +372,10 @@ class HipLinearLIFFunction(torch.autograd.Function):
         need = any(ctx.needs_input_grad[:3])
         half = _half(prec, F, N)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
+        split = None
         if not half and _split_eligible(prec, T, B, F, N):
-            sp = _split_synapse(x, w, stream)
-            if sp is not None:
-                xs, wt = sp
+            split = _split_synapse(x, w, stream)
+            xs, wt = split.xb, split.w3
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
         if checkpoint is not None and _keep_trace(F, N):
@@ -362,7 +396,9 @@ class HipLinearLIFFunction(torch.autograd.Function):
                     pre = torch.empty((T - tail, B, N), dtype=x.dtype, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail)
+                 ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail, split=split, x32=x)
+        if split is not None and not split.exact():
+            xs, wt = x, None
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
         if need:

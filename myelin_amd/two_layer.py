@@ -115,11 +115,12 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(wh, stream)) if half else (x, None)
-        # spike inputs: the hidden synapse on the exact bf16 split
+        # spike inputs: the hidden synapse on the exact bf16 split (the first
+        # group's forward learns whether the input qualifies)
+        split = None
         if not half and _split_eligible(prec, T, B, F, H):
-            sp = _split_synapse(x, wh, stream)
-            if sp is not None:
-                xs, wt = sp
+            split = _split_synapse(x, wh, stream)
+            xs, wt = split.xb, split.w3
         for k in range(0, K, G):
             t0 = k * C
             t1 = min(t0 + G * C, T)
@@ -127,7 +128,10 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             _lif_fwd(xs[t0:t1], wh, bh, m_h, 0, L, decay, threshold, reset, slope, _lib.RULE_THRESHOLD, prec, stream,
                      m_final=m_h, spikes=None if hs is None else hs[:L],
                      packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
-                     ckpt_every=C, wt=wt, exact=need)
+                     ckpt_every=C, wt=wt, exact=need, split=split if k == 0 else None,
+                     x32=x[t0:t1] if k == 0 else None)
+            if k == 0 and split is not None and not split.exact():
+                xs, wt = x, None
             s_in = words[t0:t1] if hs is None else hs[:L]
             _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None if pre_o is None else pre_o[t0:t1], counts,
                            rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,

@@ -265,7 +265,9 @@ def test_split_recompute_reproduces_forward_trace_exactly(monkeypatch):
     w = ((torch.rand(F, N, generator=g) - 0.4) * 0.2).to(DEV)
     b = (torch.rand(N, generator=g) * 0.05).to(DEV)
     stream = _lib.stream(torch.device(DEV))
-    xb, w3 = L._split_synapse(x, w, stream)
+    sp = L._split_synapse(x, w, stream)
+    assert sp.exact()
+    xb, w3 = sp.xb, sp.w3
     args = (0.95, 1.0, 0.0, 5.0, _lib.RULE_THRESHOLD, _lib.PREC["fp32"], stream)
     pre = torch.empty(T, B, N, device=DEV)
     ck = torch.empty(T // C, B, N, device=DEV)
@@ -347,3 +349,33 @@ def test_parts_products_do_not_depend_on_the_rows_computed(parts):
     rows = torch.tensor([0, 1, 255, 256, 4097, M - 1])
     ref = sum(A[rows].double() @ Bs[p].double().t() for p in range(parts)) + bias.double()
     assert_norm_close(to_np(full[rows.to(DEV)]), ref.numpy(), 1e-5, "parts product vs float64")
+
+
+@pytest.mark.parametrize("variant", ["recompute", "packed"])
+def test_two_layer_non_exact_input_falls_back_to_the_fp32_engine(monkeypatch, variant):
+    """The first group's GEMM runs on the split before the input check
+    returns; an input that is not bf16-exact redoes it on the fp32 engine,
+    so rates and gradients equal the fp32-engine run bit for bit."""
+
+    _print_case(test="two_layer_split_fallback", variant=variant)
+    T, B, F, H, O, C = 23, 4, 64, 136, 10, 4
+    g = seeded(71)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float()
+    x[0, 2, 7] = 0.3  # not a bf16 value
+    wh = (torch.rand(F, H, generator=g) - 0.4) * 0.5
+    bh = torch.rand(H, generator=g) * 0.1
+    wo = (torch.rand(H, O, generator=g) - 0.4) * 0.4
+    bo = torch.rand(O, generator=g) * 0.1
+    grate = torch.randn(B, O, generator=g)
+    fn = {"recompute": myelin.two_layer_surrogate_lif_rate_recompute_forward,
+          "packed": myelin.two_layer_surrogate_lif_rate_packed_hidden_forward}[variant]
+    p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
+    res = []
+    for min_macs in (0, 1 << 62):
+        monkeypatch.setattr(L, "_SPLIT_MIN_MACS", min_macs)
+        leaves = [t.to(DEV).requires_grad_() for t in (x, wh, bh, wo, bo)]
+        r = fn(*leaves, p, surrogate="fast_sigmoid", surrogate_slope=5.0, checkpoint_size=C)
+        r.backward(grate.to(DEV))
+        res.append([to_np(r)] + [to_np(t.grad) for t in leaves])
+    for a, b in zip(res[0], res[1]):
+        assert np.array_equal(a, b)
