@@ -2023,6 +2023,10 @@ bool bf16_aligned(const void *q, int64_t ld, bool kcontig) {
 // rows (3.6) 251 -> 235 us, but 6400 rows (3.1: a last round 1/8 full)
 // 209 -> 224 us.  So they run when the last round is at least half full.
 // Short K (784, 12 stages) measured slower (137 vs 113 us).
+// 256 x 128 tiles for a product (bf16 operands, both k-contiguous, long K)
+// whose tiles fill whole-ish rounds of 256 workgroups.  (mn-contiguous
+// operands on these tiles, with a K split filling the rounds, measured
+// slower on the split dW: 348 vs 325 us at 1024 x 4096 x 3*7200.)
 bool use_tall(const GemmArgs &g, int ta, int tb, bool half) {
   if (!half || ta || !tb || g.M < 256 || g.K * g.parts < MYELIN_TALL_MIN_K) return false;
   const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);

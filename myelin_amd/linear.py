@@ -446,7 +446,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         g_spikes = None if rate else g_out
         g_rates = g_out if rate else None
         gx = torch.empty((T, B, F), device=dev) if need_x else None
-        gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) chunk overwrites it
+        gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
         gb_acc = torch.zeros((B, N), device=dev) if (need_b and b is not None) else None
         # the reverse pass walks spans of whole checkpoint chunks, as many as
         # keep a span's trace within _CURRENT_CHUNK_ELEMS: one recompute

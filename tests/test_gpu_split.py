@@ -379,3 +379,28 @@ def test_two_layer_non_exact_input_falls_back_to_the_fp32_engine(monkeypatch, va
         res.append([to_np(r)] + [to_np(t.grad) for t in leaves])
     for a, b in zip(res[0], res[1]):
         assert np.array_equal(a, b)
+
+
+def test_parts_product_mn_layouts_at_a_weight_gradient_shape():
+    """dW-shaped three-part product (A transposed, B planes row-major,
+    1024 x 4096 x 3*2000) with and without a K split, against float64 on a
+    few rows and columns."""
+
+    _print_case(test="parts_dw_shape")
+    M, N, K, parts = 1024, 4096, 2000, 3
+    g = seeded(321)
+    A = (torch.rand(K, M, generator=g) < 0.2).to(torch.bfloat16)  # stored [K, M]: op(A) = A^T
+    Bs = torch.randn(parts, K, N, generator=g).to(torch.bfloat16)
+    stream = _lib.stream(torch.device(DEV))
+    Ad, Bd = A.to(DEV), Bs.to(DEV)
+    rows = torch.tensor([0, 5, 511, 1023])
+    cols = torch.tensor([0, 77, 2048, 4095])
+    ref = sum(A[:, rows].double().t() @ Bs[p][:, cols].double() for p in range(parts))
+    outs = []
+    for split in (False, True):
+        C = torch.empty(M, N, device=DEV)
+        L._gemm_parts(Ad, Bd, parts, K * N, C, M, N, K, M, N, N, True, False, False, stream, split=split)
+        got = C[rows.to(DEV)][:, cols.to(DEV)]
+        assert_norm_close(to_np(got), ref.numpy(), 1e-5, f"split={split}")
+        outs.append(C)
+    assert_norm_close(to_np(outs[1]), to_np(outs[0]), 1e-6, "split vs unsplit")
