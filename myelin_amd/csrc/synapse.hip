@@ -424,6 +424,32 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   store_acc(g, acc, m0 + 32 * wm, n0 + 32 * wn + (lane & 31), lane, blockIdx.z);
 }
 
+// C (+)= sum over splits of the workspace planes (+ bias), four consecutive
+// columns per thread (N, ldc, C and the workspace all allow 16-byte
+// access): one 16-byte load per plane, adds in split order.
+__global__ __launch_bounds__(256) void splitk_reduce4(GemmArgs g) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i >= g.M * g.N) return;
+  const int64_t row = i / g.N, col = i - row * g.N;
+  float *dst = g.C + row * g.ldc + col;
+  f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (g.accumulate) v = *reinterpret_cast<const f4 *>(dst);
+  f4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t plane = g.M * g.N;
+#pragma unroll 4
+  for (int z = 0; z < g.splits; ++z) {
+    const f4 w = *reinterpret_cast<const f4 *>(g.ws + z * plane + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[e] = part[e] + w[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = v[e] + part[e];
+    if (g.bias != nullptr) v[e] = v[e] + g.bias[col + e];
+  }
+  *reinterpret_cast<f4 *>(dst) = v;
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= g.M * g.N) return;
@@ -438,6 +464,16 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
   v = v + part;
   if (g.bias != nullptr) v = v + g.bias[col];
   *dst = v;
+}
+
+// the split-K reduce: four columns per thread where rows and pointers allow
+void launch_reduce(const GemmArgs &g, hipStream_t s) {
+  const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && myelin::aligned(g.C, 16) && myelin::aligned(g.ws, 16);
+  const int64_t n = g.M * g.N;
+  if (v4)
+    splitk_reduce4<<<dim3((n / 4 + 255) / 256), dim3(256), 0, s>>>(g);
+  else
+    splitk_reduce<<<dim3((n + 255) / 256), dim3(256), 0, s>>>(g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1505,7 +1541,6 @@ template <int PREC, int BT, bool H>
 __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
   constexpr int CH = kBig / BT;
   constexpr int Q = BT / 2;
-  constexpr int KS = Prec<PREC>::KS;
   __shared__ BigFusedSmem<PREC> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
@@ -2159,7 +2194,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
       launch_narrow<PREC, false>(g, ta, tb, va, grid, s);
     if (int rc = myelin::launched("gemm (narrow)")) return rc;
     if (splits > 1) {
-      splitk_reduce<<<dim3(cdiv(g.M * g.N, 256)), dim3(256), 0, s>>>(g);
+      launch_reduce(g, s);
       return myelin::launched("gemm split-k reduce");
     }
     return MYELIN_OK;
@@ -2219,7 +2254,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   }
   if (int rc = myelin::launched("gemm")) return rc;
   if (splits > 1) {
-    splitk_reduce<<<dim3(cdiv(g.M * g.N, 256)), dim3(256), 0, s>>>(g);
+    launch_reduce(g, s);
     return myelin::launched("gemm split-k reduce");
   }
   return MYELIN_OK;
@@ -2340,7 +2375,7 @@ extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtyp
   GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;
-    splitk_reduce<<<dim3(cdiv(M * N, 256)), dim3(256), 0, myelin::as_hip(stream)>>>(g);
+    launch_reduce(g, myelin::as_hip(stream));
     return myelin::launched("gemm (K = 0)");
   }
   hipStream_t s = myelin::as_hip(stream);
@@ -2370,7 +2405,7 @@ extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts
   hipStream_t s = myelin::as_hip(stream);
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;
-    splitk_reduce<<<dim3(cdiv(M * N, 256)), dim3(256), 0, s>>>(g);
+    launch_reduce(g, s);
     return myelin::launched("gemm_parts (K = 0)");
   }
   return launch_gemm<1>(g, trans_a, trans_b, true, workspace_elems, s);
