@@ -371,6 +371,7 @@ def main() -> int:
     import torch
 
     import myelin_amd as myelin
+    from myelin_amd.autograd import BWD_CHUNK
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -445,7 +446,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "bwd_chunked<ALIF, C=8, fast_sigmoid, V=2>",
+            "kernel": f"bwd_chunked<ALIF, C={BWD_CHUNK}, fast_sigmoid, V=2>",
             "achieved": bwd_gbps,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

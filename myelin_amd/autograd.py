@@ -22,10 +22,11 @@ import torch
 from myelin_amd import _lib
 
 # chunk length of the checkpointed backward (a compiled kernel parameter,
-# 8 or 16).  8 keeps the backward at 122 VGPRs (4 waves/SIMD), so a
-# [T, 128, 4096] problem runs in one occupancy round; its extra checkpoint
-# traffic (1 B per neuron-step) costs less than the second round C=16 needs.
-BWD_CHUNK = 8
+# 8 or 16).  16 halves the checkpoint traffic of 8 (0.5 instead of 1 B per
+# neuron-step for ALIF, each way); the backward issues its loads a quarter
+# chunk at a time so its registers stay near those of 8.  ALIF [256, 128,
+# 4096] fast_sigmoid: forward 190.5 -> 183.5 us, backward 270 -> 268 us.
+BWD_CHUNK = 16
 
 
 def _chunks(T: int) -> int:

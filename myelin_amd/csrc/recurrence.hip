@@ -423,12 +423,13 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
 //   gc = q * slope * sigma'(c)
 //   gp = gm*(1 - s) + gc          -> grad_x[t]
 //   ga = ga*rho - beta*gc ;  gm = gp*decay
-template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD>
+// (steps J1 - 1 down to J0 of the chunk; the whole chunk by default)
+template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD, int J0 = 0, int J1 = C>
 __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int64_t t0, int len,
                                             const float (&gsb)[C][V], const float (&pre)[C][V],
                                             const float (&cv)[C][V], float (&gm)[V], float (&ga)[V]) {
 #pragma unroll
-  for (int j = C - 1; j >= 0; --j) {
+  for (int j = J1 - 1; j >= J0; --j) {
     if (GUARD && j >= len) continue;
     float g[V];
 #pragma unroll
@@ -522,22 +523,56 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
     for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (k * C + j) * BN + base);
     for (; k > 0; --k) {
       const int64_t t0 = k * C;
-      if constexpr (GS) {
+      if constexpr (C == 16) {
+        // Chunks of 16 hold twice the trace of chunks of 8; issuing the
+        // loads a quarter at a time, as the reverse walk frees registers,
+        // keeps the live set near that of chunk 8: grad_spikes(k) of the
+        // upper half | recompute(k) | ckpt, x(k-1) lower half | reverse
+        // steps 15..12 | grad_spikes(k) lower half | reverse 11..8 |
+        // x(k-1) upper half | reverse 7..0
+        if constexpr (GS) {
 #pragma unroll
-        for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+          for (int j = C / 2; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
+#pragma unroll
+        for (int j = 0; j < C / 2; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_reverse<ALIF, C, SID, V, GS, false, 3 * C / 4, C>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (GS) {
+#pragma unroll
+          for (int j = 0; j < C / 2; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_reverse<ALIF, C, SID, V, GS, false, C / 2, 3 * C / 4>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = C / 2; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_reverse<ALIF, C, SID, V, GS, false, 0, C / 2>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        if constexpr (GS) {
+#pragma unroll
+          for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
+        }
+        // keep the issue order: grad_spikes(k) | recompute(k) | ckpt, x(k-1) |
+        // reverse(k), so the reverse phase waits only for grad_spikes(k) while
+        // the loads of chunk k-1 stay in flight
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
+#pragma unroll
+        for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
+        __builtin_amdgcn_sched_barrier(0);
+        bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // keep the issue order: grad_spikes(k) | recompute(k) | ckpt, x(k-1) |
-      // reverse(k), so the reverse phase waits only for grad_spikes(k) while
-      // the loads of chunk k-1 stay in flight
-      __builtin_amdgcn_sched_barrier(0);
-      bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
-      __builtin_amdgcn_sched_barrier(0);
-      bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
-#pragma unroll
-      for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
-      __builtin_amdgcn_sched_barrier(0);
-      bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, t0, C, gsb, pre, cv, gm, ga);
-      __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (GS) {
 #pragma unroll
@@ -633,18 +668,27 @@ int launch_bwd_sid(const BwdArgs &a, hipStream_t stream) {
     if (ok) break;
     v >>= 1;
   }
-  const dim3 grid(blocks_for((a.BN + v - 1) / v));
   const bool gs = (SID != MYELIN_SG_NONE) && a.gs != nullptr;
+  // without a spike gradient the two-neuron chunk-16 kernel does not fit
+  // the register file (about 460 registers); one neuron per lane needs < 80
+  if (C == 16 && !gs) v = 1;
+  const dim3 grid(blocks_for((a.BN + v - 1) / v));
+  // gs implies SID != NONE, and v == 2 without gs implies C == 8: the
+  // constexpr guards keep the unreachable instances out of the library
   if (v == 2) {
-    if (gs)
-      bwd_chunked<ALIF, C, SID, 2, (SID != MYELIN_SG_NONE)><<<grid, dim3(256), 0, stream>>>(a);
-    else
+    if (gs) {
+      if constexpr (SID != MYELIN_SG_NONE)
+        bwd_chunked<ALIF, C, SID, 2, true><<<grid, dim3(256), 0, stream>>>(a);
+    } else if constexpr (C != 16) {
       bwd_chunked<ALIF, C, SID, 2, false><<<grid, dim3(256), 0, stream>>>(a);
+    }
   } else {
-    if (gs)
-      bwd_chunked<ALIF, C, SID, 1, (SID != MYELIN_SG_NONE)><<<grid, dim3(256), 0, stream>>>(a);
-    else
+    if (gs) {
+      if constexpr (SID != MYELIN_SG_NONE)
+        bwd_chunked<ALIF, C, SID, 1, true><<<grid, dim3(256), 0, stream>>>(a);
+    } else {
       bwd_chunked<ALIF, C, SID, 1, false><<<grid, dim3(256), 0, stream>>>(a);
+    }
   }
   return myelin::launched("bwd_chunked");
 }
