@@ -1217,6 +1217,35 @@ __device__ __forceinline__ void big_tile(uint32_t bid, uint32_t nblk, uint32_t t
   tn = __builtin_amdgcn_readfirstlane(in / gs);
 }
 
+// Writes a wave's WM x WN blocks of 32 x 32 to C (or to the split-K
+// workspace slice of blockIdx.y).  The per-element form measures faster
+// here than store_acc's.
+template <int WM, int WN>
+__device__ __forceinline__ void big_epilogue(const GemmArgs &g, const f32x16 (&acc)[WM][WN], int64_t m0, int64_t n0,
+                                             int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int64_t col = n0 + 32 * WN * wn + 32 * j + (lane & 31);
+    if (col >= g.N) continue;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + 32 * WM * wm + 32 * i + acc_row(r, lane);
+        if (row >= g.M) continue;
+        if (g.splits > 1) {
+          g.ws[(static_cast<int64_t>(blockIdx.y) * g.M + row) * g.N + col] = acc[i][j][r];
+        } else {
+          float *dst = g.C + row * g.ldc + col;
+          float v = g.accumulate ? *dst + acc[i][j][r] : acc[i][j][r];
+          if (g.bias != nullptr) v = v + g.bias[col];
+          *dst = v;
+        }
+      }
+    }
+  }
+}
+
 // BM x BN output tile; each wave owns WM x WN blocks of 32 x 32 (the
 // launched kernels: 2 x 2, one wave per 64 x 64 quarter).  MP: bf16 operands
 // summing g.parts B parts (a separate instantiation, so the one-part kernels
@@ -1264,28 +1293,196 @@ __attribute__((amdgpu_waves_per_eu(WM * WN > 4 ? 1 : 2))) void gemm_big(GemmArgs
     big_kloop<PREC, D>(la, lb, kb, ke, st, wm, wn, lane, acc);
   }
 
-  // (the per-element form measures faster here than store_acc's)
+  big_epilogue<WM, WN>(g, acc, m0, n0, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 product with both operands k-contiguous (A [M, K], B [N, K], rows
+// 16-byte aligned, K a multiple of 64), staged by direct global -> LDS loads.
+//
+// Each 16-byte piece of a stage (64 k of a row) goes from HBM / L2 straight
+// into LDS (global_load_lds_dwordx4): no staging registers and no LDS write
+// instructions, and the only wait on the loads is the vmcnt before each
+// stage's barrier.  One wave's load fills 1 KB of LDS in lane order, so rows
+// are unpadded (128 bytes); the chunk of logical k-group c (8 k) of tile row
+// r sits at position c ^ dma_swz(r), which keeps the fragment reads
+// (32 rows x one k-group per half-wave) on distinct banks.
+//
+// NS stages in LDS; per stage: wait for the stage's loads and barrier; read
+// all of the stage's fragments into registers; issue the loads of stage
+// s + NS - 1 into the buffer stage s - 1 used (whose readers all passed the
+// barrier); run the MFMAs.  Against register staging at 8192 x 4096 x 3 x
+// 1024 (256 x 128 tiles): 221 -> 208 us; on 128 x 128 tiles (two stages,
+// two workgroups per CU) it measured mixed (12800 x 784 x 2048: 64 -> 69
+// us), so those keep register staging.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int dma_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Loads of one operand tile: ROWS rows x 64 k, NP pieces per thread.
+template <int ROWS, int NT>
+struct DmaLoader {
+  static constexpr int NP = ROWS * 8 / NT;
+  static_assert(ROWS * 8 % NT == 0, "pieces per thread");
+  const uint16_t *q[NP];
+  int lds_off[NP];  // wave-uniform byte offset of the piece group in the tile
+
+  __device__ __forceinline__ void init(int tid, int w, const uint16_t *base, int64_t mn0, int64_t mn_total,
+                                       int64_t ld) {
+    const int64_t lim = mn_total - mn0;
 #pragma unroll
-  for (int j = 0; j < WN; ++j) {
-    const int64_t col = n0 + 32 * WN * wn + 32 * j + (lane & 31);
-    if (col >= g.N) continue;
+    for (int e = 0; e < NP; ++e) {
+      const int idx = e * NT + tid;
+      const int row = idx >> 3, pos = idx & 7;
+      const int c = pos ^ dma_swz(row);
+      // rows past the edge read the last row: they feed discarded outputs
+      const int64_t rc = row < lim ? row : lim - 1;
+      q[e] = base + (mn0 + rc) * ld + 8 * c;
+      lds_off[e] = (e * NT + w * 64) * 16;
+    }
+  }
+  // The loads are issued from inline assembly, outside the compiler's
+  // accounting of LDS writes in flight: the kernel waits for them itself
+  // (vmcnt before each stage's barrier, and vmcnt(0) after the last stage,
+  // before the epilogue's own loads).  M0 holds the wave's LDS base during
+  // each load.
+  __device__ __forceinline__ void issue(char *tile, int64_t k0) const {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(tile + lds_off[e])));
+      // M0 is the compiler's: saved and restored around the load (which
+      // reads it at issue)
+      uint32_t m0_saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+          : "=&s"(m0_saved)
+          : "v"(q[e] + k0), "s"(dst)
+          : "memory");
+    }
+  }
+  __device__ __forceinline__ void shift(int64_t d) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) q[e] += d;
+  }
+};
+
+template <int BM, int BN, bool MP, int NS>
+__global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma(GemmArgs g) {
+  constexpr int WM = 2, WN = 2;
+  constexpr int WGN = BN / 64;
+  constexpr int NT = BM * BN / 64;
+  constexpr int TILE = (BM + BN) * 128;  // bytes of one stage
+  // loads per thread per stage; a stage's wait leaves the NS - 2 later
+  // stages' loads in flight
+  constexpr int NL = (BM + BN) * 8 / NT;
+  static_assert(NS == 2 || NS == 3, "two or three stages");
+  // one array per stage, so every access names its stage's array: the
+  // compiler then sees that a stage's reads and the loads in flight into
+  // the other stages do not alias, and leaves those loads in flight
+  __shared__ __attribute__((aligned(1024))) char l0[TILE];
+  __shared__ __attribute__((aligned(1024))) char l1[TILE];
+  __shared__ __attribute__((aligned(1024))) char l2[NS > 2 ? TILE : 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / WGN, wn = w % WGN;
+  const uint32_t tiles_m = static_cast<uint32_t>((g.M + BM - 1) / BM);
+  const uint32_t tiles_n = static_cast<uint32_t>((g.N + BN - 1) / BN);
+  int64_t tm, tn;
+  big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+
+  DmaLoader<BM, NT> la;
+  DmaLoader<BN, NT> lb;
+  la.init(tid, w, static_cast<const uint16_t *>(g.A), m0, g.M, g.lda);
+  lb.init(tid, w, static_cast<const uint16_t *>(g.B), n0, g.N, g.ldb);
+
+  // fragment byte offsets in a stage: A rows, then B rows after BM rows
+  int fa[WM][4], fb[WN][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int c = 2 * ks + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
+      const int r = 32 * WM * wm + 32 * i + (lane & 31);
+      fa[i][ks] = r * 128 + ((c ^ dma_swz(r)) << 4);
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + 32 * WM * wm + 32 * i + acc_row(r, lane);
-        if (row >= g.M) continue;
-        if (g.splits > 1) {
-          g.ws[(static_cast<int64_t>(blockIdx.y) * g.M + row) * g.N + col] = acc[i][j][r];
-        } else {
-          float *dst = g.C + row * g.ldc + col;
-          float v = g.accumulate ? *dst + acc[i][j][r] : acc[i][j][r];
-          if (g.bias != nullptr) v = v + g.bias[col];
-          *dst = v;
-        }
+    for (int j = 0; j < WN; ++j) {
+      const int r = 32 * WN * wn + 32 * j + (lane & 31);
+      fb[j][ks] = (BM + r) * 128 + ((c ^ dma_swz(r)) << 4);
+    }
+  }
+
+  f32x16 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t per = (ke - kb) / 64;  // stages per part (the host checks 64 | K and 64 | kchunk)
+  const int64_t total = MP ? per * g.parts : per;
+  if (per > 0) {
+    int64_t k_next = kb, left = per;  // next stage to load: k and stages left in its part
+    auto issue = [&](char *tile) {
+      la.issue(tile, k_next);
+      lb.issue(tile + BM * 128, k_next);
+      k_next += 64;
+      if (MP && --left == 0) {
+        // next part: the same k range of the following B plane
+        left = per;
+        k_next = kb;
+        lb.shift(g.b_part);
+      }
+    };
+    // stage s: wait for its loads, barrier, read its fragments from cur,
+    // load stage s + NS - 1 into nxt (read in iteration s - 1, whose readers
+    // have all passed the barrier with their fragments in registers),
+    // multiply.  (Reading stage s + 1 during stage s's MFMAs needs a second
+    // fragment set, which spills the load pointers at two waves per SIMD.)
+    auto step = [&](const char *cur, char *nxt, int64_t s) {
+      if (NS > 2 && s + 1 < total)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NL * (NS - 2)) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // a bare barrier: the loads still in flight target other stages
+      asm volatile("s_barrier" ::: "memory");
+      bf16x8 a[4][WM], b[4][WN];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) a[ks][i] = *reinterpret_cast<const bf16x8 *>(cur + fa[i][ks]);
+#pragma unroll
+        for (int j = 0; j < WN; ++j) b[ks][j] = *reinterpret_cast<const bf16x8 *>(cur + fb[j][ks]);
+      }
+      if (s + NS - 1 < total) issue(nxt);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+    };
+    issue(l0);
+    if constexpr (NS > 2) {
+      if (total > 1) issue(l1);
+      for (int64_t s = 0; s < total; s += 3) {
+        step(l0, l2, s);
+        if (s + 1 < total) step(l1, l0, s + 1);
+        if (s + 2 < total) step(l2, l1, s + 2);
+      }
+    } else {
+      for (int64_t s = 0; s < total; s += 2) {
+        step(l0, l1, s);
+        if (s + 1 < total) step(l1, l0, s + 1);
       }
     }
   }
+  big_epilogue<WM, WN>(g, acc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -2068,7 +2265,31 @@ bool use_tall(const GemmArgs &g, int ta, int tb, bool half) {
   return tiles >= 256 && (tiles % 256 == 0 || tiles % 256 >= 128);
 }
 
+#ifndef MYELIN_GEMM_DMA
+#define MYELIN_GEMM_DMA 1
+#endif
+
+// Direct global -> LDS staging (gemm_dma): bf16 operands, both k-contiguous,
+// 16-byte aligned rows, whole 64-k stages in every part and K split.
+bool use_dma(const GemmArgs &g, int ta, int tb, bool half) {
+  return MYELIN_GEMM_DMA && half && !ta && tb && g.K % 64 == 0 && al16(g.A) && al16(g.B) && g.lda % 8 == 0 &&
+         g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0);
+}
+
+// three 48 KB stages (144 KB of LDS, one workgroup per CU): each stage's
+// loads are issued two stages ahead of its MFMAs
+void launch_dma_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (g.parts > 1)
+    gemm_dma<256, 128, true, 3><<<grid, dim3(512), 0, s>>>(g);
+  else
+    gemm_dma<256, 128, false, 3><<<grid, dim3(512), 0, s>>>(g);
+}
+
 void launch_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (use_dma(g, 0, 1, true)) {
+    launch_dma_tall(g, grid, s);
+    return;
+  }
   if (g.parts > 1)
     gemm_big<1, false, true, uint16_t, 256, 128, true><<<grid, dim3(512), 0, s>>>(g);
   else
