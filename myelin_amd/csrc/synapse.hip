@@ -1486,6 +1486,211 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
 }
 
 // ---------------------------------------------------------------------------
+// bf16 product with both operands mn-contiguous (A stored [K, M], B stored
+// [K, N]: the weight-gradient products x^T G), 128 x 128 tiles staged by
+// direct global -> LDS loads.
+//
+// A stage holds 64 k rows of each operand as stored: [64][128] bf16, 256
+// bytes a row.  The MFMA fragments (8 consecutive k of one column per lane)
+// come out of LDS through the transposing read ds_read_b64_tr_b16: within
+// each 16-lane group, lane r reads the 4 values at its own address and lane
+// i receives value i % 4 of lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12.
+// So lane r of a group points at row kb + r / 4, columns n0 + 4 (r % 4) ..
+// + 3, and lane i receives rows kb .. kb + 3 of column n0 + i; two reads
+// (kb and kb + 4) make the fragment.  The 16-byte chunk of columns 8c ..
+// 8c + 7 of row k sits at position c ^ (4 (k & 3)), which puts the 32
+// lanes of two groups (4 rows x 2 chunk pairs) on distinct banks.
+// A partial last stage (K, or a K split, not a multiple of 64) is loaded
+// with guarded vector loads (zeros past the end) and written with LDS
+// stores.
+// ---------------------------------------------------------------------------
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+__device__ __forceinline__ int mn_swz(int k) { return 4 * (k & 3); }
+
+// Loads of one mn-contiguous operand tile: 64 k rows x 128 columns, 4
+// pieces of 16 bytes per thread (256 threads).
+struct DmaLoaderMN {
+  static constexpr int NP = 4;
+  const uint16_t *q[NP];  // piece at k = 0 of the stage (row kk[e])
+  int kk[NP];
+  int lds_off[NP];
+  int64_t ld;
+
+  __device__ __forceinline__ void init(int tid, int w, const uint16_t *base, int64_t mn0, int64_t mn_total,
+                                       int64_t ld_) {
+    ld = ld_;
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int idx = e * 256 + tid;
+      const int k = idx >> 4, pos = idx & 15;
+      const int c = pos ^ mn_swz(k);
+      // columns past the edge read the last whole piece (the host checks
+      // that the column count is a multiple of 8): they feed discarded
+      // outputs
+      int64_t col = mn0 + 8 * c;
+      if (col + 8 > mn_total) col = mn_total - 8;
+      kk[e] = k;
+      q[e] = base + k * ld + col;
+      lds_off[e] = (e * 256 + w * 64) * 16;
+    }
+  }
+  // a whole stage: rows k0 .. k0 + 63
+  __device__ __forceinline__ void issue(char *tile, int64_t k0) const {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(tile + lds_off[e])));
+      uint32_t m0_saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+          : "=&s"(m0_saved)
+          : "v"(q[e] + k0 * ld), "s"(dst)
+          : "memory");
+    }
+  }
+  // a partial stage: rows k0 .. ke - 1, zeros after
+  __device__ __forceinline__ void tail(char *tile, int64_t k0, int64_t ke) const {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      u4 v = {0u, 0u, 0u, 0u};
+      if (k0 + kk[e] < ke) v = *reinterpret_cast<const u4 *>(q[e] + k0 * ld);
+      *reinterpret_cast<u4 *>(tile + lds_off[e] + lane * 16) = v;
+    }
+  }
+  __device__ __forceinline__ void shift(int64_t d) {
+#pragma unroll
+    for (int e = 0; e < NP; ++e) q[e] += d;
+  }
+};
+
+template <bool MP, int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_mn(GemmArgs g) {
+  constexpr int WM = 2, WN = 2, BM = 128, BN = 128;
+  constexpr int TILE = 2 * 64 * 256;  // bytes of one stage: A rows, then B rows
+  constexpr int NL = 2 * DmaLoaderMN::NP;
+  static_assert(NS == 2 || NS == 3, "two or three stages");
+  __shared__ __attribute__((aligned(1024))) char l0[TILE];
+  __shared__ __attribute__((aligned(1024))) char l1[TILE];
+  __shared__ __attribute__((aligned(1024))) char l2[NS > 2 ? TILE : 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
+  const uint32_t tiles_m = static_cast<uint32_t>((g.M + BM - 1) / BM);
+  const uint32_t tiles_n = static_cast<uint32_t>((g.N + BN - 1) / BN);
+  int64_t tm, tn;
+  big_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+
+  DmaLoaderMN la, lb;
+  la.init(tid, w, static_cast<const uint16_t *>(g.A), m0, g.M, g.lda);
+  lb.init(tid, w, static_cast<const uint16_t *>(g.B), n0, g.N, g.ldb);
+
+  // transposing-read byte offsets within a stage, per k-step (16 k) and
+  // half (k offsets 0..3 / 4..7): lane r of 16-lane group gq points at row
+  // 16 ks + 8 (gq >> 1) + 4 h + r / 4, columns c0 + 16 (gq & 1) + 4 (r % 4)
+  const int gq = lane >> 4, r16 = lane & 15;
+  int fa[WM][4][2], fb[WN][4][2];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = 16 * ks + 8 * (gq >> 1) + 4 * h + (r16 >> 2);
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+        const int col = 32 * (WM * wm + i) + 16 * (gq & 1) + 4 * (r16 & 3);
+        fa[i][ks][h] = k * 256 + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int col = 32 * (WN * wn + j) + 16 * (gq & 1) + 4 * (r16 & 3);
+        fb[j][ks][h] = 64 * 256 + k * 256 + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
+      }
+    }
+
+  f32x16 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t per = (ke - kb + 63) / 64;  // stages per part, the last maybe partial
+  const int64_t total = MP ? per * g.parts : per;
+  if (per > 0) {
+    int64_t k_next = kb, left = per;
+    auto issue = [&](char *tile) {
+      if (k_next + 64 <= ke) {
+        la.issue(tile, k_next);
+        lb.issue(tile + 64 * 256, k_next);
+      } else {
+        la.tail(tile, k_next, ke);
+        lb.tail(tile + 64 * 256, k_next, ke);
+      }
+      k_next += 64;
+      if (MP && --left == 0) {
+        left = per;
+        k_next = kb;
+        lb.shift(g.b_part);
+      }
+    };
+    auto frag = [&](const char *cur, int off0, int off1) {
+      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)((lds_void *)(cur + off0)));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)((lds_void *)(cur + off1)));
+      typedef short v8s __attribute__((ext_vector_type(8)));
+      const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      return __builtin_bit_cast(bf16x8, v);
+    };
+    // a partial stage (the last of a part) is loaded synchronously, so the
+    // loads in flight after it are the earlier stages': no allowance then
+    const bool ragged = (ke - kb) % 64 != 0;
+    auto is_tail = [&](int64_t t) { return ragged && (t % per) == per - 1; };
+    auto step = [&](const char *cur, char *nxt, int64_t s) {
+      if (NS > 2 && s + 1 < total && !is_tail(s + 1))
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NL * (NS - 2)) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // a tail stage was written with LDS stores: lgkmcnt(0) covers them
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      bf16x8 a[4][WM], b[4][WN];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) a[ks][i] = frag(cur, fa[i][ks][0], fa[i][ks][1]);
+#pragma unroll
+        for (int j = 0; j < WN; ++j) b[ks][j] = frag(cur, fb[j][ks][0], fb[j][ks][1]);
+      }
+      if (s + NS - 1 < total) issue(nxt);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+    };
+    issue(l0);
+    if constexpr (NS > 2) {
+      if (total > 1) issue(l1);
+      for (int64_t s = 0; s < total; s += 3) {
+        step(l0, l2, s);
+        if (s + 1 < total) step(l1, l0, s + 1);
+        if (s + 2 < total) step(l2, l1, s + 2);
+      }
+    } else {
+      for (int64_t s = 0; s < total; s += 2) {
+        step(l0, l1, s);
+        if (s + 1 < total) step(l1, l0, s + 1);
+      }
+    }
+  }
+  big_epilogue<WM, WN>(g, acc, m0, n0, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
 // Fused current GEMM + LIF recurrence.
 // ---------------------------------------------------------------------------
 struct LinArgs {
@@ -2285,6 +2490,25 @@ void launch_dma_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
     gemm_dma<256, 128, false, 3><<<grid, dim3(512), 0, s>>>(g);
 }
 
+// The same for bf16 operands both mn-contiguous (the weight-gradient
+// products) on 128 x 128 tiles (gemm_dma_mn): whole 16-byte column pieces
+// and aligned rows.
+bool use_dma_mn(const GemmArgs &g, int ta, int tb, bool half) {
+  return MYELIN_GEMM_DMA && half && ta && !tb && g.M % 8 == 0 && g.N % 8 == 0 && al16(g.A) && al16(g.B) &&
+         g.lda % 8 == 0 && g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0);
+}
+
+// two 32 KB stages (two workgroups per CU).  Against register staging,
+// measured beside it: the split dW of 1024 x 4096 x 3 x 7200 288 -> 175 us
+// (629 -> 1034 TF), 784 x 2048 x 12800 113 -> 82 us; three stages (one
+// workgroup per CU) measured 276 and 99 us.
+void launch_dma_mn(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (g.parts > 1)
+    gemm_dma_mn<true, 2><<<grid, dim3(256), 0, s>>>(g);
+  else
+    gemm_dma_mn<false, 2><<<grid, dim3(256), 0, s>>>(g);
+}
+
 void launch_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
   if (use_dma(g, 0, 1, true)) {
     launch_dma_tall(g, grid, s);
@@ -2301,6 +2525,12 @@ void launch_big(const GemmArgs &g, bool half, dim3 grid, hipStream_t s) {
   constexpr int NT = BM * BN / 64;
   if constexpr (PREC == 1) {
     if (half) {
+      if constexpr (TA && !TB && BM == 128 && BN == 128) {
+        if (use_dma_mn(g, 1, 0, true)) {
+          launch_dma_mn(g, grid, s);
+          return;
+        }
+      }
       if (g.parts > 1)
         gemm_big<1, TA, TB, uint16_t, BM, BN, true><<<grid, dim3(NT), 0, s>>>(g);
       else

@@ -354,6 +354,42 @@ def test_parts_products_do_not_depend_on_the_rows_computed(parts, K):
     assert_norm_close(to_np(full[rows.to(DEV)]), ref.numpy(), 1e-5, "parts product vs float64")
 
 
+@pytest.mark.parametrize("M,N,K,parts,accumulate", [
+    (1024, 4096, 1440, 3, True),   # a config 4 span dW at one chunk
+    (264, 1032, 1000, 3, True),    # ragged tiles, K ending in a partial stage
+    (136, 200, 104, 2, False),     # K = 64 + a partial stage of 40
+    (128, 128, 40, 3, False),      # a single partial stage per part
+    (8, 8, 64, 1, False),          # one piece of columns, clamped reads
+])
+def test_mn_contiguous_products_equal_the_k_contiguous_ones(M, N, K, parts, accumulate):
+    """C (+)= sum_p A^T B_p with A [K, M] and B_p [K, N] stored as the
+    weight-gradient products store them (both mn-contiguous: staged into LDS
+    as stored and read through the transposing LDS read) equals the same
+    product with both operands transposed to k-contiguous first (the other
+    staging) bit for bit: without a K split both sum every element over the
+    same k sequence.  And it is within 1e-5 of float64."""
+
+    _print_case(test="mn_vs_kc", M=M, N=N, K=K, parts=parts)
+    g = seeded(900 + M + parts)
+    A = (torch.rand(K, M, generator=g) < 0.2).to(torch.bfloat16)
+    Bs = torch.randn(parts, K, N, generator=g).to(torch.bfloat16)
+    C0 = torch.randn(M, N, generator=g)
+    Ad, Bd = A.to(DEV), Bs.to(DEV)
+    At, Bt = Ad.t().contiguous(), Bd.transpose(1, 2).contiguous()
+    stream = _lib.stream(torch.device(DEV))
+    mn = C0.to(DEV)
+    kc = C0.to(DEV)
+    L._gemm_parts(Ad, Bd, parts, K * N, mn, M, N, K, M, N, N, True, False, accumulate, stream, split=False)
+    L._gemm_parts(At, Bt, parts, N * K, kc, M, N, K, K, K, N, False, True, accumulate, stream, split=False)
+    assert torch.equal(mn, kc), "mn-contiguous and k-contiguous products differ"
+    ref = sum(A.double().t() @ Bs[p].double() for p in range(parts)) + (C0.double() if accumulate else 0)
+    assert_norm_close(to_np(mn), ref.numpy(), 1e-5, "mn-contiguous product vs float64")
+    # with a K split (the weight-gradient route): within 1e-5 of float64 too
+    sp = C0.to(DEV)
+    L._gemm_parts(Ad, Bd, parts, K * N, sp, M, N, K, M, N, N, True, False, accumulate, stream, split=True)
+    assert_norm_close(to_np(sp), ref.numpy(), 1e-5, "split mn-contiguous product vs float64")
+
+
 @pytest.mark.parametrize("variant", ["recompute", "packed"])
 def test_two_layer_non_exact_input_falls_back_to_the_fp32_engine(monkeypatch, variant):
     """The first group's GEMM runs on the split before the input check
