@@ -207,9 +207,14 @@ int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C,
 
 /*
  * myelin_gemm_f32 with operand types: a_dtype = b_dtype = MYELIN_DT_F32, or
- * MYELIN_DT_BF16 (bf16 values in memory, precision MYELIN_PREC_BF16 only,
- * always on 128 x 128 tiles; k-contiguous operand rows 16-byte aligned,
- * mn-contiguous ones 8-byte aligned).  bf16 operands give bit-identical
+ * MYELIN_DT_BF16 (bf16 values in memory, precision MYELIN_PREC_BF16 only;
+ * k-contiguous operand rows 16-byte aligned, mn-contiguous ones 8-byte
+ * aligned).  bf16 operands run on 128 x 128 tiles, or 256 x 128 tiles for
+ * long K with both operands k-contiguous; operands both k-contiguous or
+ * both mn-contiguous with 16-byte rows (and K a multiple of 64 for the
+ * former) are staged by direct global -> LDS loads.  Every bf16 engine sums
+ * each output element in the same k order, so without a K split the result
+ * depends neither on M nor on the engine.  bf16 operands give bit-identical
  * results to fp32 operands holding the same values, at half the bytes.
  * a_dtype = MYELIN_DT_BITS with b_dtype = MYELIN_DT_F32: A is packed spike
  * bits in myelin_pack's format (lda counts int32 words: A(m,k) is bit k of
@@ -235,8 +240,8 @@ int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
 /*
  * C (+)= sum over p < parts (1..8) of op(A) op(B_p) (+ bias), B_p = B +
  * p*b_part, all bf16 operands (alignment as myelin_gemm's bf16 operands,
- * for every part) on the 128 x 128 bf16 MFMA engine; each part's k range
- * is summed in turn into the same fp32 accumulators.  With A exactly
+ * for every part) on the bf16 MFMA engines; each part's k range is summed
+ * in turn into the same fp32 accumulators.  With A exactly
  * representable in bf16 (spikes) and B_p the three planes of
  * myelin_split_bf16x3, every product is exact and the result is an fp32
  * GEMM of the unsplit B to fp32 summation accuracy, at bf16 MFMA rate.
