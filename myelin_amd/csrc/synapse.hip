@@ -1367,11 +1367,14 @@ struct DmaLoader {
   }
 };
 
-template <int BM, int BN, bool MP, int NS>
-__global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma(GemmArgs g) {
-  constexpr int WM = 2, WN = 2;
-  constexpr int WGN = BN / 64;
-  constexpr int NT = BM * BN / 64;
+template <int BM, int BN, bool MP, int NS, int WM = 2, int WN = 2>
+__global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma(
+    GemmArgs g) {
+  constexpr int WGN = BN / (32 * WN);
+  constexpr int NT = 64 * (BM / (32 * WM)) * WGN;
+  // wave tiles above 64 x 64 read a stage's fragments in two halves (k
+  // steps 0-1, then 2-3) to stay within 256 registers
+  constexpr int KH = WM * WN > 4 ? 2 : 4;
   constexpr int TILE = (BM + BN) * 128;  // bytes of one stage
   // loads per thread per stage; a stage's wait leaves the NS - 2 later
   // stages' loads in flight
@@ -1450,22 +1453,25 @@ __global__ __launch_bounds__(BM * BN / 64) __attribute__((amdgpu_waves_per_eu(2)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       // a bare barrier: the loads still in flight target other stages
       asm volatile("s_barrier" ::: "memory");
-      bf16x8 a[4][WM], b[4][WN];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int k0 = 0; k0 < 4; k0 += KH) {
+        bf16x8 a[KH][WM], b[KH][WN];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) a[ks][i] = *reinterpret_cast<const bf16x8 *>(cur + fa[i][ks]);
+        for (int ks = 0; ks < KH; ++ks) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j) b[ks][j] = *reinterpret_cast<const bf16x8 *>(cur + fb[j][ks]);
+          for (int i = 0; i < WM; ++i) a[ks][i] = *reinterpret_cast<const bf16x8 *>(cur + fa[i][k0 + ks]);
+#pragma unroll
+          for (int j = 0; j < WN; ++j) b[ks][j] = *reinterpret_cast<const bf16x8 *>(cur + fb[j][k0 + ks]);
+        }
+        if (k0 == 0 && s + NS - 1 < total) issue(nxt);
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks)
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
       }
-      if (s + NS - 1 < total) issue(nxt);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-          for (int j = 0; j < WN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
     };
     issue(l0);
     if constexpr (NS > 2) {
@@ -2509,6 +2515,25 @@ void launch_dma_mn(const GemmArgs &g, dim3 grid, hipStream_t s) {
     gemm_dma_mn<false, 2><<<grid, dim3(256), 0, s>>>(g);
 }
 
+// 256 x 256 tiles of eight 128 x 64 waves (a quarter fewer fragment reads
+// per MFMA than 64 x 64 waves, twice the MFMAs per barrier), two 64 KB
+// stages, for long-K products with direct staging whose 256 x 256 tiles
+// fill whole-ish rounds of 256 workgroups.  Against the 256 x 128 tiles,
+// measured beside them: 8192 x 4096 x 3 x 1024 217 -> 179 us (1154 TF),
+// 7200 rows 201 -> 168 us, 8192 x 4096 x 3072 207 -> 174 us.
+bool use_wide(const GemmArgs &g, int ta, int tb, bool half) {
+  if (!use_dma(g, ta, tb, half) || g.M < 256 || g.N < 256 || g.K * g.parts < MYELIN_TALL_MIN_K) return false;
+  const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
+  return tiles >= 256 && (tiles % 256 == 0 || tiles % 256 >= 128);
+}
+
+void launch_dma_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (g.parts > 1)
+    gemm_dma<256, 256, true, 2, 4, 2><<<grid, dim3(512), 0, s>>>(g);
+  else
+    gemm_dma<256, 256, false, 2, 4, 2><<<grid, dim3(512), 0, s>>>(g);
+}
+
 void launch_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
   if (use_dma(g, 0, 1, true)) {
     launch_dma_tall(g, grid, s);
@@ -2664,11 +2689,19 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   }
   const bool big = !bits && (half || use_big(g));
   if constexpr (PREC == 1) {
-    if (!bits && use_tall(g, ta, tb, half)) {
-      const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);
+    if (!bits && use_wide(g, ta, tb, half)) {
+      const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
       if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
       g.kchunk = cdiv(g.K, Prec<1>::KS) * Prec<1>::KS;  // no K split
       g.splits = 1;
+      launch_dma_wide(g, dim3(static_cast<unsigned>(tiles)), s);
+      return myelin::launched("gemm (256 x 256 tiles)");
+    }
+    if (!bits && use_tall(g, ta, tb, half)) {
+      g.kchunk = cdiv(g.K, Prec<1>::KS) * Prec<1>::KS;  // no K split
+      g.splits = 1;
+      const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);
+      if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
       launch_tall(g, dim3(static_cast<unsigned>(tiles)), s);
       return myelin::launched("gemm (256 x 128 tiles)");
     }

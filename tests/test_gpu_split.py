@@ -324,18 +324,20 @@ def test_two_layer_hidden_split_matches_fp32_engine_and_oracle(monkeypatch, vari
                 assert_norm_close(a, t.grad, 1e-4, f"grad_{name} vs oracle")
 
 
-@pytest.mark.parametrize("parts,K", [(1, 1000), (3, 1000), (2, 1024), (3, 1024)])
-def test_parts_products_do_not_depend_on_the_rows_computed(parts, K):
+@pytest.mark.parametrize("parts,K,N", [(1, 1000, 1024), (3, 1000, 1024), (2, 1024, 1024), (3, 1024, 1024),
+                                         (3, 1024, 4096)])
+def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N):
     """A 128-row slice of a bf16 product of `parts` parts (no K split)
     equals the same rows of the 8192-row product bit for bit, as a
     checkpointed recompute needs; and the product is within 1e-5 of float64.
     K = 1000 ends in a partial stage (register-staged tiles throughout);
     with K = 1024 and two or three parts the 8192-row product runs on the
-    256 x 128 tiles staged by direct global -> LDS loads while the slices
-    run on the 128 x 128 register-staged tiles."""
+    256 x 128 tiles staged by direct global -> LDS loads (N = 1024) or on
+    the 256 x 256 ones (N = 4096), while the slices run on the 128 x 128
+    register-staged tiles."""
 
-    _print_case(test="parts_rows", parts=parts, K=K)
-    M, N = 8192, 1024
+    _print_case(test="parts_rows", parts=parts, K=K, N=N)
+    M = 8192
     g = seeded(123 + parts)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
     Bs = torch.randn(parts, N, K, generator=g).to(torch.bfloat16)
