@@ -1515,10 +1515,13 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 __device__ __forceinline__ int mn_swz(int k) { return 4 * (k & 3); }
 
-// Loads of one mn-contiguous operand tile: 64 k rows x 128 columns, 4
-// pieces of 16 bytes per thread (256 threads).
+// Loads of one mn-contiguous operand tile: 64 k rows x COLS columns (COLS /
+// 8 pieces of 16 bytes a row) over NT threads.
+template <int COLS, int NT>
 struct DmaLoaderMN {
-  static constexpr int NP = 4;
+  static constexpr int CPR = COLS / 8;  // pieces per row
+  static constexpr int NP = 64 * CPR / NT;
+  static_assert(64 * CPR % NT == 0, "pieces per thread");
   const uint16_t *q[NP];  // piece at k = 0 of the stage (row kk[e])
   int kk[NP];
   int lds_off[NP];
@@ -1529,8 +1532,8 @@ struct DmaLoaderMN {
     ld = ld_;
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
-      const int idx = e * 256 + tid;
-      const int k = idx >> 4, pos = idx & 15;
+      const int idx = e * NT + tid;
+      const int k = idx / CPR, pos = idx % CPR;
       const int c = pos ^ mn_swz(k);
       // columns past the edge read the last whole piece (the host checks
       // that the column count is a multiple of 8): they feed discarded
@@ -1539,7 +1542,7 @@ struct DmaLoaderMN {
       if (col + 8 > mn_total) col = mn_total - 8;
       kk[e] = k;
       q[e] = base + k * ld + col;
-      lds_off[e] = (e * 256 + w * 64) * 16;
+      lds_off[e] = (e * NT + w * 64) * 16;
     }
   }
   // a whole stage: rows k0 .. k0 + 63
@@ -1571,17 +1574,23 @@ struct DmaLoaderMN {
   }
 };
 
-template <bool MP, int NS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_mn(GemmArgs g) {
-  constexpr int WM = 2, WN = 2, BM = 128, BN = 128;
-  constexpr int TILE = 2 * 64 * 256;  // bytes of one stage: A rows, then B rows
-  constexpr int NL = 2 * DmaLoaderMN::NP;
+template <bool MP, int NS, int BM = 128, int BN = 128, int WM = 2, int WN = 2>
+__global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_mn(
+    GemmArgs g) {
+  constexpr int WGN = BN / (32 * WN);
+  constexpr int NT = 64 * (BM / (32 * WM)) * WGN;
+  constexpr int RA = 2 * BM, RB = 2 * BN;    // bytes of an A row and of a B row
+  constexpr int TILE = 64 * (RA + RB);       // bytes of one stage: A rows, then B rows
+  constexpr int KH = WM * WN > 4 ? 2 : 4;    // k steps read at a time (as gemm_dma)
+  using LA = DmaLoaderMN<BM, NT>;
+  using LB = DmaLoaderMN<BN, NT>;
+  constexpr int NL = LA::NP + LB::NP;
   static_assert(NS == 2 || NS == 3, "two or three stages");
   __shared__ __attribute__((aligned(1024))) char l0[TILE];
   __shared__ __attribute__((aligned(1024))) char l1[TILE];
   __shared__ __attribute__((aligned(1024))) char l2[NS > 2 ? TILE : 16];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / WGN, wn = w % WGN;
   const uint32_t tiles_m = static_cast<uint32_t>((g.M + BM - 1) / BM);
   const uint32_t tiles_n = static_cast<uint32_t>((g.N + BN - 1) / BN);
   int64_t tm, tn;
@@ -1590,7 +1599,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
   const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
 
-  DmaLoaderMN la, lb;
+  LA la;
+  LB lb;
   la.init(tid, w, static_cast<const uint16_t *>(g.A), m0, g.M, g.lda);
   lb.init(tid, w, static_cast<const uint16_t *>(g.B), n0, g.N, g.ldb);
 
@@ -1607,12 +1617,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
         const int col = 32 * (WM * wm + i) + 16 * (gq & 1) + 4 * (r16 & 3);
-        fa[i][ks][h] = k * 256 + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
+        fa[i][ks][h] = k * RA + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
       }
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int col = 32 * (WN * wn + j) + 16 * (gq & 1) + 4 * (r16 & 3);
-        fb[j][ks][h] = 64 * 256 + k * 256 + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
+        fb[j][ks][h] = 64 * RA + k * RB + (((col >> 3) ^ mn_swz(k)) << 4) + (col & 7) * 2;
       }
     }
 
@@ -1631,10 +1641,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     auto issue = [&](char *tile) {
       if (k_next + 64 <= ke) {
         la.issue(tile, k_next);
-        lb.issue(tile + 64 * 256, k_next);
+        lb.issue(tile + 64 * RA, k_next);
       } else {
         la.tail(tile, k_next, ke);
-        lb.tail(tile + 64 * 256, k_next, ke);
+        lb.tail(tile + 64 * RA, k_next, ke);
       }
       k_next += 64;
       if (MP && --left == 0) {
@@ -1661,22 +1671,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       // a tail stage was written with LDS stores: lgkmcnt(0) covers them
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      bf16x8 a[4][WM], b[4][WN];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int k0 = 0; k0 < 4; k0 += KH) {
+        bf16x8 a[KH][WM], b[KH][WN];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) a[ks][i] = frag(cur, fa[i][ks][0], fa[i][ks][1]);
+        for (int ks = 0; ks < KH; ++ks) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j) b[ks][j] = frag(cur, fb[j][ks][0], fb[j][ks][1]);
+          for (int i = 0; i < WM; ++i) a[ks][i] = frag(cur, fa[i][k0 + ks][0], fa[i][k0 + ks][1]);
+#pragma unroll
+          for (int j = 0; j < WN; ++j) b[ks][j] = frag(cur, fb[j][k0 + ks][0], fb[j][k0 + ks][1]);
+        }
+        if (k0 == 0 && s + NS - 1 < total) issue(nxt);
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks)
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
       }
-      if (s + NS - 1 < total) issue(nxt);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-          for (int j = 0; j < WN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
     };
     issue(l0);
     if constexpr (NS > 2) {
@@ -2534,6 +2547,30 @@ void launch_dma_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
     gemm_dma<256, 256, false, 2, 4, 2><<<grid, dim3(512), 0, s>>>(g);
 }
 
+#ifndef MYELIN_MN_WIDE_WANT
+#define MYELIN_MN_WIDE_WANT 256  // K splits bring 256 x 256 mn-contiguous products to this many workgroups
+#endif
+
+// mn-contiguous products on 256 x 256 tiles of eight 128 x 64 waves, the
+// K split filling the CUs: when the 128 x 128 tiles alone would fill under
+// one round of 256 CUs (and a workspace allows the split).  Measured beside
+// the 128 x 128 tiles: config 3's dW, 784 x 2048 x 12800 (112 tiles of
+// 128 x 128), 83 -> 63 us; at a full round (config 4's dW, 1024 x 4096 x 3
+// x 7200, 256 tiles) they measured slower, 174 against 182 us, and without
+// a K split far slower.  Splitting to 512 workgroups measured slower than
+// to 256 on both.
+bool use_dma_mn_wide(const GemmArgs &g, int ta, int tb, bool half) {
+  return use_dma_mn(g, ta, tb, half) && g.ws != nullptr && g.M >= 256 && g.N >= 256 &&
+         cdiv(g.M, 128) * cdiv(g.N, 128) < 256 && cdiv(g.M, 256) * cdiv(g.N, 256) >= 32;
+}
+
+void launch_dma_mn_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
+  if (g.parts > 1)
+    gemm_dma_mn<true, 2, 256, 256, 4, 2><<<grid, dim3(512), 0, s>>>(g);
+  else
+    gemm_dma_mn<false, 2, 256, 256, 4, 2><<<grid, dim3(512), 0, s>>>(g);
+}
+
 void launch_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
   if (use_dma(g, 0, 1, true)) {
     launch_dma_tall(g, grid, s);
@@ -2689,6 +2726,22 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   }
   const bool big = !bits && (half || use_big(g));
   if constexpr (PREC == 1) {
+    if (!bits && use_dma_mn_wide(g, ta, tb, half)) {
+      const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
+      if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
+      int64_t splits = g.ws != nullptr ? plan_splits<1>(tiles, g.K, MYELIN_MN_WIDE_WANT) : 1;
+      while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
+      g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
+      splits = cdiv(g.K, g.kchunk);
+      g.splits = static_cast<int>(splits);
+      launch_dma_mn_wide(g, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), s);
+      if (int rc = myelin::launched("gemm (mn-contiguous, 256 x 256 tiles)")) return rc;
+      if (splits > 1) {
+        launch_reduce(g, s);
+        return myelin::launched("gemm split-k reduce");
+      }
+      return MYELIN_OK;
+    }
     if (!bits && use_wide(g, ta, tb, half)) {
       const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
       if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
@@ -2824,6 +2877,11 @@ extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, 
   for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
     const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
     const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, MYELIN_SPLIT_WANT) : plan_splits<0>(tiles, K, MYELIN_SPLIT_WANT);
+    if (s > most) most = s;
+  }
+  if (precision == MYELIN_PREC_BF16) {
+    // the 256 x 256 mn-contiguous tiles
+    const int64_t s = plan_splits<1>(cdiv(M, 256) * cdiv(N, 256), K, MYELIN_MN_WIDE_WANT);
     if (s > most) most = s;
   }
   return most > 1 ? most * M * N : 0;

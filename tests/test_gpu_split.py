@@ -358,6 +358,7 @@ def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N):
 
 @pytest.mark.parametrize("M,N,K,parts,accumulate", [
     (1024, 4096, 1440, 3, True),   # a config 4 span dW at one chunk
+    (784, 2048, 2560, 1, False),   # config 3's dW shape: split, it runs on 256 x 256 tiles
     (264, 1032, 1000, 3, True),    # ragged tiles, K ending in a partial stage
     (136, 200, 104, 2, False),     # K = 64 + a partial stage of 40
     (128, 128, 40, 3, False),      # a single partial stage per part
