@@ -86,8 +86,11 @@ def test_pointer_types_are_plain():
 
 def test_gemm_workspace_size_is_host_only_and_covers_the_split():
     lib = _lib.load()
-    # 784 x 2048 output over K = 12800: 112 tiles of 128 x 128 -> split 5 ways
-    assert lib.myelin_gemm_workspace_elems(784, 2048, 12800, _lib.PREC["bf16"]) == 5 * 784 * 2048
+    # 784 x 2048 output over K = 12800: 112 tiles of 128 x 128 would split 5
+    # ways; the 32 tiles of 256 x 256 that mn-contiguous bf16 operands take
+    # split 8 ways, and the workspace covers the larger
+    assert lib.myelin_gemm_workspace_elems(784, 2048, 12800, _lib.PREC["bf16"]) == 8 * 784 * 2048
+    assert lib.myelin_gemm_workspace_elems(784, 2048, 12800, _lib.PREC["fp32"]) == 5 * 784 * 2048
     # enough tiles, or a short K: no split, no workspace
     assert lib.myelin_gemm_workspace_elems(12800, 2048, 784, _lib.PREC["bf16"]) == 0
     assert lib.myelin_gemm_workspace_elems(784, 2048, 100, _lib.PREC["fp32"]) == 0
