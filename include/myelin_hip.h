@@ -256,6 +256,30 @@ int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts,
                       float *workspace, int64_t workspace_elems,
                       myelin_stream_t stream);
 
+/* floats of device scratch myelin_gemm_noalloc holds per GPU (64 MiB) */
+#define MYELIN_NOALLOC_SCRATCH_ELEMS (16LL * 1024 * 1024)
+
+/*
+ * myelin_gemm with no workspace argument and no allocation of any kind: the
+ * K split's partial tiles go to a static device array of
+ * MYELIN_NOALLOC_SCRATCH_ELEMS floats that each GPU holds until the process
+ * ends.  Same kernels, split and result as myelin_gemm called with a
+ * workspace of myelin_gemm_workspace_elems(M, N, K, precision) floats.
+ * Returns MYELIN_EINVAL when that workspace size exceeds the array.  The
+ * first call on a device looks up the array's device address there (a
+ * host-side query).  All calls on one GPU share its array: calls that
+ * overlap in time on one GPU (two streams or two host threads at once)
+ * race on it.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.
+ */
+int myelin_gemm_noalloc(const void *A, int a_dtype, const void *B, int b_dtype,
+                        const float *bias, float *C, int64_t M, int64_t N,
+                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                        int trans_a, int trans_b, int accumulate,
+                        int precision, myelin_stream_t stream);
+
 
 /*
  * Streamed synapse fused ahead of the LIF update, over steps
