@@ -33,7 +33,13 @@ def _np(t):
 
 
 def main(ref_root: str) -> None:
-    sys.path.insert(0, str(pathlib.Path(ref_root) / "src"))
+    src = pathlib.Path(ref_root).resolve() / "src"
+    sys.path.insert(0, str(src))
+    import myelin
+
+    # this repository's `myelin` alias package must not stand in for the reference here
+    if not pathlib.Path(myelin.__file__).resolve().is_relative_to(src):
+        raise RuntimeError(f"`import myelin` resolved to {myelin.__file__}, not the reference under {src}")
     from myelin import packing as P
     from myelin.functional import surrogate_alif_unroll, surrogate_lif_unroll
     from myelin.kernels import linear_surrogate_lif_forward, linear_surrogate_lif_rate_forward

@@ -241,14 +241,15 @@ def test_modules_match_functional_paths():
     assert packed(x).data.shape == (8, 4, 1)
 
 
-def test_streamed_synapse_bf16_batch_subset():
+def test_streamed_synapse_bf16_T50_B256():
     """LinearSurrogateLIF(784 -> 2048, stream_synapse=True, atan, bf16 GEMM)
-    then LinearSurrogateLIFRate(2048 -> 10, atan), CE on spike counts, at
-    T=50 and a 32-row batch slice; oracle = fp32 torch path on bf16-rounded
-    weights (inputs are exactly 0/1)."""
+    then LinearSurrogateLIFRate(2048 -> 10, atan), CE on spike counts, at the
+    full [50, 256, 784] (the hidden dW is the 784 x 2048 x 12800 product with
+    its K split); oracle = fp32 torch path on bf16-rounded weights (inputs
+    are exactly 0/1)."""
 
-    _print_case(test="streamed_synapse_bf16_subset")
-    T, B, F, H, O = 50, 32, 784, 2048, 10
+    _print_case(test="streamed_synapse_bf16_T50_B256")
+    T, B, F, H, O = 50, 256, 784, 2048, 10
     g = seeded(3)
     rate_f = torch.rand(F, generator=g) * 0.2
     x = (torch.rand(T, B, F, generator=g) < rate_f).float()

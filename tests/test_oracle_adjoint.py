@@ -292,3 +292,28 @@ def test_rate_gradient_matches_spike_gradient_with_uniform_weights():
     s.backward(gr.expand_as(s) / x.shape[0])
     assert_norm_close(xr.grad, xs.grad, 1e-6, "grad_x")
     assert_norm_close(wr.grad, ws.grad, 1e-6, "grad_w")
+
+
+def test_matmul_rounding_knob():
+    """The oracle's "exact" matmul rounding (float64 products rounded once to
+    fp32) is an equally valid fp32 evaluation: same rasters, gradients within
+    fp32 rounding of the native ones, and not the same bits."""
+
+    x, w, b = _linear_case(11, T=12, B=3, F=64, N=17)
+    g = seeded(12)
+    gs = torch.randn(x.shape[0], x.shape[1], w.shape[1], generator=g)
+    out = {}
+    for mode in ("native", "exact"):
+        prev = R.set_matmul_rounding(mode)
+        xr, wr = x.clone().requires_grad_(), w.clone().requires_grad_()
+        _, s = R.linear_surrogate_lif_checkpoint(xr, wr, b, 9.0, 0.7, -0.2, "atan", 5.0, 5)
+        s.backward(gs)
+        R.set_matmul_rounding(prev)
+        out[mode] = (s, xr.grad, wr.grad)
+    assert R.set_matmul_rounding("native") == "native"
+    assert torch.equal(out["native"][0], out["exact"][0])
+    assert_norm_close(out["exact"][1], out["native"][1], 1e-5, "grad_x")
+    assert_norm_close(out["exact"][2], out["native"][2], 1e-5, "grad_w")
+    assert not torch.equal(out["exact"][2], out["native"][2])
+    with pytest.raises(ValueError):
+        R.set_matmul_rounding("tf32")
