@@ -36,6 +36,19 @@ typedef struct ihipStream_t *myelin_stream_t;
 /* spike rules */
 #define MYELIN_RULE_THRESHOLD 0 /* s = m' >= th            (neurons.py:112,124) */
 #define MYELIN_RULE_SURROGATE 1 /* s = slope*(m' - th) >= 0 (surrogates.py:108) */
+/* Rules that evaluate the surrogate primitive sigma(c), c = slope*(m' - th),
+ * op by op in fp32 as myelin's torch backend does (surrogates.py:29-75) and
+ * emit the spike value its autograd graph carries; the membrane then resets
+ * as m = m'*(1 - s) + reset*s and ALIF adapts as a = a*rho + s
+ * (functional.py:140-143,183-186).  Add the surrogate id (0-5).
+ *   MYELIN_RULE_STRAIGHT_THROUGH + id: s = (H(c) + sigma(c)) - sigma(c),
+ *     H(c) = c >= 0 (hard_surrogate_spike, surrogates.py:105-111); equal
+ *     to 0 or within a few ulp of 1.
+ *   MYELIN_RULE_SMOOTH + id: s = sigma(c) (hard_forward=False,
+ *     functional.py:141,184).
+ * Dense spikes only (packed output rejects them). */
+#define MYELIN_RULE_STRAIGHT_THROUGH 16
+#define MYELIN_RULE_SMOOTH 32
 
 /* surrogate ids, same numbering as triton/lif.py:356-370 */
 #define MYELIN_SG_SIGMOID 0
@@ -48,6 +61,20 @@ typedef struct ihipStream_t *myelin_stream_t;
  * lif_unroll / alif_unroll through the membrane path only (their spikes
  * carry no gradient, functional.py:21-78) */
 #define MYELIN_SG_NONE 6
+/* Backward surrogate codes for a forward run with MYELIN_RULE_STRAIGHT_THROUGH
+ * (resp. MYELIN_RULE_SMOOTH) + id: MYELIN_SG_AUTOGRAD (resp.
+ * MYELIN_SG_AUTOGRAD_SMOOTH) + id.  The recompute reproduces that forward
+ * and the adjoint is evaluated in the operation order and fp32 rounding of
+ * torch autograd through surrogate_lif_unroll / surrogate_alif_unroll
+ * (functional.py:115-189): per step, dL/ds = ((dL/ds_t + dL/da' +
+ * dL/dm'' * reset) - dL/dm'' * m'), then the primitive's own backward
+ * formulas (quotient rule for fast_sigmoid / superspike, sigmoid_backward,
+ * atan's 1/(1+p^2), clamp mask, erf's 2/sqrt(pi)*exp(-z^2)).  Chunk 16 only.
+ * The other codes (0-6) use the closed-form derivative sigma'(c) of
+ * surrogates.py:78-102, as the reference's Triton kernels do
+ * (triton/lif.py:225-249) with exact 0/1 spikes. */
+#define MYELIN_SG_AUTOGRAD 16
+#define MYELIN_SG_AUTOGRAD_SMOOTH 32
 
 /* GEMM input precision (accumulation is always fp32) */
 #define MYELIN_PREC_F32 0

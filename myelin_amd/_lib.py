@@ -19,7 +19,13 @@ LIB_PATH = pathlib.Path(os.environ.get("MYELIN_HIP_LIB", pathlib.Path(__file__).
 
 OK, EINVAL, EHIP = 0, 1, 2
 RULE_THRESHOLD, RULE_SURROGATE = 0, 1
+# + surrogate id: spike values of hard_surrogate_spike / the smooth primitive,
+# evaluated op by op as torch does
+RULE_STRAIGHT_THROUGH, RULE_SMOOTH = 16, 32
 SG_NONE = 6
+# + surrogate id: the backward in torch autograd's operation order, after a
+# forward run with RULE_STRAIGHT_THROUGH / RULE_SMOOTH + the same id
+SG_AUTOGRAD, SG_AUTOGRAD_SMOOTH = 16, 32
 PREC = {"fp32": 0, "bf16": 1}
 DT_BITS = 7  # packed spike bits (int32 words) as a GEMM operand
 DT_BF16X3 = 8  # three bf16 planes summing exactly to an fp32 tensor

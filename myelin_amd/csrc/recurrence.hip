@@ -116,9 +116,165 @@ struct FwdArgs {
   int64_t chunk;
 };
 
-// One neuron step.  Returns the spike; updates m (and a for ALIF).
+// ---------------------------------------------------------------------------
+// The surrogate primitives and their autograd backward, op by op.
+//
+// sg_smooth<SID>(c) is sigma(c) of surrogates.py:29-75 with every operation
+// rounded to fp32 in the order torch evaluates the expression (scalars are
+// fp32; `x / scalar` is a true division, as ATen's CPU kernel does it).
+// sg_grad_autograd<SID>(c, g) is dL/dc for dL/dsigma = g, evaluated as
+// torch autograd differentiates that expression: the derivative formula of
+// each primitive op, applied from the output back, and a tensor used twice
+// summing its two gradients.  The operations are IEEE-exact for
+// fast_sigmoid, superspike and triangular.  sigmoid, atan and
+// multi_gaussian also need exp / atan / erf: these are evaluated in double
+// and rounded once (the fp32 value nearest the true one), which is what
+// the host's vectorised fp32 versions return for all but a small fraction
+// of arguments (about 1 % for exp, 2 % for erf, 1e-4 for atan); where they
+// differ, the last bit differs.
+// ---------------------------------------------------------------------------
+constexpr float kPiF = 3.14159265358979323846f;
+
+__device__ __forceinline__ float exp_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+__device__ __forceinline__ float atan_rn(float x) { return static_cast<float>(atan(static_cast<double>(x))); }
+__device__ __forceinline__ float erf_rn(float x) { return static_cast<float>(erf(static_cast<double>(x))); }
+
+__device__ __forceinline__ float sign_of(float c) { return c > 0.0f ? 1.0f : (c < 0.0f ? -1.0f : 0.0f); }
+
+// 0.5 * (1 + erf((c - mean) / (sqrt(2) * sigma)))  (surrogates.py:61-62)
+__device__ __forceinline__ float normal_cdf(float c, float mean, float k) {
+  const float z = (c - mean) / k;
+  return 0.5f * (1.0f + erf_rn(z));
+}
+
+template <int SID>
+__device__ __forceinline__ float sg_smooth(float c) {
+  if constexpr (SID == MYELIN_SG_SIGMOID) {
+    return 1.0f / (1.0f + exp_rn(-c));
+  } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
+    // 0.5 * (c / (1 + |c|) + 1)
+    const float q = c / (1.0f + fabsf(c));
+    return 0.5f * (q + 1.0f);
+  } else if constexpr (SID == MYELIN_SG_ATAN) {
+    // atan(pi * c / 2) / pi + 0.5
+    const float p = (c * kPiF) / 2.0f;
+    return atan_rn(p) / kPiF + 0.5f;
+  } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
+    // (1 - |c|).clamp(0, 1)
+    return fminf(fmaxf(1.0f - fabsf(c), 0.0f), 1.0f);
+  } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
+    // c / (1 + |c|) + 0.5
+    return c / (1.0f + fabsf(c)) + 0.5f;
+  } else {
+    // 0.6 * cdf(c; 0, 0.5) + 0.2 * cdf(c; 1, 1) + 0.2 * cdf(c; -1, 1),
+    // sqrt(2) * sigma formed in double, as Python does, then rounded
+    const float center = 0.6f * normal_cdf(c, 0.0f, static_cast<float>(1.4142135623730951 * 0.5));
+    const float right = 0.2f * normal_cdf(c, 1.0f, static_cast<float>(1.4142135623730951));
+    const float left = 0.2f * normal_cdf(c, -1.0f, static_cast<float>(1.4142135623730951));
+    return (center + right) + left;
+  }
+}
+
+// d/dc of erf's argument chain: 2/sqrt(pi) * exp(-z^2) * g, then / k
+// (the erf and true-division backward formulas)
+__device__ __forceinline__ float normal_cdf_grad(float c, float mean, float k, float w, float g) {
+  const float z = (c - mean) / k;
+  const float gh = g * w;     // w * cdf(...)
+  const float gn = gh * 0.5f;  // 0.5 * (1 + erf(z))
+  const float ez = exp_rn(-(z * z));
+  const float gz = (static_cast<float>(1.1283791670955126) * ez) * gn;
+  return gz / k;
+}
+
+template <int SID>
+__device__ __forceinline__ float sg_grad_autograd(float c, float g) {
+  if constexpr (SID == MYELIN_SG_SIGMOID) {
+    // sigmoid_backward: g * (1 - y) * y
+    const float y = sg_smooth<SID>(c);
+    return (g * (1.0f - y)) * y;
+  } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID || SID == MYELIN_SG_SUPERSPIKE) {
+    // q = c / b, b = 1 + |c|: dq/dc = 1/b (numerator) and
+    // -q/b * sign(c) (denominator through abs), summed.  q/b has the sign
+    // of c (and is 0 where c is), so ((-gq) * (q/b)) * sign(c) is
+    // (-gq) * |q/b| exactly: a sign flip commutes with rounding.
+    const float b = 1.0f + fabsf(c);
+    const float gq = (SID == MYELIN_SG_FAST_SIGMOID) ? g * 0.5f : g;
+    const float g_num = gq / b;
+    const float q = c / b;
+    return g_num + (-gq) * fabsf(q / b);
+  } else if constexpr (SID == MYELIN_SG_ATAN) {
+    // (/ pi) -> atan: g / (p^2 + 1) -> (/ 2) -> (* pi)
+    const float p = (c * kPiF) / 2.0f;
+    const float g_at = g / kPiF;
+    const float g_p = g_at / (p * p + 1.0f);
+    return (g_p / 2.0f) * kPiF;
+  } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
+    // clamp passes g where min <= r <= max; rsub negates; abs: * sign(c)
+    const float r = 1.0f - fabsf(c);
+    const float g_r = (r >= 0.0f && r <= 1.0f) ? g : 0.0f;
+    return (-g_r) * sign_of(c);
+  } else {
+    const float g_center = normal_cdf_grad(c, 0.0f, static_cast<float>(1.4142135623730951 * 0.5), 0.6f, g);
+    const float g_right = normal_cdf_grad(c, 1.0f, static_cast<float>(1.4142135623730951), 0.2f, g);
+    const float g_left = normal_cdf_grad(c, -1.0f, static_cast<float>(1.4142135623730951), 0.2f, g);
+    // autograd reaches c through the last-built branch first
+    return (g_right + g_left) + g_center;
+  }
+}
+
+constexpr bool rule_autograd(int rule) { return rule >= MYELIN_RULE_STRAIGHT_THROUGH; }
+
+// Spike value of the straight-through (hard_surrogate_spike) or smooth rule
+// from the primitive's value sm = sigma(c).
+template <int RULE>
+__device__ __forceinline__ float spike_value(float c, float sm) {
+  if constexpr (RULE >= MYELIN_RULE_SMOOTH) {
+    return sm;
+  } else {
+    const float h = c >= 0.0f ? 1.0f : 0.0f;
+    return (h + sm) - sm;
+  }
+}
+
+template <int RULE>
+__device__ __forceinline__ float autograd_spike(float c) {
+  return spike_value<RULE>(c, sg_smooth<RULE & 15>(c));
+}
+
+// fast_sigmoid and superspike divide three numerators by b = 1 + |c| per
+// step (c in the primitive, q and the upstream gradient in its backward).
+// The backward shares one reciprocal y = 1/b (an IEEE division, so y is 1/b
+// rounded to nearest) and forms each quotient as
+//   q0 = x*y ; e = x - b*q0 (exact in an fma) ; q = q0 + e*y (one rounding).
+// With y within half an ulp of 1/b and q0 within one ulp of x/b, q is x/b
+// rounded to nearest (Markstein's theorem), i.e. the IEEE quotient, as long
+// as the residual e stays normal: |x| >= 2^-100 and x/b normal.  x = 0
+// gives a zero, of possibly the other sign.  (Checked against IEEE division
+// on the host for every fp32 significand of b with numerators in that
+// range.)
+constexpr bool sg_quotient_form(int sid) {
+  return sid == MYELIN_SG_FAST_SIGMOID || sid == MYELIN_SG_SUPERSPIKE;
+}
+
+__device__ __forceinline__ float div_by(float x, float b, float y) {
+  const float q0 = x * y;
+  const float e = __builtin_fmaf(-b, q0, x);
+  return __builtin_fmaf(e, y, q0);
+}
+
+// sigma(c) from q = c / (1 + |c|)
+template <int SID>
+__device__ __forceinline__ float sg_from_quotient(float q) {
+  if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
+    return 0.5f * (q + 1.0f);
+  } else {
+    return q + 0.5f;
+  }
+}
+
+// One neuron step.  Returns the spike value; updates m (and a for ALIF).
 template <bool ALIF, int RULE>
-__device__ __forceinline__ bool neuron_step(float &m, float &a, float x, const FwdArgs &p) {
+__device__ __forceinline__ float neuron_step(float &m, float &a, float x, const FwdArgs &p) {
   float mp = m * p.decay;
   mp = mp + x;
   float th = p.thr;
@@ -126,17 +282,27 @@ __device__ __forceinline__ bool neuron_step(float &m, float &a, float x, const F
     float ba = p.beta * a;
     th = p.thr + ba;
   }
-  bool s;
-  if constexpr (RULE == MYELIN_RULE_THRESHOLD) {
-    s = mp >= th;
+  float s;
+  if constexpr (rule_autograd(RULE)) {
+    // m'*(1 - s) + reset*s ; a*rho + s
+    const float c = p.slope * (mp - th);
+    s = autograd_spike<RULE>(c);
+    const float keep = mp * (1.0f - s);
+    m = keep + p.reset * s;
   } else {
-    float c = p.slope * (mp - th);
-    s = c >= 0.0f;
+    bool h;
+    if constexpr (RULE == MYELIN_RULE_THRESHOLD) {
+      h = mp >= th;
+    } else {
+      float c = p.slope * (mp - th);
+      h = c >= 0.0f;
+    }
+    m = h ? p.reset : mp;
+    s = h ? 1.0f : 0.0f;
   }
-  m = s ? p.reset : mp;
   if constexpr (ALIF) {
     float ra = a * p.rho;
-    a = ra + (s ? 1.0f : 0.0f);
+    a = ra + s;
   }
   return s;
 }
@@ -187,7 +353,7 @@ __global__ __launch_bounds__(256) void fwd_dense_generic(FwdArgs p) {
         cc = (cc + 1 == p.chunk) ? 0 : cc + 1;
         float sp[V];
 #pragma unroll
-        for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p) ? 1.0f : 0.0f;
+        for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p);
         st_stream<V>(p.spikes + t * BN + base, sp);
       }
     }
@@ -204,7 +370,7 @@ __device__ __forceinline__ void fwd_block(const FwdArgs &p, int64_t base, int64_
   for (int u = 0; u < U; ++u) {
     float sp[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p) ? 1.0f : 0.0f;
+    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p);
     st_stream<V>(p.spikes + (t0 + u) * p.BN + base, sp);
   }
 }
@@ -273,7 +439,7 @@ __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
     float xv[V], sp[V];
     ld_stream<V>(xv, p.x + t * BN + base);
 #pragma unroll
-    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], xv[v], p) ? 1.0f : 0.0f;
+    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], xv[v], p);
     st_stream<V>(p.spikes + t * BN + base, sp);
   }
   st<V>(p.m_final + base, m);
@@ -326,7 +492,7 @@ __global__ __launch_bounds__(256) void fwd_packed(FwdArgs p) {
         }
         cc = (cc + 1 == p.chunk) ? 0 : cc + 1;
         bool s = false;
-        if (active) s = neuron_step<ALIF, RULE>(m, a, cur[u], p);
+        if (active) s = neuron_step<ALIF, RULE>(m, a, cur[u], p) != 0.0f;
         const uint64_t bits = __ballot(s);
         int32_t *row = p.packed + t * words_per_step;
         if (lane == 0 && g_wave < words_per_step) row[g_wave] = static_cast<int32_t>(bits & 0xffffffffu);
@@ -388,10 +554,15 @@ struct BwdArgs {
 
 // Recompute one chunk forward from its checkpointed state: pre[j] = m'_t,
 // cv[j] = c_t = slope*(m'_t - th_t) (for SG_NONE: m'_t - th_t, so that
-// c >= 0 is the plain threshold test).  GUARD: only the first `len` steps.
-template <bool ALIF, int C, int SID, int V, bool GUARD>
+// c >= 0 is the plain threshold test), aux[j] = 1/(1 + |c_t|) for the
+// autograd-order quotient forms.  GUARD: only the first `len` steps.
+// FR: 0 for exact 0/1 spikes, else the forward's autograd rule
+// (straight-through / smooth), whose spike values the reset and the
+// adaptation carry.
+template <bool ALIF, int C, int SID, int V, bool GUARD, int FR, bool RZ>
 __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const float (&xb)[C][V], float (&m)[V],
-                                              float (&a)[V], float (&pre)[C][V], float (&cv)[C][V]) {
+                                              float (&a)[V], float (&pre)[C][V], float (&cv)[C][V],
+                                              float (&aux)[C][V]) {
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     if (GUARD && j >= len) break;
@@ -405,13 +576,30 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
         th = p.thr + ba;
       }
       const float c = (SID == MYELIN_SG_NONE) ? mp - th : p.slope * (mp - th);
-      const bool s = c >= 0.0f;
       pre[j][v] = mp;
       cv[j][v] = c;
-      m[v] = s ? p.reset : mp;
+      float s;
+      if constexpr (FR != 0) {
+        if constexpr (sg_quotient_form(SID)) {
+          // the reciprocal the reverse walk shares between its quotients
+          const float b = 1.0f + fabsf(c);
+          const float y = 1.0f / b;
+          aux[j][v] = y;
+          s = spike_value<FR>(c, sg_from_quotient<SID>(div_by(c, b, y)));
+        } else {
+          s = autograd_spike<FR>(c);
+        }
+        const float keep = mp * (1.0f - s);
+        // RZ: reset == 0, whose term only adds a zero
+        m[v] = RZ ? keep : keep + p.reset * s;
+      } else {
+        const bool h = c >= 0.0f;
+        s = h ? 1.0f : 0.0f;
+        m[v] = h ? p.reset : mp;
+      }
       if constexpr (ALIF) {
         float ra = a[v] * p.rho;
-        a[v] = ra + (s ? 1.0f : 0.0f);
+        a[v] = ra + s;
       }
     }
   }
@@ -419,15 +607,23 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
 
 // Walk one chunk backwards, storing grad_x for t0 + j.  Per step, with
 // gm = dL/dm_{t+1}, ga = dL/da_{t+1}:
-//   q  = gm*(reset - m') + gs_t + ga
-//   gc = q * slope * sigma'(c)
-//   gp = gm*(1 - s) + gc          -> grad_x[t]
-//   ga = ga*rho - beta*gc ;  gm = gp*decay
+//   closed form (FR == 0):
+//     q  = gm*(reset - m') + gs_t + ga
+//     gc = q * slope * sigma'(c)
+//     gp = gm*(1 - s) + gc          -> grad_x[t]
+//     ga = ga*rho - beta*gc ;  gm = gp*decay
+//   autograd order (FR != 0), s the forward's spike value:
+//     gS = ((gs_t + ga) + gm*reset) - gm*m'     (dL/ds, in the order the
+//           stack, adaptation, reset and m'*(1 - s) nodes deliver it)
+//     gd = sg_grad_autograd(c, gS) * slope      (dL/d(m' - th))
+//     gp = gm*(1 - s) + gd          -> grad_x[t]
+//     ga = ga*rho + (-gd)*beta ;  gm = gp*decay
 // (steps J1 - 1 down to J0 of the chunk; the whole chunk by default)
-template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD, int J0 = 0, int J1 = C>
+template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD, int FR, bool RZ, int J0 = 0, int J1 = C>
 __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int64_t t0, int len,
                                             const float (&gsb)[C][V], const float (&pre)[C][V],
-                                            const float (&cv)[C][V], float (&gm)[V], float (&ga)[V]) {
+                                            const float (&cv)[C][V], const float (&aux)[C][V], float (&gm)[V],
+                                            float (&ga)[V]) {
 #pragma unroll
   for (int j = J1 - 1; j >= J0; --j) {
     if (GUARD && j >= len) continue;
@@ -441,6 +637,44 @@ __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int6
         const float gp = s != 0.0f ? 0.0f : gm[v];
         g[v] = gp;
         if constexpr (ALIF) ga[v] = ga[v] * p.rho;
+        gm[v] = gp * p.decay;
+      } else if constexpr (FR != 0) {
+        float sv, b = 0.0f, y = 0.0f, q = 0.0f;
+        if constexpr (sg_quotient_form(SID)) {
+          b = 1.0f + fabsf(c);
+          y = aux[j][v];
+          q = div_by(c, b, y);
+          sv = spike_value<FR>(c, sg_from_quotient<SID>(q));
+        } else {
+          sv = autograd_spike<FR>(c);
+        }
+        const float G = gm[v];
+        float gS;
+        if constexpr (GS) {
+          gS = gsb[j][v];
+          if constexpr (ALIF) gS = gS + ga[v];
+          if constexpr (!RZ) gS = gS + G * p.reset;
+        } else if constexpr (ALIF) {
+          gS = RZ ? ga[v] : ga[v] + G * p.reset;
+        } else {
+          gS = G * p.reset;
+        }
+        gS = gS - G * pre[j][v];
+        float gc;
+        if constexpr (sg_quotient_form(SID)) {
+          // as sg_grad_autograd, with the shared reciprocal
+          const float gq = (SID == MYELIN_SG_FAST_SIGMOID) ? gS * 0.5f : gS;
+          gc = div_by(gq, b, y) + (-gq) * fabsf(div_by(q, b, y));
+        } else {
+          gc = sg_grad_autograd<SID>(c, gS);
+        }
+        const float gd = gc * p.slope;
+        const float gp = G * (1.0f - sv) + gd;
+        g[v] = gp;
+        if constexpr (ALIF) {
+          float r = ga[v] * p.rho;
+          ga[v] = r + (-gd) * p.beta;
+        }
         gm[v] = gp * p.decay;
       } else {
         const float dsdm = p.slope * sg_deriv<SID>(c);
@@ -478,7 +712,7 @@ __device__ __forceinline__ void bwd_load_ckpt(const BwdArgs &p, int64_t k, int64
 // full chunks then run as straight-line code, software-pipelined: the
 // checkpoint and x of chunk k-1 are loaded while chunk k is walked
 // backwards, and grad_spikes of chunk k while chunk k is recomputed.
-template <bool ALIF, int C, int SID, int V, bool GS>
+template <bool ALIF, int C, int SID, int V, bool GS, int FR, bool RZ = false>
 __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t base = gid * V;
@@ -501,7 +735,7 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
     for (int v = 0; v < V; ++v) ga[v] = 0.0f;
   }
 
-  float xb[C][V], gsb[C][V], pre[C][V], cv[C][V], m[V], a[V];
+  float xb[C][V], gsb[C][V], pre[C][V], cv[C][V], aux[C][V], m[V], a[V];
   if (rem > 0) {
     const int64_t t0 = Kf * C;
     bwd_load_ckpt<ALIF, V>(p, Kf, base, m, a);
@@ -513,8 +747,8 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
       for (int j = 0; j < C; ++j)
         if (j < rem) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
     }
-    bwd_recompute<ALIF, C, SID, V, true>(p, rem, xb, m, a, pre, cv);
-    bwd_reverse<ALIF, C, SID, V, GS, true>(p, base, t0, rem, gsb, pre, cv, gm, ga);
+    bwd_recompute<ALIF, C, SID, V, true, FR, RZ>(p, rem, xb, m, a, pre, cv, aux);
+    bwd_reverse<ALIF, C, SID, V, GS, true, FR, RZ>(p, base, t0, rem, gsb, pre, cv, aux, gm, ga);
   }
   if (Kf > 0) {
     int64_t k = Kf - 1;
@@ -535,25 +769,25 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
           for (int j = C / 2; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
         }
         __builtin_amdgcn_sched_barrier(0);
-        bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
         __builtin_amdgcn_sched_barrier(0);
         bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
 #pragma unroll
         for (int j = 0; j < C / 2; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, 3 * C / 4, C>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 3 * C / 4, C>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (GS) {
 #pragma unroll
           for (int j = 0; j < C / 2; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
         }
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, C / 2, 3 * C / 4>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, C / 2, 3 * C / 4>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = C / 2; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, 0, C / 2>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 0, C / 2>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
       } else {
         if constexpr (GS) {
@@ -564,13 +798,13 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
         // reverse(k), so the reverse phase waits only for grad_spikes(k) while
         // the loads of chunk k-1 stay in flight
         __builtin_amdgcn_sched_barrier(0);
-        bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
+        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
         __builtin_amdgcn_sched_barrier(0);
         bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
 #pragma unroll
         for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, t0, C, gsb, pre, cv, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -578,8 +812,8 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
 #pragma unroll
       for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + j * BN + base);
     }
-    bwd_recompute<ALIF, C, SID, V, false>(p, C, xb, m, a, pre, cv);
-    bwd_reverse<ALIF, C, SID, V, GS, false>(p, base, 0, C, gsb, pre, cv, gm, ga);
+    bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
+    bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, 0, C, gsb, pre, cv, aux, gm, ga);
   }
   st<V>(p.gm0 + base, gm);
   if constexpr (ALIF) st<V>(p.ga0 + base, ga);
@@ -593,15 +827,21 @@ int64_t blocks_for(int64_t lanes) { return (lanes + 255) / 256; }
 
 template <bool ALIF, int RULE>
 int launch_fwd(const FwdArgs &a, hipStream_t stream) {
+  constexpr bool AG = rule_autograd(RULE);
   if (a.packed != nullptr) {
-    const int64_t lanes = a.B * a.W * 32;
-    fwd_packed<ALIF, RULE, MYELIN_FWD_UNROLL><<<dim3(blocks_for(lanes)), dim3(256), 0, stream>>>(a);
-    return myelin::launched("fwd_packed");
+    if constexpr (AG) {
+      return myelin::invalid("spike rule %d emits spike values; packed output takes the threshold rules", RULE);
+    } else {
+      const int64_t lanes = a.B * a.W * 32;
+      fwd_packed<ALIF, RULE, MYELIN_FWD_UNROLL><<<dim3(blocks_for(lanes)), dim3(256), 0, stream>>>(a);
+      return myelin::launched("fwd_packed");
+    }
   }
-  // widest vector the pointers and BN allow
+  // widest vector the pointers and BN allow (at most 2 neurons per lane for
+  // the autograd rules, which are built at 1 and 2)
   const void *ptrs[] = {a.x, a.m0, a.m_final, a.spikes, a.ckpt_m, ALIF ? a.a0 : nullptr,
                         ALIF ? a.a_final : nullptr, ALIF ? a.ckpt_a : nullptr};
-  int v = MYELIN_FWD_VEC;
+  int v = (AG && MYELIN_FWD_VEC > 2) ? 2 : MYELIN_FWD_VEC;
   while (v > 1) {
     bool ok = (a.BN % v) == 0;
     for (const void *q : ptrs)
@@ -620,21 +860,38 @@ int launch_fwd(const FwdArgs &a, hipStream_t stream) {
   const dim3 grid(blocks_for(lanes));
   constexpr int U = MYELIN_FWD_UNROLL;
   if (a.ckpt_m != nullptr && a.chunk % U != 0) {
-    if (v == 4)
-      fwd_dense_generic<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
-    else if (v == 2)
-      fwd_dense_generic<ALIF, RULE, 2, U><<<grid, dim3(256), 0, stream>>>(a);
-    else
-      fwd_dense_generic<ALIF, RULE, 1, U><<<grid, dim3(256), 0, stream>>>(a);
+    if constexpr (AG) {
+      fwd_dense_generic<ALIF, RULE, 1, U><<<dim3(blocks_for(a.BN)), dim3(256), 0, stream>>>(a);
+    } else {
+      if (v == 4)
+        fwd_dense_generic<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
+      else if (v == 2)
+        fwd_dense_generic<ALIF, RULE, 2, U><<<grid, dim3(256), 0, stream>>>(a);
+      else
+        fwd_dense_generic<ALIF, RULE, 1, U><<<grid, dim3(256), 0, stream>>>(a);
+    }
     return myelin::launched("fwd_dense_generic");
   }
-  if (v == 4)
-    fwd_dense<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
-  else if (v == 2)
+  if (v == 2)
     fwd_dense<ALIF, RULE, 2, U><<<grid, dim3(256), 0, stream>>>(a);
-  else
+  else if (v == 1)
     fwd_dense<ALIF, RULE, 1, U><<<grid, dim3(256), 0, stream>>>(a);
+  else if constexpr (!AG)
+    fwd_dense<ALIF, RULE, 4, U><<<grid, dim3(256), 0, stream>>>(a);
   return myelin::launched("fwd_dense");
+}
+
+template <bool ALIF, int BASE>
+int launch_fwd_autograd(const FwdArgs &a, int sid, hipStream_t stream) {
+  switch (sid) {
+    case MYELIN_SG_SIGMOID: return launch_fwd<ALIF, BASE + MYELIN_SG_SIGMOID>(a, stream);
+    case MYELIN_SG_FAST_SIGMOID: return launch_fwd<ALIF, BASE + MYELIN_SG_FAST_SIGMOID>(a, stream);
+    case MYELIN_SG_ATAN: return launch_fwd<ALIF, BASE + MYELIN_SG_ATAN>(a, stream);
+    case MYELIN_SG_TRIANGULAR: return launch_fwd<ALIF, BASE + MYELIN_SG_TRIANGULAR>(a, stream);
+    case MYELIN_SG_SUPERSPIKE: return launch_fwd<ALIF, BASE + MYELIN_SG_SUPERSPIKE>(a, stream);
+    case MYELIN_SG_MULTI_GAUSSIAN: return launch_fwd<ALIF, BASE + MYELIN_SG_MULTI_GAUSSIAN>(a, stream);
+    default: return myelin::invalid("unknown spike rule %d", BASE + sid);
+  }
 }
 
 template <bool ALIF>
@@ -654,13 +911,19 @@ int fwd_entry(FwdArgs &a, int rule, hipStream_t stream) {
   a.W = (a.N + 31) / 32;
   if (rule == MYELIN_RULE_THRESHOLD) return launch_fwd<ALIF, MYELIN_RULE_THRESHOLD>(a, stream);
   if (rule == MYELIN_RULE_SURROGATE) return launch_fwd<ALIF, MYELIN_RULE_SURROGATE>(a, stream);
+  if (rule >= MYELIN_RULE_SMOOTH)
+    return launch_fwd_autograd<ALIF, MYELIN_RULE_SMOOTH>(a, rule - MYELIN_RULE_SMOOTH, stream);
+  if (rule >= MYELIN_RULE_STRAIGHT_THROUGH)
+    return launch_fwd_autograd<ALIF, MYELIN_RULE_STRAIGHT_THROUGH>(a, rule - MYELIN_RULE_STRAIGHT_THROUGH, stream);
   return myelin::invalid("unknown spike rule %d", rule);
 }
 
-template <bool ALIF, int C, int SID>
+// FR: 0 for the closed form, else the forward's autograd rule (the
+// smooth rule's kernels are built at one neuron per lane only)
+template <bool ALIF, int C, int SID, int FR>
 int launch_bwd_sid(const BwdArgs &a, hipStream_t stream) {
   const void *ptrs[] = {a.x, a.ckpt_m, a.gs, a.gmT, a.gx, a.gm0, a.ckpt_a, a.gaT, a.ga0};
-  int v = MYELIN_BWD_VEC;
+  int v = FR >= MYELIN_RULE_SMOOTH ? 1 : MYELIN_BWD_VEC;
   while (v > 1) {
     bool ok = (a.BN % v) == 0;
     for (const void *q : ptrs)
@@ -670,41 +933,62 @@ int launch_bwd_sid(const BwdArgs &a, hipStream_t stream) {
   }
   const bool gs = (SID != MYELIN_SG_NONE) && a.gs != nullptr;
   // without a spike gradient the two-neuron chunk-16 kernel does not fit
-  // the register file (about 460 registers); one neuron per lane needs < 80
-  if (C == 16 && !gs) v = 1;
+  // the register file (about 460 registers); one neuron per lane needs < 80.
+  // The autograd-order kernels without a spike gradient are built at one
+  // neuron per lane only.
+  if ((C == 16 || FR != 0) && !gs) v = 1;
   const dim3 grid(blocks_for((a.BN + v - 1) / v));
-  // gs implies SID != NONE, and v == 2 without gs implies C == 8: the
-  // constexpr guards keep the unreachable instances out of the library
+  // gs implies SID != NONE, and v == 2 without gs implies C == 8 and the
+  // closed form: the constexpr guards keep the unreachable instances out
+  // of the library
   if (v == 2) {
     if (gs) {
-      if constexpr (SID != MYELIN_SG_NONE)
-        bwd_chunked<ALIF, C, SID, 2, true><<<grid, dim3(256), 0, stream>>>(a);
-    } else if constexpr (C != 16) {
-      bwd_chunked<ALIF, C, SID, 2, false><<<grid, dim3(256), 0, stream>>>(a);
+      // reset == 0 (either sign): the autograd order's reset terms only add
+      // zeros, so the hard-forward kernel is also built without them
+      if constexpr (SID != MYELIN_SG_NONE && FR != 0 && FR < MYELIN_RULE_SMOOTH) {
+        if (a.reset == 0.0f) {
+          bwd_chunked<ALIF, C, SID, 2, true, FR, true><<<grid, dim3(256), 0, stream>>>(a);
+          return myelin::launched("bwd_chunked");
+        }
+      }
+      if constexpr (SID != MYELIN_SG_NONE && FR < MYELIN_RULE_SMOOTH)
+        bwd_chunked<ALIF, C, SID, 2, true, FR><<<grid, dim3(256), 0, stream>>>(a);
+    } else if constexpr (C != 16 && FR == 0) {
+      bwd_chunked<ALIF, C, SID, 2, false, FR><<<grid, dim3(256), 0, stream>>>(a);
     }
   } else {
     if (gs) {
       if constexpr (SID != MYELIN_SG_NONE)
-        bwd_chunked<ALIF, C, SID, 1, true><<<grid, dim3(256), 0, stream>>>(a);
+        bwd_chunked<ALIF, C, SID, 1, true, FR><<<grid, dim3(256), 0, stream>>>(a);
     } else {
-      bwd_chunked<ALIF, C, SID, 1, false><<<grid, dim3(256), 0, stream>>>(a);
+      bwd_chunked<ALIF, C, SID, 1, false, FR><<<grid, dim3(256), 0, stream>>>(a);
     }
   }
   return myelin::launched("bwd_chunked");
 }
 
+// code: a surrogate id (closed form) or MYELIN_SG_AUTOGRAD[_SMOOTH] + id
 template <bool ALIF, int C>
-int launch_bwd_c(const BwdArgs &a, int sid, hipStream_t stream) {
-  switch (sid) {
-    case MYELIN_SG_SIGMOID: return launch_bwd_sid<ALIF, C, MYELIN_SG_SIGMOID>(a, stream);
-    case MYELIN_SG_FAST_SIGMOID: return launch_bwd_sid<ALIF, C, MYELIN_SG_FAST_SIGMOID>(a, stream);
-    case MYELIN_SG_ATAN: return launch_bwd_sid<ALIF, C, MYELIN_SG_ATAN>(a, stream);
-    case MYELIN_SG_TRIANGULAR: return launch_bwd_sid<ALIF, C, MYELIN_SG_TRIANGULAR>(a, stream);
-    case MYELIN_SG_SUPERSPIKE: return launch_bwd_sid<ALIF, C, MYELIN_SG_SUPERSPIKE>(a, stream);
-    case MYELIN_SG_MULTI_GAUSSIAN: return launch_bwd_sid<ALIF, C, MYELIN_SG_MULTI_GAUSSIAN>(a, stream);
-    case MYELIN_SG_NONE: return launch_bwd_sid<ALIF, C, MYELIN_SG_NONE>(a, stream);
-    default: return myelin::invalid("unknown surrogate id %d", sid);
+int launch_bwd_c(const BwdArgs &a, int code, hipStream_t stream) {
+  switch (code) {
+#define MYELIN_BWD_CASES(SID)                                                                          \
+  case SID: return launch_bwd_sid<ALIF, C, SID, 0>(a, stream);                                       \
+  case MYELIN_SG_AUTOGRAD + SID:                                                                       \
+    return launch_bwd_sid<ALIF, C, SID, MYELIN_RULE_STRAIGHT_THROUGH + SID>(a, stream);                \
+  case MYELIN_SG_AUTOGRAD_SMOOTH + SID:                                                                \
+    if constexpr (C == 16) return launch_bwd_sid<ALIF, C, SID, MYELIN_RULE_SMOOTH + SID>(a, stream);   \
+    break;
+    MYELIN_BWD_CASES(MYELIN_SG_SIGMOID)
+    MYELIN_BWD_CASES(MYELIN_SG_FAST_SIGMOID)
+    MYELIN_BWD_CASES(MYELIN_SG_ATAN)
+    MYELIN_BWD_CASES(MYELIN_SG_TRIANGULAR)
+    MYELIN_BWD_CASES(MYELIN_SG_SUPERSPIKE)
+    MYELIN_BWD_CASES(MYELIN_SG_MULTI_GAUSSIAN)
+#undef MYELIN_BWD_CASES
+    case MYELIN_SG_NONE: return launch_bwd_sid<ALIF, C, MYELIN_SG_NONE, 0>(a, stream);
+    default: return myelin::invalid("unknown surrogate code %d", code);
   }
+  return myelin::invalid("surrogate code %d (smooth forward) needs chunk 16; got %d", code, C);
 }
 
 template <bool ALIF>

@@ -3,9 +3,12 @@ kernels.py:30-865).
 
 Same function names, positional and keyword arguments, defaults, return
 types and validation messages as the reference.  ``backend`` accepts every
-name the reference does; all of them select the single HIP path, so
-callers that pass ``"triton"``, ``"triton_generated"``, ``"auto"`` or
-``"torch"`` run unchanged.  Triton tile knobs (``block_size``, ``block_b``,
+name the reference does and every name runs the HIP kernels, so callers
+that pass ``"triton"``, ``"triton_generated"``, ``"auto"`` or ``"torch"``
+run unchanged.  For the surrogate LIF/ALIF forwards the name also picks the
+arithmetic the reference would have run: torch autograd's (straight-through
+spike values, autograd's operation order) or its fused GPU kernels' (0/1
+spikes, closed-form derivative).  Triton tile knobs (``block_size``, ``block_b``,
 ``block_n``, ``block_f``) are accepted and ignored: the HIP kernels pick
 their own launch shapes.  Inputs must be fp32 ROCm device tensors; there is
 no CPU fallback.
@@ -177,6 +180,25 @@ def alif_forward(
     return ALIFState(membrane=m, adaptation=a), spikes
 
 
+def _surrogate_codes(sid: int, hard_forward: bool, autograd_order: bool) -> tuple[int, int]:
+    """(forward spike rule, backward surrogate code) of one arithmetic.
+
+    ``autograd_order``: the arithmetic of myelin's torch backend
+    (``surrogate_*_unroll`` differentiated by autograd, functional.py:115-189):
+    straight-through spike values ``(H + sigma) - sigma`` (or ``sigma`` when
+    ``hard_forward=False``), reset ``m'(1 - s) + reset s`` and the adjoint
+    in autograd's operation order.  Otherwise the fused GPU kernels'
+    arithmetic (triton/lif.py:195-288): exact 0/1 spikes and the closed-form
+    ``sigma'(c)`` of surrogates.py:78-102.
+    """
+
+    if autograd_order:
+        if hard_forward:
+            return _lib.RULE_STRAIGHT_THROUGH + sid, _lib.SG_AUTOGRAD + sid
+        return _lib.RULE_SMOOTH + sid, _lib.SG_AUTOGRAD_SMOOTH + sid
+    return _lib.RULE_SURROGATE, sid
+
+
 def surrogate_lif_forward(
     inputs: torch.Tensor,
     initial_state: LIFState,
@@ -188,18 +210,30 @@ def surrogate_lif_forward(
     backend: Backend = "auto",
     block_size: int = 256,
 ) -> tuple[LIFState, torch.Tensor]:
-    """Hard-forward surrogate LIF with a fused reverse-time backward (kernels.py:249-337)."""
+    """Surrogate LIF with a fused reverse-time backward (kernels.py:249-337).
+
+    The backend picks the arithmetic the reference would run on a GPU
+    tensor: ``"torch"`` (and any backend with ``hard_forward=False``, which
+    the reference sends to torch) reproduces ``surrogate_lif_unroll`` under
+    torch autograd -- straight-through spike values and autograd's operation
+    order; ``"auto"``, ``"hip"``, ``"triton"`` and ``"triton_generated"``
+    run the fused kernels' arithmetic (0/1 spikes, closed-form derivative),
+    as the reference's Triton route does (triton/lif.py:195-288).
+    """
 
     sid = surrogate_id(surrogate)
     _check_backend(backend)
-    if not hard_forward:
-        raise ValueError("HIP surrogate LIF currently supports only hard_forward=True")
+    if not hard_forward and backend == "triton":
+        raise ValueError("Triton surrogate LIF currently supports only hard_forward=True")
+    if not hard_forward and backend == "triton_generated":
+        raise ValueError("generated Triton surrogate LIF currently supports only hard_forward=True")
     _check_inputs(inputs)
     m0 = _check_state(initial_state.membrane, inputs, "membrane")
+    rule, code = _surrogate_codes(sid, hard_forward, backend == "torch" or not hard_forward)
     with torch.cuda.device(inputs.device):
         m, spikes = HipLIFFunction.apply(
             inputs.contiguous(), m0, _f32(params.decay), _f32(params.threshold), _f32(params.reset),
-            _f32(surrogate_slope), _lib.RULE_SURROGATE, sid,
+            _f32(surrogate_slope), rule, code,
         )
     return LIFState(membrane=m), spikes
 
@@ -214,24 +248,30 @@ def surrogate_alif_forward(
     hard_forward: bool = True,
     backend: Backend = "auto",
 ) -> tuple[ALIFState, torch.Tensor]:
-    """Hard-forward surrogate ALIF with the fused two-state adjoint (kernels.py:340-392).
+    """Surrogate ALIF with the fused two-state adjoint (kernels.py:340-392).
 
-    The reference has no fused path here (it falls back to torch autograd);
-    the gradient matches autograd through ``surrogate_alif_unroll``.
+    The reference runs this only through torch autograd (``"auto"`` falls
+    back to it, kernels.py:374-389), so ``"auto"`` and ``"torch"`` reproduce
+    that arithmetic: straight-through spike values and the adjoint in
+    autograd's operation order, in the fused kernels.  ``"hip"``,
+    ``"triton"`` and ``"triton_generated"`` select the fused kernels' own
+    arithmetic (0/1 spikes, closed-form derivative); with
+    ``hard_forward=False`` every backend runs the smooth forward of
+    ``surrogate_alif_unroll`` in autograd order.
     """
 
     sid = surrogate_id(surrogate)
     _check_backend(backend)
-    if not hard_forward:
-        raise ValueError("HIP surrogate ALIF currently supports only hard_forward=True")
     _check_inputs(inputs)
     m0 = _check_state(initial_state.membrane, inputs, "membrane")
     a0 = _check_state(initial_state.adaptation, inputs, "adaptation")
+    autograd_order = backend in ("auto", "torch") or not hard_forward
+    rule, code = _surrogate_codes(sid, hard_forward, autograd_order)
     with torch.cuda.device(inputs.device):
         m, a, spikes = HipALIFFunction.apply(
             inputs.contiguous(), m0, a0, _f32(params.decay), _f32(params.adaptation_decay),
             _f32(params.threshold), _f32(params.beta), _f32(params.reset), _f32(surrogate_slope),
-            _lib.RULE_SURROGATE, sid,
+            rule, code,
         )
     return ALIFState(membrane=m, adaptation=a), spikes
 

@@ -91,9 +91,10 @@ class SurrogateLIFCell(nn.Module):
         self.hard_forward = hard_forward
 
     def forward(self, state: LIFState, input_current: torch.Tensor) -> tuple[LIFState, torch.Tensor]:
+        # the reference cell steps through torch ops: autograd arithmetic
         st, s = surrogate_lif_forward(input_current.unsqueeze(0), state, self.params,
                                       surrogate=surrogate_name(self.surrogate), surrogate_slope=self.surrogate_slope,
-                                      hard_forward=self.hard_forward)
+                                      hard_forward=self.hard_forward, backend="torch")
         return st, s[0]
 
 
@@ -111,15 +112,17 @@ class SurrogateALIFCell(nn.Module):
     def forward(self, state: ALIFState, input_current: torch.Tensor) -> tuple[ALIFState, torch.Tensor]:
         st, s = surrogate_alif_forward(input_current.unsqueeze(0), state, self.params,
                                        surrogate=surrogate_name(self.surrogate), surrogate_slope=self.surrogate_slope,
-                                       hard_forward=self.hard_forward)
+                                       hard_forward=self.hard_forward, backend="torch")
         return st, s[0]
 
 
 class TimeUnroll(nn.Module):
     """Run a cell over time-major ``[T, B, N]`` inputs in one fused launch
-    (modules.py:415-582); the initial state defaults to zeros."""
+    (modules.py:415-582); the initial state defaults to zeros.  The default
+    backend is ``"torch"``, as in the reference: surrogate cells then keep
+    the arithmetic of stepping the cell through torch ops."""
 
-    def __init__(self, cell: nn.Module, *, backend: Backend = "auto") -> None:
+    def __init__(self, cell: nn.Module, *, backend: Backend = "torch") -> None:
         super().__init__()
         self.cell = cell
         self.backend: Backend = backend

@@ -25,6 +25,11 @@ see ``tests/test_oracle_*.py``):
   float64 finite differences through the smooth (``hard_forward=False``)
   path, and golden vectors written from the reference itself
   (``tests/golden/make_golden.py``).
+* ``surrogate_adjoint_autograd_order`` -- equal, value for value, to
+  ``torch.autograd`` through the unrolls for every surrogate, LIF and ALIF,
+  hard and smooth forward, with a nonzero reset and final-state gradients
+  (``tests/test_oracle_adjoint.py``); three other summation orders of the
+  spike gradient are shown to differ.
 * packing -- ``numpy.packbits(bitorder="little")`` viewed as little-endian
   int32 (independent routine), the reference's vectors
   (``tests/test_packing.py:66-74,193-201``) and golden vectors.
@@ -239,6 +244,85 @@ def surrogate_alif_unroll(
         a = a * rho + s
         out.append(s)
     return m, a, torch.stack(out, 0)
+
+
+# ---------------------------------------------------------------------------
+# the adjoint of the surrogate unrolls in autograd's operation order
+# ---------------------------------------------------------------------------
+
+
+def _primitive_grad_autograd(name: str, c: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """dL/dc for dL/dsigma = g through the primitive of surrogates.py:29-75,
+    op by op as torch autograd differentiates it (each node's derivative
+    formula, from the output back; two uses of c summed)."""
+
+    if name in ("fast_sigmoid", "superspike"):
+        b = 1.0 + c.abs()
+        gq = g * 0.5 if name == "fast_sigmoid" else g
+        return gq / b + (-gq * ((c / b) / b)) * c.sign()  # div: numerator + (denominator via abs)
+    if name == "sigmoid":
+        y = torch.sigmoid(c)
+        return g * (1.0 - y) * y  # sigmoid_backward(grad, result)
+    if name == "atan":
+        p = torch.pi * c / 2.0
+        return (g / torch.pi) / (p * p + 1.0) / 2.0 * torch.pi  # (/pi) atan (/2) (pi*)
+    if name == "triangular":
+        r = 1.0 - c.abs()
+        return -(g * ((r >= 0.0) & (r <= 1.0)).to(g.dtype)) * c.sign()  # clamp mask, rsub, abs
+    if name == "multi_gaussian":
+        parts = []
+        for w, mean, sigma in ((0.6, 0.0, 0.5), (0.2, 1.0, 1.0), (0.2, -1.0, 1.0)):
+            k = 1.4142135623730951 * sigma
+            z = (c - mean) / k
+            parts.append(2.0 / math.sqrt(math.pi) * torch.exp(-(z.pow(2))) * (g * w * 0.5) / k)
+        return (parts[1] + parts[2]) + parts[0]  # the last-built branches reach c first
+    raise ValueError(f"unknown surrogate {name!r}")
+
+
+def surrogate_adjoint_autograd_order(inputs, m0, a0, grad_spikes, grad_m, grad_a, tau_mem, tau_adaptation,
+                                     threshold, reset, beta, surrogate, slope=10.0, hard_forward=True, alif=True):
+    """Gradients of ``surrogate_alif_unroll`` / ``surrogate_lif_unroll``
+    (functional.py:115-189) computed without autograd, in the operation
+    order and fp32 rounding that torch autograd uses for them.
+
+    Per step, reverse time, with G = dL/dm_{t+1}, A = dL/da_{t+1}:
+      dL/ds = ((gs_t + A) + G*reset) - G*m'   (the stack, adaptation, reset
+              and m'*(1 - s) nodes deliver their gradients in that order)
+      gd    = primitive_grad(c, dL/ds) * slope
+      gp    = G*(1 - s) + gd  -> dL/dx_t ;  A <- A*rho + (-gd)*beta ;
+      G     <- gp*decay
+    This is the order the HIP kernels' autograd-order mode evaluates.
+    Returns (grad_x, grad_m0, grad_a0 or None).
+    """
+
+    d = decay_from_tau(tau_mem)
+    rho = decay_from_tau(tau_adaptation) if alif else 0.0
+    m, a = m0, a0
+    trace = []
+    for x in inputs.unbind(0):
+        mp = m * d + x
+        th = threshold + beta * a if alif else threshold
+        c = slope * (mp - th)
+        sm = surrogate_primitive(surrogate, c)
+        s = ((c >= 0).to(c.dtype) + sm) - sm if hard_forward else sm
+        trace.append((mp, c, s))
+        m = mp * (1.0 - s) + reset * s
+        if alif:
+            a = a * rho + s
+    G = torch.zeros_like(m0) if grad_m is None else grad_m
+    A = torch.zeros_like(m0) if (grad_a is None or not alif) else grad_a
+    gx = torch.empty_like(inputs)
+    for t in range(inputs.shape[0] - 1, -1, -1):
+        mp, c, s = trace[t]
+        gs = grad_spikes[t] if grad_spikes is not None else torch.zeros_like(mp)
+        g_s = ((gs + A) + G * reset) - G * mp
+        gd = _primitive_grad_autograd(surrogate, c, g_s) * slope
+        gp = G * (1.0 - s) + gd
+        gx[t] = gp
+        if alif:
+            A = A * rho + (-gd) * beta
+        G = gp * d
+    return gx, G, (A if alif else None)
 
 
 # ---------------------------------------------------------------------------

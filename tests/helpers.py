@@ -37,3 +37,37 @@ def raster_agreement(a, b) -> float:
 
 def seeded(seed: int) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
+
+
+def elementwise_rel_err(a, b, floor: float = 1e-3) -> float:
+    """max |a - b| / max(|b|, floor * max|b|): a relative bound per element,
+    with elements below `floor` of the tensor's largest held to that floor."""
+
+    a = to_np(a).astype(np.float64)
+    b = to_np(b).astype(np.float64)
+    if b.size == 0:
+        return 0.0
+    top = np.abs(b).max()
+    if top == 0.0:
+        return float(np.abs(a).max())
+    scale = np.maximum(np.abs(b), floor * top)
+    return float((np.abs(a - b) / scale).max())
+
+
+def assert_elementwise_close(a, b, rtol: float, what: str = "", floor: float = 1e-3) -> None:
+    err = elementwise_rel_err(a, b, floor)
+    assert err <= rtol, f"{what}: max |a-b| / max(|b|, {floor:g} max|b|) = {err:.3e} > {rtol:.1e}"
+
+
+def assert_same_bits(a, b, what: str = "") -> None:
+    """Equal values (torch.equal: -0 == +0), with the first mismatches named."""
+
+    a_t = torch.as_tensor(to_np(a))
+    b_t = torch.as_tensor(to_np(b))
+    assert a_t.shape == b_t.shape, f"{what}: shape {tuple(a_t.shape)} vs {tuple(b_t.shape)}"
+    if torch.equal(a_t, b_t):
+        return
+    bad = (a_t != b_t).nonzero()
+    idx = tuple(bad[0].tolist())
+    raise AssertionError(f"{what}: {bad.shape[0]} of {a_t.numel()} elements differ; first at {idx}: "
+                         f"{a_t[idx].item()!r} vs {b_t[idx].item()!r} (max rel {norm_rel_err(a_t, b_t):.2e})")

@@ -51,6 +51,24 @@ def test_validation_errors_are_reported_without_launching():
     assert lib.myelin_pack(None, 0, None, 0, 5, None) == 0
 
 
+def test_autograd_order_codes_are_validated_without_launching():
+    st = _lib.RULE_STRAIGHT_THROUGH + 1
+    # spike values cannot be packed into bits
+    with pytest.raises(ValueError, match="packed output takes the threshold rules"):
+        _lib.call("myelin_lif_fwd_f32", 1, 1, 1, None, 1, None, 4, 1, 1, 0.9, 1.0, 0.0, 10.0, st, 16, None)
+    # the autograd rules exist for surrogate ids 0-5 only
+    with pytest.raises(ValueError, match="unknown spike rule 22"):
+        _lib.call("myelin_lif_fwd_f32", 1, 1, 1, 1, None, None, 4, 1, 1, 0.9, 1.0, 0.0, 10.0,
+                  _lib.RULE_STRAIGHT_THROUGH + _lib.SG_NONE, 16, None)
+    with pytest.raises(ValueError, match="unknown surrogate code 22"):
+        _lib.call("myelin_lif_bwd_f32", 1, 1, None, None, 1, 1, 4, 4, 0.9, 1.0, 0.0, 10.0,
+                  _lib.SG_AUTOGRAD + _lib.SG_NONE, 16, None)
+    # the smooth-forward backward is built at chunk 16 only
+    with pytest.raises(ValueError, match="needs chunk 16"):
+        _lib.call("myelin_alif_bwd_f32", 1, 1, 1, None, None, None, 1, 1, 1, 4, 4, 0.9, 0.9, 1.0, 1.8, 0.0,
+                  10.0, _lib.SG_AUTOGRAD_SMOOTH + 1, 8, None)
+
+
 def test_error_message_is_per_thread():
     import threading
 

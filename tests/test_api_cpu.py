@@ -33,6 +33,28 @@ def test_shape_and_backend_errors_match_reference_wording():
                                      myelin.LIFParams(), surrogate="relu")
 
 
+def test_smooth_forward_on_triton_backends_raises_reference_message():
+    """hard_forward=False is the torch route in the reference; its Triton
+    backends refuse it with these messages (kernels.py:273-276,290-293)."""
+
+    x, st = torch.zeros(2, 3, 4), myelin.LIFState(torch.zeros(3, 4))
+    with pytest.raises(ValueError, match="^Triton surrogate LIF currently supports only hard_forward=True$"):
+        myelin.surrogate_lif_forward(x, st, myelin.LIFParams(), hard_forward=False, backend="triton")
+    with pytest.raises(ValueError, match="^generated Triton surrogate LIF currently supports only hard_forward"):
+        myelin.surrogate_lif_forward(x, st, myelin.LIFParams(), hard_forward=False, backend="triton_generated")
+
+
+def test_backend_selects_the_arithmetic():
+    """torch / hard_forward=False / ALIF auto: autograd's arithmetic; the
+    fused-kernel arithmetic otherwise (codes per include/myelin_hip.h)."""
+
+    from myelin_amd import _lib
+
+    assert kernels._surrogate_codes(1, True, True) == (_lib.RULE_STRAIGHT_THROUGH + 1, _lib.SG_AUTOGRAD + 1)
+    assert kernels._surrogate_codes(2, False, True) == (_lib.RULE_SMOOTH + 2, _lib.SG_AUTOGRAD_SMOOTH + 2)
+    assert kernels._surrogate_codes(4, True, False) == (_lib.RULE_SURROGATE, 4)
+
+
 def test_params_match_reference_properties():
     p = myelin.LIFParams(tau_mem=10.0)
     assert p.decay == 1.0 - 1.0 / 10.0

@@ -56,8 +56,9 @@ def test_kernels_through_reference_paths():
     xr = x.clone().requires_grad_()
     _, _, sr = R.surrogate_alif_unroll(xr, z, z, 20.0, 50.0, 1.0, 0.0, 1.8, "fast_sigmoid", 10.0)
     sr.backward(gs)
-    assert raster_agreement(s, sr) >= 0.9999
-    assert_norm_close(xg.grad.cpu(), xr.grad, 1e-4, "surrogate alif grad_x")
+    # the default ALIF arithmetic is autograd's: same spikes and gradient
+    assert torch.equal(s.detach().cpu(), sr.detach())
+    assert torch.equal(xg.grad.cpu(), xr.grad)
 
     xs = (torch.rand(T, B, F, generator=g) < 0.3).float()
     w = (torch.rand(F, N, generator=g) - 0.5) * 0.6

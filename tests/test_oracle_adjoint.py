@@ -15,13 +15,20 @@ from tests.helpers import assert_norm_close, seeded
 
 ALIF = dict(tau_mem=20.0, tau_adaptation=50.0, threshold=1.0, reset=0.0, beta=1.8)
 
-# max|a-b|/max|b| allowed between an fp32 adjoint and torch.autograd through
-# the reference unroll.  The parity bar (1e-5) is held against the exact
-# adjoint of the fp32 forward (oracle orc_adjoint_exact).  torch.autograd
-# differentiates each surrogate primitive op by op (fast_sigmoid's and
-# superspike's quotient rule cancels for large |c|) and is itself measured up
-# to 2.8e-5 (fast_sigmoid), 6.2e-5 (superspike), 1.9e-5 (sigmoid), 5.6e-5 (atan) from
+# max|a-b|/max|b| allowed between the closed-form adjoint (the arithmetic of
+# the fused GPU kernels: 0/1 spikes, sigma'(c) in closed form, as the
+# reference's Triton kernels compute it) and torch.autograd through the
+# reference unroll.  The two are different fp32 evaluations of one
+# gradient: the closed form is held to 1e-5 of the exact adjoint of the fp32
+# forward (oracle orc_adjoint_exact); torch.autograd differentiates each
+# surrogate primitive op by op (fast_sigmoid's and superspike's quotient
+# rule cancels for large |c|), carries spike values (H + sigma) - sigma of
+# 0.99999994 into the reset, and is itself measured up to 2.8e-5
+# (fast_sigmoid), 6.2e-5 (superspike), 1.9e-5 (sigmoid), 5.6e-5 (atan) from
 # that exact adjoint at T=256; these bounds are that distance with headroom.
+# The autograd arithmetic itself is reproduced value for value by
+# surrogate_adjoint_autograd_order (below) and by the kernels' autograd-order
+# mode.
 TOL_VS_AUTOGRAD = {
     "fast_sigmoid": 1e-4,
     "atan": 1e-4,
@@ -317,3 +324,89 @@ def test_matmul_rounding_knob():
     assert not torch.equal(out["exact"][2], out["native"][2])
     with pytest.raises(ValueError):
         R.set_matmul_rounding("tf32")
+
+
+# ---------------------------------------------------------------- autograd order
+@pytest.mark.parametrize("surrogate", R.SURROGATE_NAMES)
+@pytest.mark.parametrize("alif", [True, False])
+@pytest.mark.parametrize("hard", [True, False])
+def test_autograd_order_adjoint_equals_autograd(surrogate, alif, hard):
+    """The restated operation order reproduces torch.autograd through the
+    unroll value for value, with a nonzero reset and final-state gradients."""
+
+    x, m0, a0, gs, gm, ga = _case(13, 64, 3, 41)
+    tau, tau_a, thr, reset, beta, slope = 20.0, 50.0, 1.0, -0.3, 1.8, 10.0
+    xr, mr, ar = (t.clone().requires_grad_() for t in (x, m0, a0))
+    if alif:
+        m, a, s = R.surrogate_alif_unroll(xr, mr, ar, tau, tau_a, thr, reset, beta, surrogate, slope,
+                                          hard_forward=hard)
+        torch.autograd.backward([s, m, a], [gs, gm, ga])
+    else:
+        m, s = R.surrogate_lif_unroll(xr, mr, tau, thr, reset, surrogate, slope, hard_forward=hard)
+        torch.autograd.backward([s, m], [gs, gm])
+    gx, gm0, ga0 = R.surrogate_adjoint_autograd_order(x, m0, a0, gs, gm, ga, tau, tau_a, thr, reset, beta,
+                                                      surrogate, slope, hard_forward=hard, alif=alif)
+    assert torch.equal(gx, xr.grad)
+    assert torch.equal(gm0, mr.grad)
+    if alif:
+        assert torch.equal(ga0, ar.grad)
+
+
+@pytest.mark.parametrize("gs_on,final", [(False, True), (True, False)])
+def test_autograd_order_adjoint_partial_gradients(gs_on, final):
+    x, m0, a0, gs, gm, ga = _case(14, 40, 2, 33)
+    xr, mr, ar = (t.clone().requires_grad_() for t in (x, m0, a0))
+    m, a, s = R.surrogate_alif_unroll(xr, mr, ar, 20.0, 50.0, 1.0, 0.2, 1.8, "fast_sigmoid", 10.0)
+    outs = ([s] if gs_on else []) + ([m, a] if final else [])
+    torch.autograd.backward(outs, ([gs] if gs_on else []) + ([gm, ga] if final else []))
+    gx, gm0, ga0 = R.surrogate_adjoint_autograd_order(x, m0, a0, gs if gs_on else None, gm if final else None,
+                                                      ga if final else None, 20.0, 50.0, 1.0, 0.2, 1.8,
+                                                      "fast_sigmoid", 10.0)
+    assert torch.equal(gx, xr.grad) and torch.equal(gm0, mr.grad) and torch.equal(ga0, ar.grad)
+
+
+def test_autograd_order_is_a_distinct_rounding():
+    """The order pins bits: the closed form of the same gradient, and the
+    restatement with the spike gradient summed in another order, differ
+    from autograd (while staying within fp32 noise of it)."""
+
+    x, m0, a0, gs, gm, ga = _case(15, 128, 2, 128)
+    xr = x.clone().requires_grad_()
+    m, a, s = R.surrogate_alif_unroll(xr, m0, a0, 20.0, 50.0, 1.0, 0.0, 1.8, "fast_sigmoid", 10.0)
+    torch.autograd.backward([s, m, a], [gs, gm, ga])
+    closed, _, _ = c_ref.alif_bwd(x.numpy(), m0.numpy(), a0.numpy(), gs.numpy(), gm.numpy(), ga.numpy(),
+                                  np.float32(R.decay_from_tau(20.0)), np.float32(R.decay_from_tau(50.0)),
+                                  1.0, 1.8, 0.0, 10.0, "fast_sigmoid")
+    assert not np.array_equal(closed, xr.grad.numpy())
+    assert_norm_close(closed, xr.grad, 1e-4, "closed form vs autograd")
+    # another summation order of dL/ds, planted in a copy of the oracle's
+    # inner loop, on the CPU
+    reordered = _reordered_adjoint(x, m0, a0, gs, gm, ga)
+    assert not torch.equal(reordered, xr.grad)
+    assert_norm_close(reordered, xr.grad, 1e-4, "reordered vs autograd")
+
+
+def _reordered_adjoint(x, m0, a0, gs, gm, ga):
+    """surrogate_adjoint_autograd_order with dL/ds summed as
+    ((gs - G*m') + A) + G*reset (fast_sigmoid, reset 0)."""
+
+    d, rho = R.decay_from_tau(20.0), R.decay_from_tau(50.0)
+    m, a, trace = m0, a0, []
+    for xt in x.unbind(0):
+        mp = m * d + xt
+        c = 10.0 * (mp - (1.0 + 1.8 * a))
+        sm = R.surrogate_primitive("fast_sigmoid", c)
+        s = ((c >= 0).to(c.dtype) + sm) - sm
+        trace.append((mp, c, s))
+        m = mp * (1.0 - s) + 0.0 * s
+        a = a * rho + s
+    G, A, out = gm, ga, torch.empty_like(x)
+    for t in range(x.shape[0] - 1, -1, -1):
+        mp, c, s = trace[t]
+        g_s = ((gs[t] - G * mp) + A) + G * 0.0
+        gd = R._primitive_grad_autograd("fast_sigmoid", c, g_s) * 10.0
+        gp = G * (1.0 - s) + gd
+        out[t] = gp
+        A = A * rho + (-gd) * 1.8
+        G = gp * d
+    return out
