@@ -6,9 +6,11 @@ Bars:
   bf16 within 1e-5 of the float64 product of the bf16-rounded inputs.
 * fp32 linear paths vs the reference (golden vectors recorded from myelin's
   torch backend) and the oracle: spike rasters >= 99.99 % equal, membranes
-  within 1e-5, gradients within 1e-4 max-norm relative (the GEMM sums in a
-  different order than the CPU matmul; the reference's own Triton-vs-torch
-  tests use atol 1e-4 / rtol 1e-3, tests/test_triton_lif.py:1378-1379).
+  and gradients within 1e-5 max-norm relative (measured <= 4e-7); against
+  the golden vectors also within 1e-4 per element, |a - b| <= 1e-4 *
+  max(|b|, 1e-3 max|b|) (measured <= 1.9e-5: the GEMM sums in another order
+  than the CPU matmul, and the reference's spikes (H + sigma) - sigma can
+  sit an ulp below 1 in its reset and backward).
 * bf16 synapse: against the fp32 oracle run on bf16-rounded weights, rasters
   >= 99.99 %, losses and gradients within 2e-2 relative.
 """
@@ -25,7 +27,7 @@ import myelin_amd as myelin
 from myelin_amd import _lib
 from myelin_amd.linear import _gemm, linear
 from oracle import torch_ref as R
-from tests.helpers import assert_norm_close, raster_agreement, seeded, to_np
+from tests.helpers import assert_elementwise_close, assert_norm_close, raster_agreement, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -116,6 +118,14 @@ def test_linear_synapse_function_grads():
     assert_norm_close(bd.grad.cpu(), br.grad, 1e-5, "gb")
 
 
+def _golden_grads_close(xd, wd, bd, tag):
+    for name, t in (("gx", xd), ("gw", wd), ("gb", bd)):
+        if t is None:
+            continue
+        assert_norm_close(to_np(t.grad), LIN[f"{tag}_{name}"], 1e-5, name)
+        assert_elementwise_close(t.grad, LIN[f"{tag}_{name}"], 1e-4, name)
+
+
 def _golden_inputs():
     return (torch.from_numpy(LIN[k]) for k in ("x", "w", "b", "gs", "gfin", "grate"))
 
@@ -139,10 +149,7 @@ def test_linear_spike_paths_match_reference(bias, ck, with_final):
     assert raster_agreement(s, LIN[f"{tag}_s"]) >= 0.9999
     assert bool(((s == 0) | (s == 1)).all())
     assert_norm_close(to_np(st.membrane), LIN[f"{tag}_mT"], 1e-5, "membrane")
-    assert_norm_close(to_np(xd.grad), LIN[f"{tag}_gx"], 1e-4, "grad_x")
-    assert_norm_close(to_np(wd.grad), LIN[f"{tag}_gw"], 1e-4, "grad_w")
-    if bias:
-        assert_norm_close(to_np(bd.grad), LIN[f"{tag}_gb"], 1e-4, "grad_b")
+    _golden_grads_close(xd, wd, bd, tag)
 
 
 @pytest.mark.parametrize("bias", [False, True])
@@ -166,10 +173,7 @@ def test_linear_rate_paths_match_reference(bias, ck, red):
         # torch's mean over [B, N] sums in a device-dependent order
         assert_norm_close(to_np(r), LIN[f"{tag}_r"], 1e-6, "mean rate")
     assert_norm_close(to_np(st.membrane), LIN[f"{tag}_mT"], 1e-5, "membrane")
-    assert_norm_close(to_np(xd.grad), LIN[f"{tag}_gx"], 1e-4, "grad_x")
-    assert_norm_close(to_np(wd.grad), LIN[f"{tag}_gw"], 1e-4, "grad_w")
-    if bias:
-        assert_norm_close(to_np(bd.grad), LIN[f"{tag}_gb"], 1e-4, "grad_b")
+    _golden_grads_close(xd, wd, bd, tag)
 
 
 @pytest.mark.parametrize("T,B,F,N", [(20, 9, 40, 70), (33, 16, 64, 128), (5, 1, 3, 1)])
@@ -198,9 +202,9 @@ def test_linear_checkpoint_sizes_agree_and_match_oracle(T, B, F, N):
     es.backward(gs)
     assert raster_agreement(res[0][0], es) >= 0.9999
     if raster_agreement(res[0][0], es) == 1.0:
-        assert_norm_close(res[0][1], xr.grad, 1e-4, "grad_x")
-        assert_norm_close(res[0][2], wr.grad, 1e-4, "grad_w")
-        assert_norm_close(res[0][3], br.grad, 1e-4, "grad_b")
+        assert_norm_close(res[0][1], xr.grad, 1e-5, "grad_x")
+        assert_norm_close(res[0][2], wr.grad, 1e-5, "grad_w")
+        assert_norm_close(res[0][3], br.grad, 1e-5, "grad_b")
 
 
 @pytest.mark.parametrize("N", [17, 31, 32, 33, 64, 100])

@@ -3,9 +3,11 @@ packed-hidden variants, kernels.py:779-846).
 
 Bars (as for the one-layer linear paths): readout rates equal to the
 reference's when the rasters agree (rates are counts / T), gradients within
-1e-4 max-norm relative of the reference's (the MFMA GEMM sums in another
-order than the CPU matmul; the reference's own packed-vs-dense test uses
-atol 1e-4 / rtol 1e-3, tests/test_triton_lif.py:2500-2504).  The packed
+1e-5 max-norm relative of the reference's and of the oracle's (measured <=
+1.4e-6) and, against the reference's golden vectors, within 2e-4 per
+element, |a - b| <= 2e-4 * max(|b|, 1e-3 max|b|) (measured <= 8.4e-5: the
+MFMA GEMMs sum in another order than the CPU matmul, and the reference's
+spikes (H + sigma) - sigma can sit an ulp below 1).  The packed
 variant's readout GEMMs read the hidden spikes as packed bits; for readouts
 narrower than 128 neurons both variants run the same GEMM kernel and K
 split, so they must agree bit for bit (wider: within 1e-5).
@@ -21,7 +23,7 @@ import torch
 
 import myelin_amd as myelin
 from oracle import torch_ref as R
-from tests.helpers import assert_norm_close, raster_agreement, seeded, to_np
+from tests.helpers import assert_elementwise_close, assert_norm_close, raster_agreement, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -62,12 +64,10 @@ def test_two_layer_matches_reference(variant, bias, ck, sg):
     tag = f"{'b' if bias else 'nob'}_c{ck}_{sg}"
     assert np.array_equal(to_np(r), TWO[f"{tag}_r"])
     gx, gwh, gbh, gwo, gbo = _grads(leaves)
-    assert_norm_close(gx, TWO[f"{tag}_gx"], 1e-4, "grad_x")
-    assert_norm_close(gwh, TWO[f"{tag}_gwh"], 1e-4, "grad_hidden_weight")
-    assert_norm_close(gwo, TWO[f"{tag}_gwo"], 1e-4, "grad_output_weight")
-    if bias:
-        assert_norm_close(gbh, TWO[f"{tag}_gbh"], 1e-4, "grad_hidden_bias")
-        assert_norm_close(gbo, TWO[f"{tag}_gbo"], 1e-4, "grad_output_bias")
+    pairs = [(gx, "gx"), (gwh, "gwh"), (gwo, "gwo")] + ([(gbh, "gbh"), (gbo, "gbo")] if bias else [])
+    for got, name in pairs:
+        assert_norm_close(got, TWO[f"{tag}_{name}"], 1e-5, name)
+        assert_elementwise_close(got, TWO[f"{tag}_{name}"], 2e-4, name)
 
 
 def _random_net(seed, T, B, F, H, O):
@@ -114,7 +114,7 @@ def test_two_layer_matches_oracle_and_variants_agree(shape):
     got = out["recompute"]
     if np.array_equal(got[0], rr.detach().numpy()):
         for name, g, t in zip(("x", "wh", "bh", "wo", "bo"), got[1:], leaves):
-            assert_norm_close(g, t.grad, 1e-4, f"grad_{name}")
+            assert_norm_close(g, t.grad, 1e-5, f"grad_{name}")
     else:
         # a threshold tie flipped one readout spike: rates differ by 1/T there
         assert np.abs(got[0] - rr.detach().numpy()).max() <= 1.0 / T + 1e-7
