@@ -1451,8 +1451,10 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NL * (NS - 2)) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      // a bare barrier: the loads still in flight target other stages
-      asm volatile("s_barrier" ::: "memory");
+      // the loads still in flight target other stages; lgkmcnt(0) retires
+      // this wave's LDS reads of the previous stage, whose buffer the
+      // direct loads issued after this barrier overwrite
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
       for (int k0 = 0; k0 < 4; k0 += KH) {
         bf16x8 a[KH][WM], b[KH][WN];
@@ -2726,21 +2728,24 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   }
   const bool big = !bits && (half || use_big(g));
   if constexpr (PREC == 1) {
+    // the 256 x 256 mn-contiguous tiles pay only with a K split (their
+    // grid is under one round of the chip): plan it first, and take the
+    // 128 x 128 tiles below when K or the workspace allows no split
     if (!bits && use_dma_mn_wide(g, ta, tb, half)) {
       const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
       if (tiles > 0x7fffffff) return myelin::invalid("gemm: output too large");
-      int64_t splits = g.ws != nullptr ? plan_splits<1>(tiles, g.K, MYELIN_MN_WIDE_WANT) : 1;
+      int64_t splits = plan_splits<1>(tiles, g.K, MYELIN_MN_WIDE_WANT);
       while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
-      g.kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
-      splits = cdiv(g.K, g.kchunk);
-      g.splits = static_cast<int>(splits);
-      launch_dma_mn_wide(g, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), s);
-      if (int rc = myelin::launched("gemm (mn-contiguous, 256 x 256 tiles)")) return rc;
+      const int64_t kchunk = cdiv(cdiv(g.K, splits), KS) * KS;
+      splits = cdiv(g.K, kchunk);
       if (splits > 1) {
+        g.kchunk = kchunk;
+        g.splits = static_cast<int>(splits);
+        launch_dma_mn_wide(g, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), s);
+        if (int rc = myelin::launched("gemm (mn-contiguous, 256 x 256 tiles)")) return rc;
         launch_reduce(g, s);
         return myelin::launched("gemm split-k reduce");
       }
-      return MYELIN_OK;
     }
     if (!bits && use_wide(g, ta, tb, half)) {
       const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);

@@ -132,10 +132,14 @@ def _split_synapse(x, w, stream):
 
 def _split_eligible(prec: int, T: int, B: int, F: int, N: int) -> bool:
     """fp32 synapse on the chunked route with rows the bf16 loaders take and
-    enough work to amortise the input check."""
+    enough work to amortise the input check -- and no graph being captured
+    on the current stream: the split's choice needs the input check's flag
+    on the host (``_Split.exact``), a wait that capture does not allow and
+    whose answer a replay could not revisit, so captured layers keep the
+    fp32 engine."""
 
     return (prec == _lib.PREC["fp32"] and not _fused(B, N) and F % 8 == 0 and N % 8 == 0
-            and T * B * F * N >= _SPLIT_MIN_MACS)
+            and T * B * F * N >= _SPLIT_MIN_MACS and not torch.cuda.is_current_stream_capturing())
 
 
 class HipLinearFunction(torch.autograd.Function):

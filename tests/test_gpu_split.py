@@ -24,7 +24,7 @@ import myelin_amd as myelin
 from myelin_amd import _lib
 from myelin_amd import linear as L
 from oracle import torch_ref as R
-from tests.helpers import assert_norm_close, raster_agreement, seeded, to_np
+from tests.helpers import assert_elementwise_close, assert_norm_close, raster_agreement, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -324,20 +324,20 @@ def test_two_layer_hidden_split_matches_fp32_engine_and_oracle(monkeypatch, vari
                 assert_norm_close(a, t.grad, 1e-5, f"grad_{name} vs oracle")
 
 
-@pytest.mark.parametrize("parts,K,N", [(1, 1000, 1024), (3, 1000, 1024), (2, 1024, 1024), (3, 1024, 1024),
-                                         (3, 1024, 4096)])
-def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N):
+@pytest.mark.parametrize("parts,K,N,M", [(1, 1000, 1024, 8192), (3, 1000, 1024, 8192), (2, 1024, 1024, 8192),
+                                           (3, 1024, 1024, 8192), (3, 1024, 4096, 8192), (3, 1024, 4096, 7200)])
+def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N, M):
     """A 128-row slice of a bf16 product of `parts` parts (no K split)
-    equals the same rows of the 8192-row product bit for bit, as a
+    equals the same rows of the M-row product bit for bit, as a
     checkpointed recompute needs; and the product is within 1e-5 of float64.
     K = 1000 ends in a partial stage (register-staged tiles throughout);
-    with K = 1024 and two or three parts the 8192-row product runs on the
+    with K = 1024 and two or three parts the full product runs on the
     256 x 128 tiles staged by direct global -> LDS loads (N = 1024) or on
-    the 256 x 256 ones (N = 4096), while the slices run on the 128 x 128
-    register-staged tiles."""
+    the 256 x 256 ones (N = 4096; at M = 7200, a long-horizon layer's last
+    backward span, the last row of tiles is ragged), while the slices run on
+    the 128 x 128 register-staged tiles."""
 
-    _print_case(test="parts_rows", parts=parts, K=K, N=N)
-    M = 8192
+    _print_case(test="parts_rows", parts=parts, K=K, N=N, M=M)
     g = seeded(123 + parts)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
     Bs = torch.randn(parts, N, K, generator=g).to(torch.bfloat16)
@@ -359,6 +359,8 @@ def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N):
 @pytest.mark.parametrize("M,N,K,parts,accumulate", [
     (1024, 4096, 1440, 3, True),   # a config 4 span dW at one chunk
     (784, 2048, 2560, 1, False),   # config 3's dW shape: split, it runs on 256 x 256 tiles
+    (784, 2048, 2600, 3, False),   # the same on three parts, K ending in a partial stage
+    (1024, 2048, 1000, 3, True),   # three parts on 256 x 256 tiles, accumulating, partial stage
     (264, 1032, 1000, 3, True),    # ragged tiles, K ending in a partial stage
     (136, 200, 104, 2, False),     # K = 64 + a partial stage of 40
     (128, 128, 40, 3, False),      # a single partial stage per part
@@ -387,10 +389,14 @@ def test_mn_contiguous_products_equal_the_k_contiguous_ones(M, N, K, parts, accu
     assert torch.equal(mn, kc), "mn-contiguous and k-contiguous products differ"
     ref = sum(A.double().t() @ Bs[p].double() for p in range(parts)) + (C0.double() if accumulate else 0)
     assert_norm_close(to_np(mn), ref.numpy(), 1e-5, "mn-contiguous product vs float64")
-    # with a K split (the weight-gradient route): within 1e-5 of float64 too
+    # with a K split (the weight-gradient route; 256 x 256 tiles where the
+    # 128 x 128 grid is under one round): within 1e-5 of float64 too, and
+    # per element within summation-order noise of the unsplit product (a
+    # tile summing the wrong rows or k range is off by O(1))
     sp = C0.to(DEV)
     L._gemm_parts(Ad, Bd, parts, K * N, sp, M, N, K, M, N, N, True, False, accumulate, stream, split=True)
     assert_norm_close(to_np(sp), ref.numpy(), 1e-5, "split mn-contiguous product vs float64")
+    assert_elementwise_close(sp, mn, 1e-4, "split vs unsplit, per element", floor=1e-2)
 
 
 @pytest.mark.parametrize("variant", ["recompute", "packed"])
@@ -446,3 +452,55 @@ def test_parts_product_mn_layouts_at_a_weight_gradient_shape():
         assert_norm_close(to_np(got), ref.numpy(), 1e-5, f"split={split}")
         outs.append(C)
     assert_norm_close(to_np(outs[1]), to_np(outs[0]), 1e-6, "split vs unsplit")
+
+
+def test_split_synapse_is_not_used_under_graph_capture():
+    """A layer large enough for the split (2**32 MACs, spike inputs) keeps
+    the fp32 engine while a graph is captured -- the split's choice waits on
+    the host for the input check, which capture forbids.  The captured
+    forward equals the eager forward on the fp32 engine value for value, on
+    every replay (eager work in between)."""
+
+    _print_case(test="split_under_capture")
+    T, B, F, N = 128, 32, 1024, 1024
+    assert not L._fused(B, N) and T * B * F * N >= L._SPLIT_MIN_MACS
+    g = seeded(808)
+    x = (torch.rand(T, B, F, generator=g) < 0.05).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.45) * 0.1).to(DEV)
+    p = myelin.LIFParams()
+
+    def fwd():
+        with torch.no_grad():
+            return myelin.linear_surrogate_lif_forward(x, w, None, p, surrogate="superspike")
+
+    calls = []
+    real = L._split_synapse
+    L._split_synapse = lambda *a: calls.append(1) or real(*a)
+    try:
+        _, s_eager_split = fwd()  # eager: the split runs
+        assert calls, "the split path did not run eagerly"
+        calls.clear()
+        saved, L._SPLIT_MIN_MACS = L._SPLIT_MIN_MACS, 1 << 62
+        try:
+            st_ref, s_ref = fwd()  # eager on the fp32 engine
+        finally:
+            L._SPLIT_MIN_MACS = saved
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fwd()  # warm up on a side stream (eager: the split runs)
+        torch.cuda.current_stream().wait_stream(side)
+        calls.clear()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st_cap, s_cap = fwd()
+        assert not calls, "the split path ran under capture"
+    finally:
+        L._split_synapse = real
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(s_cap, s_ref) and torch.equal(st_cap.membrane, st_ref.membrane)
+        _ = (x * 2.0).sum().item()  # eager work between replays
+    assert raster_agreement(s_cap, s_eager_split) >= 0.9999
