@@ -153,7 +153,8 @@ __device__ __forceinline__ float sg_smooth(float c) {
     return 1.0f / (1.0f + exp_rn(-c));
   } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
     // 0.5 * (c / (1 + |c|) + 1)
-    const float q = c / (1.0f + fabsf(c));
+    const float b = 1.0f + fabsf(c);
+    const float q = myelin::div_by(c, b, myelin::recip_rn(b));
     return 0.5f * (q + 1.0f);
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     // atan(pi * c / 2) / pi + 0.5
@@ -164,7 +165,8 @@ __device__ __forceinline__ float sg_smooth(float c) {
     return fminf(fmaxf(1.0f - fabsf(c), 0.0f), 1.0f);
   } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
     // c / (1 + |c|) + 0.5
-    return c / (1.0f + fabsf(c)) + 0.5f;
+    const float b = 1.0f + fabsf(c);
+    return myelin::div_by(c, b, myelin::recip_rn(b)) + 0.5f;
   } else {
     // 0.6 * cdf(c; 0, 0.5) + 0.2 * cdf(c; 1, 1) + 0.2 * cdf(c; -1, 1),
     // sqrt(2) * sigma formed in double, as Python does, then rounded
@@ -198,10 +200,10 @@ __device__ __forceinline__ float sg_grad_autograd(float c, float g) {
     // of c (and is 0 where c is), so ((-gq) * (q/b)) * sign(c) is
     // (-gq) * |q/b| exactly: a sign flip commutes with rounding.
     const float b = 1.0f + fabsf(c);
+    const float y = myelin::recip_rn(b);
     const float gq = (SID == MYELIN_SG_FAST_SIGMOID) ? g * 0.5f : g;
-    const float g_num = gq / b;
-    const float q = c / b;
-    return g_num + (-gq) * fabsf(q / b);
+    const float q = myelin::div_by(c, b, y);
+    return myelin::div_by(gq, b, y) + (-gq) * fabsf(myelin::div_by(q, b, y));
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     // (/ pi) -> atan: g / (p^2 + 1) -> (/ 2) -> (* pi)
     const float p = (c * kPiF) / 2.0f;
@@ -242,25 +244,14 @@ __device__ __forceinline__ float autograd_spike(float c) {
 }
 
 // fast_sigmoid and superspike divide three numerators by b = 1 + |c| per
-// step (c in the primitive, q and the upstream gradient in its backward).
-// The backward shares one reciprocal y = 1/b (an IEEE division, so y is 1/b
-// rounded to nearest) and forms each quotient as
-//   q0 = x*y ; e = x - b*q0 (exact in an fma) ; q = q0 + e*y (one rounding).
-// With y within half an ulp of 1/b and q0 within one ulp of x/b, q is x/b
-// rounded to nearest (Markstein's theorem), i.e. the IEEE quotient, as long
-// as the residual e stays normal: |x| >= 2^-100 and x/b normal.  x = 0
-// gives a zero, of possibly the other sign.  (Checked against IEEE division
-// on the host for every fp32 significand of b with numerators in that
-// range.)
+// step (c in the primitive, q and the upstream gradient in its backward):
+// the backward shares one reciprocal myelin::recip_rn(b) between them
+// (myelin::div_by, the IEEE quotient for numerators of magnitude >= 2^-100;
+// a smaller one only ever meets a term it cannot change).
 constexpr bool sg_quotient_form(int sid) {
   return sid == MYELIN_SG_FAST_SIGMOID || sid == MYELIN_SG_SUPERSPIKE;
 }
 
-__device__ __forceinline__ float div_by(float x, float b, float y) {
-  const float q0 = x * y;
-  const float e = __builtin_fmaf(-b, q0, x);
-  return __builtin_fmaf(e, y, q0);
-}
 
 // sigma(c) from q = c / (1 + |c|)
 template <int SID>
@@ -518,17 +509,18 @@ __device__ __forceinline__ float sg_deriv(float c) {
     const float d = 1.0f + e;
     return e / (d * d);
   } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
+    // 0.5 / d^2 = 0.5 * (1 / d^2), both rounded once (a power of two)
     float d = 1.0f + fabsf(c);
-    return 0.5f / (d * d);
+    return 0.5f * myelin::recip_rn(d * d);
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     float s = 1.5707963267948966f * c;
-    return 0.5f / (1.0f + s * s);
+    return 0.5f * myelin::recip_rn(1.0f + s * s);
   } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
     float sg = (c > 0.0f) ? 1.0f : ((c < 0.0f) ? -1.0f : 0.0f);
     return fabsf(c) < 1.0f ? -sg : 0.0f;
   } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
     float d = 1.0f + fabsf(c);
-    return 1.0f / (d * d);
+    return myelin::recip_rn(d * d);
   } else if constexpr (SID == MYELIN_SG_NONE) {
     return 0.0f;
   } else {
@@ -583,9 +575,9 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
         if constexpr (sg_quotient_form(SID)) {
           // the reciprocal the reverse walk shares between its quotients
           const float b = 1.0f + fabsf(c);
-          const float y = 1.0f / b;
+          const float y = myelin::recip_rn(b);
           aux[j][v] = y;
-          s = spike_value<FR>(c, sg_from_quotient<SID>(div_by(c, b, y)));
+          s = spike_value<FR>(c, sg_from_quotient<SID>(myelin::div_by(c, b, y)));
         } else {
           s = autograd_spike<FR>(c);
         }
@@ -643,7 +635,7 @@ __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int6
         if constexpr (sg_quotient_form(SID)) {
           b = 1.0f + fabsf(c);
           y = aux[j][v];
-          q = div_by(c, b, y);
+          q = myelin::div_by(c, b, y);
           sv = spike_value<FR>(c, sg_from_quotient<SID>(q));
         } else {
           sv = autograd_spike<FR>(c);
@@ -664,7 +656,7 @@ __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int6
         if constexpr (sg_quotient_form(SID)) {
           // as sg_grad_autograd, with the shared reciprocal
           const float gq = (SID == MYELIN_SG_FAST_SIGMOID) ? gS * 0.5f : gS;
-          gc = div_by(gq, b, y) + (-gq) * fabsf(div_by(q, b, y));
+          gc = myelin::div_by(gq, b, y) + (-gq) * fabsf(myelin::div_by(q, b, y));
         } else {
           gc = sg_grad_autograd<SID>(c, gS);
         }

@@ -1851,17 +1851,18 @@ __device__ __forceinline__ float sg_deriv(float c) {
     const float d = 1.0f + e;
     return e / (d * d);
   } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
+    // 0.5 / d^2 = 0.5 * (1 / d^2), both rounded once (a power of two)
     float d = 1.0f + fabsf(c);
-    return 0.5f / (d * d);
+    return 0.5f * myelin::recip_rn(d * d);
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     float s = 1.5707963267948966f * c;
-    return 0.5f / (1.0f + s * s);
+    return 0.5f * myelin::recip_rn(1.0f + s * s);
   } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
     float sg = (c > 0.0f) ? 1.0f : ((c < 0.0f) ? -1.0f : 0.0f);
     return fabsf(c) < 1.0f ? -sg : 0.0f;
   } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
     float d = 1.0f + fabsf(c);
-    return 1.0f / (d * d);
+    return myelin::recip_rn(d * d);
   } else {
     float z = c / 0.5f, r = c - 1.0f, l = c + 1.0f;
     return 0.47873073648171924f * expf(-0.5f * z * z) + 0.07978845608028655f * expf(-0.5f * r * r) +

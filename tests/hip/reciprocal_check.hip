@@ -1,0 +1,34 @@
+// Test-only kernel: the reciprocal and quotient helpers of
+// myelin_amd/csrc/common.h against IEEE division on the GPU, for every fp32
+// significand of the divisor.  One lane per significand, one result word
+// per lane (bit flags), no atomics.  Built by tests/hip/build.py.
+#include "../../myelin_amd/csrc/common.h"
+
+namespace {
+
+__global__ void reciprocal_check(uint32_t *out, uint32_t n, float scale) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float b = __uint_as_float(0x3f800000u | i) * scale;
+  const float y = myelin::recip_rn(b);
+  uint32_t f = (y != 1.0f / b) ? 1u : 0u;
+  // quotients of hashed numerators (both signs, spread over exponents)
+  uint32_t h = i * 2654435761u + 12345u;
+  for (int j = 0; j < 16; ++j) {
+    h = h * 1664525u + 1013904223u;
+    const int ex = static_cast<int>(h % 120u) - 60;
+    float x = __uint_as_float(0x3f800000u | (h >> 9)) * ldexpf(1.0f, ex);
+    if (j & 1) x = -x;
+    if (j == 0) x = 1.0f;
+    if (j == 1) x = b;
+    f |= (myelin::div_by(x, b, y) != x / b) ? (2u << j) : 0u;
+  }
+  out[i] = f;
+}
+
+}  // namespace
+
+extern "C" int myelin_test_reciprocal_check(uint32_t *out, uint32_t n, float scale, hipStream_t stream) {
+  reciprocal_check<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(out, n, scale);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
