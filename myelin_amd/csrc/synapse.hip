@@ -1732,6 +1732,13 @@ struct LinArgs {
   int rule;
 };
 
+// the outputs a launch writes: bits 1 pre, 2 spikes, 4 packed, 8
+// checkpoints, 16 rates
+__host__ __device__ int lin_outputs(const LinArgs &p) {
+  return (p.pre != nullptr ? 1 : 0) | (p.spikes != nullptr ? 2 : 0) | (p.packed != nullptr ? 4 : 0) |
+         (p.ckpt != nullptr ? 8 : 0) | (p.rates != nullptr ? 16 : 0);
+}
+
 // BT batch rows x 64 neurons per workgroup, 64/BT timesteps per chunk
 // (GEMM rows r = j*BT + bb).  Wave w owns batch rows bb = w*Q .. w*Q+Q-1
 // (Q = BT/4) of the recurrence; lane = neuron.
@@ -2081,6 +2088,354 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
     if (p.m_final != nullptr) p.m_final[flat] = m[q];
     if (p.rates != nullptr) p.rates[flat] = cnt[q] / p.rate_denominator;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Fused current GEMM + LIF, software-pipelined: the recurrence of time chunk
+// c - 1 runs from the MFMA accumulators while the GEMM of chunk c runs.
+// Operands are bf16 in memory: x [T, B, F] and wt [N, F], rows 16-byte
+// aligned.
+//
+// Tile: 16 batch rows x 16 steps (256 GEMM rows) x 128 neurons, eight
+// waves of 64 x 64, stages ("windows") of 64 k staged through three LDS
+// buffers by direct global -> LDS loads (unpadded 128-byte rows, k-groups
+// swizzled by swz), two
+// windows ahead, continuously across chunks.  Element r of a lane's 32 x 32
+// accumulator block is row 8 (r >> 2) + 4 (lane >> 5) + (r & 3) (acc_row);
+// the A rows are gathered so that row R of a block is batch row
+// ((R >> 2) & 1) of the block's pair at step 4 (R >> 3) + (R & 3), which
+// makes element r step r of one (batch row, neuron) chain.  Each wave holds
+// two accumulator sets: the GEMM of chunk c accumulates into one while the
+// recurrence steps of chunk c - 1 are taken from the other, a few between
+// consecutive windows, so the VALU work and the trace stores overlap the
+// MFMAs and the operand loads of the next chunk.
+//
+// Vector memory operations retire in issue order (loads and stores share
+// vmcnt), so a window waits for its loads with vmcnt(6): all but the six
+// direct loads of the next window, issued last.  The recurrence steps of a
+// window (and their stores) run between its barrier and that issue, so a
+// window's stores need only retire by the next window's wait.  Lanes past B
+// or N compute the chain of batch row B - 1 or neuron N - 1 (their operand
+// rows, bias and start state are clamped to it) and store the same value to
+// the same address as the lane that owns it, so the stores need no masks.
+//
+// In a partial last stage (F % 64 != 0) the pieces past F load a zero page
+// and the 16-k steps entirely past F are skipped.  The k order -- stages of
+// 64, four 16-k MFMAs each -- is the other bf16 engines', so the currents
+// equal theirs bit for bit.  Workgroups go round-robin to the 8 XCDs; the
+// logical tiles are batch-tile-major and each XCD is handed a contiguous run
+// of them, so the workgroups sharing a batch tile's x rows share one L2.
+// Offsets are 32-bit: B * N * 4 < 2^32 (a step's trace) and 32 B F < 2^32
+// (16 steps of x).
+// ---------------------------------------------------------------------------
+namespace acc_fwd {
+constexpr int BM = 256, BN = 128, NT = 512, WGN = 2;
+constexpr int TILE = (BM + BN) * 128;  // bytes of one stage
+constexpr int NPA = BM * 8 / NT, NPB = BN * 8 / NT;
+constexpr int NL = NPA + NPB;  // direct loads per thread per stage
+
+// batch row (0..15) and step (0..15) of tile row r
+__device__ __forceinline__ int row_batch(int r) { return 2 * (r >> 5) + ((r >> 2) & 1); }
+// the 16-byte k-group position swizzle of tile row r: a function of r & 31
+// (so the row blocks of a wave share it), distinct over any 8 aligned rows
+// and, with the row's bank half, over any 16 (the fragment reads are
+// conflict-free whether the LDS serves 8 or 16 lanes a cycle)
+__device__ __forceinline__ int swz(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
+__device__ __forceinline__ int row_step(int r) { return 4 * ((r >> 3) & 3) + (r & 3); }
+
+// the source of the pieces of a partial last stage that lie past F
+__device__ __align__(16) const uint16_t kZeroPiece[8] = {};
+
+// one store at base + off (bytes; base uniform): the scalar-base form keeps
+// the per-step address arithmetic on the scalar unit
+__device__ __forceinline__ void store_at(const char *base, uint32_t off, float v) {
+  asm volatile("global_store_dword %0, %1, %2" ::"v"(off), "v"(v), "s"(base) : "memory");
+}
+// the same, nontemporal (streamed past the caches' reuse)
+__device__ __forceinline__ void store_nt_at(const char *base, uint32_t off, float v) {
+  asm volatile("global_store_dword %0, %1, %2 nt" ::"v"(off), "v"(v), "s"(base) : "memory");
+}
+}  // namespace acc_fwd
+
+// OUTS: the outputs written, as bits 1 pre, 2 spikes, 4 packed, 8
+// checkpoints, 16 rates (the hot sets are compiled without the branches), or
+// -1 for any set, read from p
+template <int RULE, int OUTS>
+__global__ __launch_bounds__(acc_fwd::NT) __attribute__((amdgpu_waves_per_eu(2))) void linear_lif_fwd_pipe(LinArgs p) {
+  using namespace acc_fwd;
+  __shared__ __attribute__((aligned(1024))) char lds[3 * TILE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w / WGN, wn = w % WGN;
+  const int64_t B = p.B, N = p.N, F = p.F, BNt = p.B * p.N;
+  const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN), nblk = gridDim.x;
+  uint32_t tile = blockIdx.x;
+  if (nblk % 8 == 0) tile = (tile % 8) * (nblk / 8) + tile / 8;
+  const int64_t n0 = __builtin_amdgcn_readfirstlane(tile % tiles_n) * static_cast<int64_t>(BN);
+  const int64_t b0 = __builtin_amdgcn_readfirstlane(tile / tiles_n) * static_cast<int64_t>(16);
+  const int64_t nchunks = (p.t_end - p.t_begin + 15) / 16;
+  const int64_t nst = (F + 63) / 64;  // windows per chunk, the last possibly partial
+  const int kq_last = F % 64 != 0 ? static_cast<int>((F % 64 + 15) / 16) : 4;
+
+  // Operand pieces (16 bytes: 8 bf16 of k) as 32-bit byte offsets from a
+  // uniform base: A piece e of thread tid is tile row (e * NT + tid) / 8 at
+  // k-group position (idx & 7) ^ swz(row) of the stage, from the chunk's
+  // first x row; B pieces likewise from row n0 of wt.  Rows past B read
+  // batch row B - 1 at the same step (the chains the lanes past B
+  // duplicate), rows past the end of time step t0 (accumulator rows the
+  // recurrence skips), rows past N row N - 1.
+  uint32_t oa[NPA], ob[NPB];
+  const uint16_t *xa = nullptr;  // the current chunk's first x row
+  auto point_a = [&](int64_t t0) {
+    xa = p.xh + t0 * B * F;
+#pragma unroll
+    for (int e = 0; e < NPA; ++e) {
+      const int idx = e * NT + tid, ra = idx >> 3;
+      const int step = t0 + row_step(ra) < p.t_end ? row_step(ra) : 0;
+      const int64_t b = b0 + row_batch(ra);
+      oa[e] = static_cast<uint32_t>(((step * B + (b < B ? b : B - 1)) * F + 8 * ((idx & 7) ^ swz(ra))) * 2);
+    }
+  };
+  const uint16_t *wb0 = p.wt + n0 * F;
+#pragma unroll
+  for (int e = 0; e < NPB; ++e) {
+    const int idx = e * NT + tid, r = idx >> 3;
+    const int64_t rr = n0 + r < N ? r : N - 1 - n0;
+    ob[e] = static_cast<uint32_t>((rr * F + 8 * ((idx & 7) ^ swz(r))) * 2);
+  }
+  auto issue = [&](char *tile, int64_t k0) {
+    const bool part = k0 + 64 > F;  // uniform: the partial last stage
+    const char *xk = reinterpret_cast<const char *>(xa + k0), *wk = reinterpret_cast<const char *>(wb0 + k0);
+#pragma unroll
+    for (int e = 0; e < NL; ++e) {
+      const int eo = e < NPA ? e : e - NPA, idx = eo * NT + tid;
+      // the wave's 64 pieces fill 1 KB of the stage in lane order
+      const uint32_t dst = static_cast<uint32_t>(
+          reinterpret_cast<uintptr_t>((lds_void *)(tile + (e < NPA ? 0 : BM * 128) + (eo * NT + w * 64) * 16)));
+      const char *base = e < NPA ? xk : wk;
+      const uint32_t o = e < NPA ? oa[e] : ob[e - NPA];
+      uint32_t m0_saved;
+      if (part) {
+        // pieces past F load the zero page
+        const char *src = base + o;
+        if (k0 + 8 * ((idx & 7) ^ swz(idx >> 3)) >= F) src = reinterpret_cast<const char *>(kZeroPiece);
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+            : "=&s"(m0_saved)
+            : "v"(src), "s"(dst)
+            : "memory");
+      } else {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+            : "=&s"(m0_saved)
+            : "v"(o), "s"(base), "s"(dst)
+            : "memory");
+      }
+    }
+  };
+  // fragment byte offsets in a stage (row blocks i, column blocks j sit
+  // 4096 bytes apart: their rows have the same swizzle)
+  int fa[4], fb[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int c = 2 * ks + (lane >> 5), r = lane & 31;
+    fa[ks] = (64 * wm + r) * 128 + ((c ^ swz(r)) << 4);
+    fb[ks] = (BM + 64 * wn + r) * 128 + ((c ^ swz(r)) << 4);
+  }
+  // kq: the stage's 16-k steps that hold data (4, or fewer in a partial last
+  // stage: the rest multiply zeros)
+  auto mfma_stage = [&](f32x16(&acc)[2][2], const char *cur, int kq) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks >= kq) break;  // uniform
+      bf16x8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(cur + fa[ks] + 4096 * i);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const bf16x8 *>(cur + fb[ks] + 4096 * j);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // chains: (row block i, column block j) -> batch row, neuron (clamped);
+  // off: the chain's byte offset in a [B, N] slice; pk_off: the byte offset
+  // of the packed word of column block 0 in a [B, W] slice
+  const int64_t wpk = (n0 + 64 * wn) / 32;  // packed word of column block 0
+  float m[2][2], cnt[2][2], bias[2];
+  uint32_t off[2][2], pk_off[2];
+  bool bok[2], nok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t n = n0 + 64 * wn + 32 * j + (lane & 31);
+    nok[j] = n < N;
+    bias[j] = p.bias != nullptr ? p.bias[nok[j] ? n : N - 1] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t b = b0 + 4 * wm + 2 * i + (lane >> 5);
+    bok[i] = b < B;
+    const int64_t bc = bok[i] ? b : B - 1;
+    pk_off[i] = static_cast<uint32_t>((bc * p.W + wpk) * 4);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + 64 * wn + 32 * j + (lane & 31);
+      const int64_t flat = bc * N + (nok[j] ? n : N - 1);
+      off[i][j] = static_cast<uint32_t>(flat * 4);
+      m[i][j] = p.m0 != nullptr ? p.m0[flat] : 0.0f;
+      cnt[i][j] = 0.0f;
+    }
+  }
+  // take the start state and bias before the loop: a first use inside it
+  // would make the compiler wait for every vector memory operation
+  // (vmcnt(0)) at each recurrence step, its scoreboard not seeing them retire
+  asm volatile("" ::"v"(m[0][0]), "v"(m[0][1]), "v"(m[1][0]), "v"(m[1][1]), "v"(bias[0]), "v"(bias[1]));
+  int next_ck = 0;  // the next checkpoint step, relative to t_begin
+
+  // the next load batch: chunk ic, stage is, LDS buffer ib
+  int ic = 0, is = 0, ib = 0, a_chunk = -1;
+  const int nst32 = static_cast<int>(nst), nch32 = static_cast<int>(nchunks);
+  auto issue_next = [&]() {
+    if (ic >= nch32) return;  // uniform
+    if (ic != a_chunk) {
+      point_a(p.t_begin + 16 * static_cast<int64_t>(ic));
+      a_chunk = ic;
+    }
+    issue(lds + ib * TILE, is * 64);
+    ib = ib == 2 ? 0 : ib + 1;
+    if (++is == nst32) {
+      is = 0;
+      ++ic;
+    }
+  };
+
+  // recurrence step r (of its chunk: accumulator element r) at step t_cur,
+  // from accumulator set acc; the trace pointers run with t_cur (advanced
+  // per step rather than recomputed, which would let the compiler hoist
+  // sixteen steps' addresses into scalar registers)
+  int64_t t_cur = p.t_begin;
+  const int outs = OUTS >= 0 ? OUTS : lin_outputs(p);
+  const char *pre_c = reinterpret_cast<const char *>(p.pre);
+  const char *spk_c = reinterpret_cast<const char *>(p.spikes + p.t_begin * BNt);
+  const char *pk_c = reinterpret_cast<const char *>(p.packed + p.t_begin * B * p.W);
+  const char *ck_c = reinterpret_cast<const char *>(p.ckpt);
+  auto rec_step = [&](const f32x16(&acc)[2][2], int r) {
+    const int64_t t = t_cur;
+    if (t >= p.t_end) return;  // uniform
+    if ((outs & 8) && t - p.t_begin == next_ck) {
+      // every lane: the lanes past B or N write their owner's value
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) store_at(ck_c, off[i][j], m[i][j]);
+      ck_c += BNt * 4;
+      next_ck += static_cast<int>(p.ckpt_every);
+    }
+    const char *pre_t = pre_c, *spk_t = spk_c;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // the empty asm pins the read (and the bias add) to this step: the
+        // accumulator set is loop-invariant over the windows, and a hoisted
+        // add would hold sixteen steps of currents in extra registers
+        float a = acc[i][j][r];
+        asm volatile("" : "+v"(a));
+        const float c_in = a + bias[j];
+        float mp = m[i][j] * p.decay;
+        mp = mp + c_in;
+        bool sp;
+        if constexpr (RULE == MYELIN_RULE_THRESHOLD) {
+          sp = mp >= p.thr;
+        } else {
+          const float c = p.slope * (mp - p.thr);
+          sp = c >= 0.0f;
+        }
+        if (outs & 1) store_at(pre_t, off[i][j], mp);
+        if (outs & 2) store_nt_at(spk_t, off[i][j], sp ? 1.0f : 0.0f);
+        m[i][j] = sp ? p.reset : mp;
+        if (outs & 16) cnt[i][j] = cnt[i][j] + (sp ? 1.0f : 0.0f);
+        if (outs & 4) {
+          // lanes 0-31: 32 neurons of the block's first batch row; 32-63: the next row
+          const uint64_t bits = __ballot(bok[i] && nok[j] && sp);
+          if ((lane & 31) == 0 && bok[i] && wpk + j < p.W)
+            store_at(pk_c + 4 * j, pk_off[i], __builtin_bit_cast(float, static_cast<uint32_t>(lane ? (bits >> 32) : bits)));
+        }
+      }
+    }
+    ++t_cur;
+    pre_c += BNt * 4;
+    spk_c += BNt * 4;
+    pk_c += B * p.W * 4;
+  };
+  auto rec_switch = [&](const f32x16(&acc)[2][2], int r) {
+    switch (r) {
+#define MYELIN_REC(k) \
+  case k:             \
+    rec_step(acc, k); \
+    break;
+      MYELIN_REC(0) MYELIN_REC(1) MYELIN_REC(2) MYELIN_REC(3) MYELIN_REC(4) MYELIN_REC(5) MYELIN_REC(6)
+      MYELIN_REC(7) MYELIN_REC(8) MYELIN_REC(9) MYELIN_REC(10) MYELIN_REC(11) MYELIN_REC(12) MYELIN_REC(13)
+      MYELIN_REC(14) MYELIN_REC(15)
+#undef MYELIN_REC
+      default: break;
+    }
+  };
+
+  // Chunk c: its GEMM into cur (none past the last chunk) with the
+  // recurrence of chunk c - 1 from prev (none for the first) spread over its
+  // windows: step r runs in window ceil((r + 1) nst / 16) - 1, before the
+  // window's load issue.  Waves 0-3 take their steps before their MFMAs,
+  // waves 4-7 (the other wave on each SIMD) after theirs, so that one
+  // wave's recurrence arithmetic runs while the other's MFMAs occupy the
+  // SIMD's matrix pipe.  cur is copied to prev at the end of the chunk.
+  const bool late = w >= 4;
+  f32x16 cur[2][2], prev[2][2];
+  int wb = 0;  // LDS buffer of the current window
+  issue_next();
+  issue_next();
+  for (int c = 0; c <= nch32; ++c) {
+    const int nw = c < nch32 ? nst32 : 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cur[i][j][r] = 0.0f;
+    int r = c > 0 ? 0 : 16;
+    for (int s = 0; s < nw; ++s) {
+      // this window's loads: every operation but the next window's batch
+      // when that is issued (the last vector memory operations issued),
+      // else all
+      if (ic * nst32 + is > c * nst32 + s + 1)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NL) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int kq = s + 1 < nst32 ? 4 : kq_last;
+      if (late) mfma_stage(cur, lds + wb * TILE, kq);
+      for (; r < 16 && ((r + 1) * nst32 + 15) / 16 <= s + 1; ++r) rec_switch(prev, r);
+      issue_next();
+      if (!late) mfma_stage(cur, lds + wb * TILE, kq);
+      wb = wb == 2 ? 0 : wb + 1;
+    }
+    for (; r < 16; ++r) rec_switch(prev, r);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) prev[i][j] = cur[i][j];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      // every lane: the lanes past B or N write their owner's value
+      if (p.m_final != nullptr) *reinterpret_cast<float *>(reinterpret_cast<char *>(p.m_final) + off[i][j]) = m[i][j];
+      if (p.rates != nullptr)
+        *reinterpret_cast<float *>(reinterpret_cast<char *>(p.rates) + off[i][j]) = cnt[i][j] / p.rate_denominator;
+    }
 }
 
 // Three bf16 values whose float sum is exactly v: h = bf16(v) (nearest
@@ -3016,10 +3371,33 @@ extern "C" int myelin_linear_lif_fwd_bf16(const uint16_t *x, const uint16_t *wt,
     return myelin::invalid("linear_lif_fwd_bf16: x and wt need 16-byte aligned rows (F %% 8 == 0)");
   a.xh = x;
   a.wt = wt;
+  hipStream_t s = myelin::as_hip(stream);
+  // 16 batch rows x 128 neurons per workgroup (one per CU, 144 KB of LDS),
+  // the recurrence run from the accumulators under the next chunk's GEMM,
+  // when that fills at least three quarters of the chip and its 32-bit
+  // offsets fit (a step's [B, N] trace, 16 steps of x); otherwise the 8- /
+  // 16-row tiles below
+  const int64_t acc_tiles = cdiv(N, acc_fwd::BN) * cdiv(B, 16);
+  if (acc_tiles >= 192 && acc_tiles <= 0x7fffffff && B * N < (int64_t{1} << 30) && B * F < (int64_t{1} << 27)) {
+    const dim3 grid(static_cast<unsigned>(acc_tiles)), block(acc_fwd::NT);
+    const int outs = lin_outputs(a);
+    const bool thr = a.rule == MYELIN_RULE_THRESHOLD;
+    // a training forward (trace + spikes), an inference forward (spikes),
+    // anything else
+    if (outs == 3)
+      thr ? linear_lif_fwd_pipe<MYELIN_RULE_THRESHOLD, 3><<<grid, block, 0, s>>>(a)
+          : linear_lif_fwd_pipe<MYELIN_RULE_SURROGATE, 3><<<grid, block, 0, s>>>(a);
+    else if (outs == 2)
+      thr ? linear_lif_fwd_pipe<MYELIN_RULE_THRESHOLD, 2><<<grid, block, 0, s>>>(a)
+          : linear_lif_fwd_pipe<MYELIN_RULE_SURROGATE, 2><<<grid, block, 0, s>>>(a);
+    else
+      thr ? linear_lif_fwd_pipe<MYELIN_RULE_THRESHOLD, -1><<<grid, block, 0, s>>>(a)
+          : linear_lif_fwd_pipe<MYELIN_RULE_SURROGATE, -1><<<grid, block, 0, s>>>(a);
+    return myelin::launched("linear_lif_fwd_bf16 (pipelined recurrence)");
+  }
   const int bt = (cdiv(N, kBig) * cdiv(B, 16) >= 512) ? 16 : 8;
   const dim3 grid(cdiv(N, kBig), cdiv(B, bt));
   if (grid.y > 65535) return myelin::invalid("linear_lif_fwd_bf16: B too large");
-  hipStream_t s = myelin::as_hip(stream);
   if (bt == 16)
     linear_lif_fwd_big<1, 16, true><<<grid, dim3(256), 0, s>>>(a);
   else

@@ -325,6 +325,103 @@ def test_fused_forward_equals_gemm_then_recurrence(T, B, F, N, prec):
     assert torch.equal(a["pk"], myelin.pack_spikes(a["s"]).data)
 
 
+# 16 batch rows x 128 neurons per workgroup, grid >= 192: the accumulator-
+# resident recurrence kernel.  F = 136: two 64-k stages and a partial one
+# of one 16-k step; 64: one stage; 40: the partial stage only; 120 and 88:
+# partial stages of four and two 16-k steps; ragged B and N; T not a
+# multiple of the 16-step chunk; a grid that is not a multiple of 8 (195
+# tiles: no XCD remapping); and the 784 -> 2048 layer at T = 50, B = 256.
+@pytest.mark.parametrize("T,B,F,N,t_begin,rule", [
+    (21, 250, 136, 1500, 0, 0), (17, 256, 64, 1536, 0, 1), (33, 400, 40, 1024, 0, 0),
+    (21, 250, 136, 1500, 6, 1), (19, 200, 120, 1920, 0, 1), (23, 256, 88, 1536, 3, 0),
+    (50, 256, 784, 2048, 0, 0)])
+def test_fused_bf16_accumulator_kernel_equals_gemm_then_recurrence(T, B, F, N, t_begin, rule):
+    """myelin_linear_lif_fwd_bf16 on its accumulator-recurrence kernel
+    against the bf16 GEMM (bias epilogue) then myelin_lif_currents_fwd: the
+    same k order and per-step arithmetic, so every output (membrane,
+    spikes, pre-reset trace, packed words, rates, checkpoints) is equal bit
+    for bit, from any start step."""
+
+    _print_case(test="fused_acc_vs_unfused", T=T, B=B, F=F, N=N, t_begin=t_begin, rule=rule)
+    assert -(-N // 128) * -(-B // 16) >= 192
+    g = seeded(T * 7 + B + F + N)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.45) * 0.4).to(DEV)
+    bias = (torch.rand(N, generator=g) * 0.1).to(DEV)
+    m0 = (torch.rand(B, N, generator=g) * 0.5).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    xb = x.to(torch.bfloat16)
+    wt = w.t().contiguous().to(torch.bfloat16)
+    W = (N + 31) // 32
+    ck_every = 5
+    Tr = T - t_begin
+    nck = -(-Tr // ck_every)
+
+    def outputs():
+        return dict(m=torch.empty(B, N, device=DEV), s=torch.zeros(T, B, N, device=DEV),
+                    pre=torch.empty(Tr, B, N, device=DEV), pk=torch.zeros(T, B, W, dtype=torch.int32, device=DEV),
+                    r=torch.empty(B, N, device=DEV), ck=torch.empty(nck, B, N, device=DEV))
+
+    a = outputs()
+    _lib.call("myelin_linear_lif_fwd_bf16", _lib.ptr(xb), _lib.ptr(wt), _lib.ptr(bias), _lib.ptr(m0),
+              _lib.ptr(a["m"]), _lib.ptr(a["s"]), _lib.ptr(a["pre"]), _lib.ptr(a["pk"]), _lib.ptr(a["r"]),
+              _lib.ptr(a["ck"]), T, B, F, N, t_begin, T, ck_every, 0.9, 0.6, -0.1, 5.0, rule, stream)
+    b = outputs()
+    cur = torch.empty(T, B, N, device=DEV)
+    _gemm(xb, wt, cur, T * B, N, F, F, F, N, False, True, False, _lib.PREC["bf16"], stream, bias=bias, split=False)
+    _lib.call("myelin_lif_currents_fwd", _lib.ptr(cur[t_begin:]), _lib.ptr(m0), _lib.ptr(b["m"]), _lib.ptr(b["s"]),
+              _lib.ptr(b["pre"]), _lib.ptr(b["pk"]), _lib.ptr(b["r"]), None, _lib.ptr(b["ck"]), T, B, N, t_begin, T,
+              t_begin, t_begin, ck_every, 0.9, 0.6, -0.1, 5.0, rule, stream)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    assert bool((a["s"][t_begin:] != 0).any()) and bool((a["s"][t_begin:] == 0).any())
+
+
+# The kernel is compiled apart for the training output set (trace + spikes)
+# and the inference one (spikes), without the per-output branches.
+@pytest.mark.parametrize("outs", ["train", "infer"])
+@pytest.mark.parametrize("T,B,F,N,t_begin,rule", [
+    (21, 250, 136, 1500, 0, 0), (19, 200, 120, 1920, 2, 1), (50, 256, 784, 2048, 0, 0)])
+def test_fused_bf16_accumulator_kernel_output_sets(T, B, F, N, t_begin, rule, outs):
+    """The specialised output sets of the accumulator-recurrence kernel
+    against the bf16 GEMM then myelin_lif_currents_fwd, bit for bit."""
+
+    _print_case(test="fused_acc_output_sets", T=T, B=B, F=F, N=N, t_begin=t_begin, rule=rule, outs=outs)
+    g = seeded(T * 5 + B + F + N)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).float().to(DEV)
+    w = ((torch.rand(F, N, generator=g) - 0.45) * 0.4).to(DEV)
+    bias = (torch.rand(N, generator=g) * 0.1).to(DEV)
+    m0 = (torch.rand(B, N, generator=g) * 0.5).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    xb = x.to(torch.bfloat16)
+    wt = w.t().contiguous().to(torch.bfloat16)
+    Tr = T - t_begin
+
+    def outputs():
+        o = dict(m=torch.empty(B, N, device=DEV), s=torch.zeros(T, B, N, device=DEV))
+        if outs == "train":
+            o["pre"] = torch.empty(Tr, B, N, device=DEV)
+        return o
+
+    def ptrs(o):
+        return (_lib.ptr(o["m"]), _lib.ptr(o["s"]), _lib.ptr(o.get("pre")), None, None, None)
+
+    a = outputs()
+    _lib.call("myelin_linear_lif_fwd_bf16", _lib.ptr(xb), _lib.ptr(wt), _lib.ptr(bias), _lib.ptr(m0), *ptrs(a),
+              T, B, F, N, t_begin, T, 1, 0.9, 0.6, -0.1, 5.0, rule, stream)
+    b = outputs()
+    cur = torch.empty(T, B, N, device=DEV)
+    _gemm(xb, wt, cur, T * B, N, F, F, F, N, False, True, False, _lib.PREC["bf16"], stream, bias=bias, split=False)
+    _lib.call("myelin_lif_currents_fwd", _lib.ptr(cur[t_begin:]), _lib.ptr(m0), _lib.ptr(b["m"]), _lib.ptr(b["s"]),
+              _lib.ptr(b.get("pre")), None, None, None, None, T, B, N, t_begin, T, t_begin, t_begin, 1, 0.9, 0.6,
+              -0.1, 5.0, rule, stream)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    assert bool((a["s"][t_begin:] != 0).any()) and bool((a["s"][t_begin:] == 0).any())
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (64, 64), (130, 257), (1000, 24)])
 def test_bf16_copies_round_like_torch(rows, cols):
     _print_case(test="bf16_copies", rows=rows, cols=cols)
