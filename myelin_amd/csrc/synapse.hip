@@ -800,41 +800,51 @@ __global__ __launch_bounds__(256) void gemm_smallk(GemmArgs g) {
     for (int j = 0; j < 4; ++j) bias[j] = g.bias[(c0 + j < g.N) ? c0 + j : g.N - 1];
   }
   const bool full = c0 + 3 < g.N;
+  // the row loop, compiled apart with and without reads of C: a read of C
+  // inside the loop would make every row wait for all of the wave's stores
+  auto rows = [&](auto acc_c) {
+    constexpr bool ACC = decltype(acc_c)::value;
 #pragma unroll
-  for (int i = 0; i < RW; ++i) {
-    const int64_t r = r0 + i;
-    if (r >= g.M) break;  // uniform
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < RW; ++i) {
+      const int64_t r = r0 + i;
+      if (r >= g.M) break;  // uniform
+      float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      const int q = i * KMAX + k;
-      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av[q / 64]), q % 64));
+      for (int k = 0; k < KMAX; ++k) {
+        const int q = i * KMAX + k;
+        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av[q / 64]), q % 64));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = __builtin_fmaf(a, b[k][j], o[j]);
-    }
-    float *dst = g.C + r * g.ldc + c0;
-    if (VC && full) {
-      f4 prev = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (g.accumulate) prev = *reinterpret_cast<const f4 *>(dst);
-      f4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float t = g.accumulate ? prev[j] + o[j] : o[j];
-        if (g.bias != nullptr) t = t + bias[j];
-        v[j] = t;
+        for (int j = 0; j < 4; ++j) o[j] = __builtin_fmaf(a, b[k][j], o[j]);
       }
-      *reinterpret_cast<f4 *>(dst) = v;
-    } else {
+      float *dst = g.C + r * g.ldc + c0;
+      if (VC && full) {
+        f4 prev = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (ACC) prev = *reinterpret_cast<const f4 *>(dst);
+        f4 v;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (c0 + j < g.N) {
-          float t = g.accumulate ? dst[j] + o[j] : o[j];
+        for (int j = 0; j < 4; ++j) {
+          float t = ACC ? prev[j] + o[j] : o[j];
           if (g.bias != nullptr) t = t + bias[j];
-          dst[j] = t;
+          v[j] = t;
+        }
+        *reinterpret_cast<f4 *>(dst) = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (c0 + j < g.N) {
+            float t = o[j];
+            if constexpr (ACC) t = dst[j] + t;
+            if (g.bias != nullptr) t = t + bias[j];
+            dst[j] = t;
+          }
         }
       }
     }
-  }
+  };
+  if (g.accumulate)
+    rows(std::true_type{});
+  else
+    rows(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -3382,9 +3392,12 @@ extern "C" int myelin_linear_lif_fwd_bf16(const uint16_t *x, const uint16_t *wt,
     const dim3 grid(static_cast<unsigned>(acc_tiles)), block(acc_fwd::NT);
     const int outs = lin_outputs(a);
     const bool thr = a.rule == MYELIN_RULE_THRESHOLD;
-    // a training forward (trace + spikes), an inference forward (spikes),
-    // anything else
-    if (outs == 3)
+    // a training forward (trace + spikes, with or without their packed
+    // twin), an inference forward (spikes), anything else
+    if (outs == 7)
+      thr ? linear_lif_fwd_pipe<MYELIN_RULE_THRESHOLD, 7><<<grid, block, 0, s>>>(a)
+          : linear_lif_fwd_pipe<MYELIN_RULE_SURROGATE, 7><<<grid, block, 0, s>>>(a);
+    else if (outs == 3)
       thr ? linear_lif_fwd_pipe<MYELIN_RULE_THRESHOLD, 3><<<grid, block, 0, s>>>(a)
           : linear_lif_fwd_pipe<MYELIN_RULE_SURROGATE, 3><<<grid, block, 0, s>>>(a);
     else if (outs == 2)

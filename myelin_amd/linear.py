@@ -223,7 +223,7 @@ def _span(T: int, checkpoint: int, BN: int) -> int:
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
              spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, exact=False,
-             pre_from=None, split=None, x32=None):
+             pre_from=None, split=None, x32=None, x_bits=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
@@ -246,10 +246,17 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     works while the host waits for the check; if the input is not
     bf16-exact that GEMM is redone on the fp32 engine into the same buffer
     and every later chunk takes the fp32 engine.
+    ``x_bits``: the input as packed spike words ``[T, B, ceil(F / 32)]``,
+    which the chunked route's GEMM reads in place of ``x`` (fp32 synapse
+    weights ``w``; the same sums bit for bit).
     """
 
-    T, B, F = x.shape
-    half = x.dtype == torch.bfloat16
+    if x_bits is not None:
+        T, B = x_bits.shape[:2]
+        F = w.shape[0]
+    else:
+        T, B, F = x.shape
+    half = x_bits is None and x.dtype == torch.bfloat16
     parts = half and wt.ndim == 3  # exact split: wt holds the planes [3, N, F]
     N = wt.shape[-2] if half else w.shape[1]
     if _fused(B, N):
@@ -289,7 +296,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
 
     def gemm(c0, c1, cur, s):
         rows = (c1 - c0) * B
-        if parts:
+        if x_bits is not None:
+            _gemm(x_bits[c0:c1], w, cur, rows, N, F, x_bits.shape[2], N, N, False, False, False, prec, s, bias=b,
+                  a_bits=True, split=not exact)
+        elif parts:
             _gemm_parts(x[c0:c1], wt, 3, N * F, cur, rows, N, F, F, F, N, False, True, False, s, bias=b,
                         split=not exact)
         elif half:
@@ -363,6 +373,37 @@ def _keep_trace(F: int, N: int) -> bool:
     return N <= 32 and 8 * N <= F
 
 
+def _attach_bits(out, words) -> None:
+    """Records the bit-packed copy of a spike tensor the layer wrote, with
+    the tensor's version: a consumer may read the bits instead (1 bit per
+    spike instead of 32) while the tensor is unmodified."""
+
+    out._myelin_bits = (words, out._version)
+
+
+def _spike_bits(x):
+    """The packed words of ``x [T, B, F]`` recorded by the layer that wrote
+    it, or None when there are none or ``x`` changed since (its version
+    moved on)."""
+
+    rec = getattr(x, "_myelin_bits", None)
+    if rec is None:
+        return None
+    words, version = rec
+    T, B, F = x.shape
+    if version != x._version or words.shape != (T, B, -(-F // 32)) or words.device != x.device:
+        return None
+    return words
+
+
+def _bits_consumer(B: int, F: int, N: int, prec: int) -> bool:
+    """A layer reads its input's packed twin: the chunked route with a
+    narrow output (the GEMMs stream the input once per pass; the bits cut
+    those reads 32-fold and sum the same products in the same order)."""
+
+    return N <= 32 and not _fused(B, N) and not _half(prec, F, N)
+
+
 class HipLinearLIFFunction(torch.autograd.Function):
     """Outputs ``(final_membrane, spikes)`` or, with ``rate=True``,
     ``(final_membrane, rates)`` where ``rates = spike_count / T``."""
@@ -376,12 +417,16 @@ class HipLinearLIFFunction(torch.autograd.Function):
         need = any(ctx.needs_input_grad[:3])
         half = _half(prec, F, N)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
+        bits = _spike_bits(x) if _bits_consumer(B, F, N, prec) else None
         split = None
-        if not half and _split_eligible(prec, T, B, F, N):
+        if not half and bits is None and _split_eligible(prec, T, B, F, N):
             split = _split_synapse(x, w, stream)
             xs, wt = split.xb, split.w3
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
+        # spikes: their packed twin too (N / 8 bytes per row more), for a
+        # narrow layer reading them next
+        words = torch.empty((T, B, -(-N // 32)), dtype=torch.int32, device=dev) if not rate else None
         if checkpoint is not None and _keep_trace(F, N):
             checkpoint = None
         pre = ckpt = None
@@ -399,12 +444,18 @@ class HipLinearLIFFunction(torch.autograd.Function):
                     tail = (math.ceil(T / span) - 1) * span
                     pre = torch.empty((T - tail, B, N), dtype=x.dtype, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
-                 spikes=None if rate else out, pre=pre, rates=out if rate else None, ckpt=ckpt,
-                 ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail, split=split, x32=x)
+                 spikes=None if rate else out, pre=pre, packed=words, rates=out if rate else None, ckpt=ckpt,
+                 ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail, split=split, x32=x,
+                 x_bits=bits)
         if split is not None and not split.exact():
             xs, wt = x, None
+        if words is not None:
+            _attach_bits(out, words)
+        if bits is not None:
+            xs = bits  # what the backward's weight GEMM reads
         ctx.set_materialize_grads(False)
-        ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None)
+        ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None,
+                    F if bits is not None else None)
         if need:
             # the bf16 synapse keeps the bf16 copies of x and W^T (what its GEMMs read)
             ctx.save_for_backward(xs, w, b, pre, ckpt, wt)
@@ -415,17 +466,17 @@ class HipLinearLIFFunction(torch.autograd.Function):
         none = (None,) * 12
         if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
             return none
-        decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b = ctx.meta
+        decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b, bits_f = ctx.meta
         xs, w, b, pre, ckpt, wt = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
         gx, gw, gb = linear_backward(xs, w, b if has_b else None, pre, ckpt, wt, g_m, g_out, decay, threshold,
                                      reset, sid, slope, checkpoint, rate, prec, rule, need_x, need_w,
-                                     need_b and has_b)
+                                     need_b and has_b, bits_f=bits_f)
         return gx, gw, gb, None, None, None, None, None, None, None, None, None
 
 
 def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset, sid, slope, checkpoint, rate,
-                    prec, rule, need_x=True, need_w=True, need_b=True):
+                    prec, rule, need_x=True, need_w=True, need_b=True, bits_f=None):
     """Gradients (dX, dW, db) of the streamed-synapse LIF, span by span in
     reverse time: recompute the span's pre-reset trace from its first
     checkpoint (``checkpoint=None``: the saved trace ``pre`` covers all T;
@@ -433,10 +484,14 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
     the forward), reverse the recurrence into G = dL/dI, then ``dX = G W^T`` and
     ``dW += X^T G`` on the MFMA GEMM and ``db`` as a fixed-order column
     sum.  ``xs`` is fp32, or
-    bf16 with ``wt = W^T`` bf16 for the bf16 synapse; ``g_out`` is dL/dspikes
-    ``[T, B, N]`` or, with ``rate``, dL/drates ``[B, N]``."""
+    bf16 with ``wt = W^T`` bf16 for the bf16 synapse, or (``bits_f`` = F)
+    the input spikes' packed words ``[T, B, ceil(F / 32)]``; ``g_out`` is
+    dL/dspikes ``[T, B, N]`` or, with ``rate``, dL/drates ``[B, N]``."""
 
     T, B, F = xs.shape
+    x_bits = xs if bits_f is not None else None
+    if x_bits is not None:
+        F = bits_f
     N = w.shape[1]
     BN = B * N
     dev = xs.device
@@ -491,7 +546,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                     if j + 2 < n_spans:
                         side.wait_event(free[i])
                     _lif_fwd(xs, w, b, ckpt[j * per], j * span, min(j * span + span, T), decay, threshold, reset,
-                             slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True)
+                             slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True, x_bits=x_bits)
                     ready[i].record(side)
 
             if tail is None:
@@ -513,7 +568,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 pre_k = bufs[k % 2]
             else:
                 _lif_fwd(xs, w, b, ckpt[k * per], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
-                         pre=scratch, wt=wt, exact=True)
+                         pre=scratch, wt=wt, exact=True, x_bits=x_bits)
                 pre_k = scratch
             _lib.call(
                 "myelin_linear_pre_bwd",
@@ -536,6 +591,9 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                     _lib.call("myelin_split_bf16x3", _lib.ptr(G), _lib.ptr(G3), rows, N, 0, stream)
                 _gemm_parts(xs[t0:t1], G3, 3, rows * N, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1,
                             stream)
+            elif gw is not None and x_bits is not None:
+                _gemm(x_bits[t0:t1], G, gw, F, N, rows, x_bits.shape[2], N, N, True, False, k != n_spans - 1, prec,
+                      stream, a_bits=True)
             elif gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
                 _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream)
