@@ -601,6 +601,21 @@ __device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, in
   constexpr int R = 8;
   const float *B = static_cast<const float *>(g.B);
   const int total = N * klen;
+  // e / d as a multiply-high by ceil(2^32 / d) (d >= 2; d = 1 is e
+  // itself): exact for e * d < 2^32 (e < 32 * KSUB here), where a hardware
+  // division would cost ~20 ops
+  const uint32_t d = TB ? static_cast<uint32_t>(klen) : static_cast<uint32_t>(N);
+  const uint32_t mag = d > 1 ? static_cast<uint32_t>((0x100000000ull + d - 1) / d) : 0u;
+  auto split = [&](int e, int &n, int &kk) {
+    const int q = d > 1 ? static_cast<int>(__umulhi(static_cast<uint32_t>(e), mag)) : e;
+    if constexpr (TB) {
+      n = q;
+      kk = e - q * klen;
+    } else {
+      kk = q;
+      n = e - q * N;
+    }
+  };
   for (int e0 = tid; e0 < total; e0 += 256 * R) {
     float v[R];
 #pragma unroll
@@ -608,28 +623,15 @@ __device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, in
       int e = e0 + 256 * r;
       e = e < total ? e : total - 1;  // clamped: every load in range
       int n, kk;
-      if constexpr (TB) {
-        n = e / klen;
-        kk = e - n * klen;
-        v[r] = B[n * g.ldb + ks + kk];
-      } else {
-        kk = e / N;
-        n = e - kk * N;
-        v[r] = B[(ks + kk) * g.ldb + n];
-      }
+      split(e, n, kk);
+      v[r] = TB ? B[n * g.ldb + ks + kk] : B[(ks + kk) * g.ldb + n];
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int e = e0 + 256 * r;
       if (e < total) {
         int n, kk;
-        if constexpr (TB) {
-          n = e / klen;
-          kk = e - n * klen;
-        } else {
-          kk = e / N;
-          n = e - kk * N;
-        }
+        split(e, n, kk);
         bs[n][kk] = cvt<PREC>(v[r]);
       }
     }
@@ -2651,19 +2653,22 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
 // out[n] (+)= sum_r in[r, n].  A block of 16 waves takes 64 columns; wave
 // q sums rows q, q+16, ... of its column, then wave 0 adds the 16 partials
 // in wave order (fixed order: deterministic).
-__global__ __launch_bounds__(1024) void col_sum(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
-                                                int64_t cols, int accumulate) {
-  __shared__ float part[16][64];
-  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+// 8 columns per workgroup (a 2048-column sum spreads over 256 CUs): thread
+// (column c = tid % 8, group q = tid / 8) sums rows q, q + 32, ... in order,
+// then the 32 group sums are added in group order
+__global__ __launch_bounds__(256) void col_sum(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
+                                               int64_t cols, int accumulate) {
+  __shared__ float part[32][8];
+  const int c = threadIdx.x & 7, q = threadIdx.x >> 3;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 8 + c;
   float s = 0.0f;
   if (n < cols)
-    for (int64_t r = q; r < rows; r += 16) s = s + in[r * cols + n];
-  part[q][lane] = s;
+    for (int64_t r = q; r < rows; r += 32) s = s + in[r * cols + n];
+  part[q][c] = s;
   __syncthreads();
   if (q == 0 && n < cols) {
     float t = 0.0f;
-    for (int i = 0; i < 16; ++i) t = t + part[i][lane];
+    for (int i = 0; i < 32; ++i) t = t + part[i][c];
     out[n] = accumulate ? out[n] + t : t;
   }
 }
@@ -3511,7 +3516,9 @@ extern "C" int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int
   if (rows < 0 || cols < 0) return myelin::invalid("col_sum: negative size");
   if (cols == 0) return MYELIN_OK;
   if (out == nullptr || (rows > 0 && in == nullptr)) return myelin::invalid("col_sum: null pointer");
-  col_sum<<<dim3(cdiv(cols, 64)), dim3(1024), 0, myelin::as_hip(stream)>>>(in, out, rows, cols, accumulate);
+  if (cdiv(cols, 8) > 0x7fffffff) return myelin::invalid("col_sum: too many columns");
+  col_sum<<<dim3(static_cast<unsigned>(cdiv(cols, 8))), dim3(256), 0, myelin::as_hip(stream)>>>(in, out, rows, cols,
+                                                                                                 accumulate);
   return myelin::launched("col_sum");
 }
 
@@ -3645,22 +3652,23 @@ __global__ __launch_bounds__(256) void split_bf16x3_t(const float *__restrict__ 
   }
 }
 
-// dst[c, r] = bf16(src[r, c]) through a 64 x 64 LDS tile
+// dst[c, r] = bf16(src[r, c]) through a 32 x 32 LDS tile (4 elements per
+// thread: a weight-sized matrix still spreads over the whole chip)
 __global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
                                                       int64_t rows, int64_t cols) {
-  __shared__ float tile[64][65];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  __shared__ float tile[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 32, c0 = static_cast<int64_t>(blockIdx.x) * 32;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
-    tile[ty + 4 * k][tx] = (r < rows && c < cols) ? src[r * cols + c] : 0.0f;
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = r0 + ty + 8 * k, c = c0 + tx;
+    tile[ty + 8 * k][tx] = (r < rows && c < cols) ? src[r * cols + c] : 0.0f;
   }
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
-    if (c < cols && r < rows) dst[c * rows + r] = to_bf16(tile[tx][ty + 4 * k]);
+  for (int k = 0; k < 4; ++k) {
+    const int64_t c = c0 + ty + 8 * k, r = r0 + tx;
+    if (c < cols && r < rows) dst[c * rows + r] = to_bf16(tile[tx][ty + 8 * k]);
   }
 }
 
@@ -3708,7 +3716,7 @@ extern "C" int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t ro
   if (rows < 0 || cols < 0) return myelin::invalid("transpose_bf16: negative size");
   if (rows == 0 || cols == 0) return MYELIN_OK;
   if (src == nullptr || dst == nullptr) return myelin::invalid("transpose_bf16: null pointer");
-  if (cdiv(rows, 64) > 65535) return myelin::invalid("transpose_bf16: too many rows");
-  transpose_bf16<<<dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, rows, cols);
+  if (cdiv(rows, 32) > 65535 || cdiv(cols, 32) > 0x7fffffff) return myelin::invalid("transpose_bf16: too large");
+  transpose_bf16<<<dim3(cdiv(cols, 32), cdiv(rows, 32)), dim3(256), 0, myelin::as_hip(stream)>>>(src, dst, rows, cols);
   return myelin::launched("transpose_bf16");
 }

@@ -288,7 +288,8 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     state = m_final
     if state is None and n > 1:
         state = torch.empty((B, N), dtype=torch.float32, device=dev)
-    counts = torch.zeros((B, N), dtype=torch.float32, device=dev) if rates is not None else None
+    # spike counts carried across chunks (one chunk counts in registers)
+    counts = torch.zeros((B, N), dtype=torch.float32, device=dev) if rates is not None and n > 1 else None
     if overlap:
         side.wait_stream(main)
         done = [torch.cuda.Event(), torch.cuda.Event()]  # GEMM wrote buffer i
