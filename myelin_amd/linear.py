@@ -501,13 +501,17 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
     with torch.cuda.device(dev):
         stream = _lib.stream(dev)
         wg = _cast_bf16(w, stream) if (half and need_x) else w
-        gm = g_m.float().contiguous().clone() if g_m is not None else torch.zeros((B, N), device=dev)
+        # the zero-started buffers (the membrane adjoint unless given, the bias
+        # gradient's accumulator) share one allocation: one fill launch
+        want_gb = need_b and b is not None
+        zeros = torch.zeros(((g_m is None) + want_gb, B, N), device=dev) if (g_m is None or want_gb) else None
+        gm = g_m.float().contiguous().clone() if g_m is not None else zeros[0]
         g_out = None if g_out is None else g_out.float().contiguous()
         g_spikes = None if rate else g_out
         g_rates = g_out if rate else None
         gx = torch.empty((T, B, F), device=dev) if need_x else None
         gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
-        gb_acc = torch.zeros((B, N), device=dev) if (need_b and b is not None) else None
+        gb_acc = zeros[-1] if want_gb else None
         # the reverse pass walks spans of whole checkpoint chunks, as many as
         # keep a span's trace within _CURRENT_CHUNK_ELEMS: one recompute
         # (from the span's first checkpoint, which the recurrence carries
