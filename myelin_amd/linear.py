@@ -276,11 +276,15 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     p0 = t0 if pre_from is None else pre_from  # pre holds the steps from p0 on
     bounds = sorted({*range(t0, t1, step), t1} | ({p0} if t0 < p0 < t1 else set()))
     n = len(bounds) - 1
-    # several chunks: each chunk's GEMM runs on the side stream one chunk
-    # ahead of the recurrence, into two alternating currents buffers
+    # several chunks on the fp32 engine: each chunk's GEMM runs on the side
+    # stream one chunk ahead of the recurrence, into two alternating
+    # currents buffers.  The bf16 engines (and the split) fill the chip with
+    # one workgroup per CU, and beside them the recurrence and the GEMM
+    # slow each other down (config 4's step: 7.92-8.01 ms overlapped, 7.53
+    # serial), so they run in turn on the one stream.
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
-    overlap = n > 1 and main.cuda_stream == stream and side.cuda_stream != stream
+    overlap = n > 1 and not half and main.cuda_stream == stream and side.cuda_stream != stream
     curs = [torch.empty((step, B, N), dtype=torch.float32, device=dev) for _ in range(2 if overlap else 1)]
     # the membrane carried across chunks lives in m_final (each lane reads
     # its m0 before writing, so m0 may be m_final); a single chunk needs no
@@ -532,11 +536,12 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             raise ValueError("the saved trace does not cover the last backward span")
         recomputes = checkpoint is not None and (tail is None or n_spans > 1)
         scratch = torch.empty((min(span, T), B, N), device=dev) if recomputes else None
-        # GEMM recomputes run one span ahead on a side stream, into two
-        # alternating trace buffers: span k-1's recompute overlaps span k's
-        # reverse pass and weight GEMMs.  ready[i]: buffer i holds its span's
-        # trace; free[i]: the reverse pass has read buffer i.
-        overlap = checkpoint is not None and n_spans > 1
+        # GEMM recomputes on the fp32 engine run one span ahead on a side
+        # stream, into two alternating trace buffers: span k-1's recompute
+        # overlaps span k's reverse pass and weight GEMMs (the bf16 engines
+        # and the split run in turn, as in the forward).  ready[i]: buffer i
+        # holds its span's trace; free[i]: the reverse pass has read buffer i.
+        overlap = checkpoint is not None and n_spans > 1 and not (half or parts)
         if overlap:
             main = torch.cuda.current_stream(dev)
             side = _side_stream(dev)
