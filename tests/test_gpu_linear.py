@@ -378,9 +378,10 @@ def test_fused_bf16_accumulator_kernel_equals_gemm_then_recurrence(T, B, F, N, t
     assert bool((a["s"][t_begin:] != 0).any()) and bool((a["s"][t_begin:] == 0).any())
 
 
-# The kernel is compiled apart for the training output set (trace + spikes)
-# and the inference one (spikes), without the per-output branches.
-@pytest.mark.parametrize("outs", ["train", "infer"])
+# The kernel is compiled apart for the training output sets (trace + spikes,
+# with or without their packed twin) and the inference one (spikes),
+# without the per-output branches.
+@pytest.mark.parametrize("outs", ["train", "train_packed", "infer"])
 @pytest.mark.parametrize("T,B,F,N,t_begin,rule", [
     (21, 250, 136, 1500, 0, 0), (19, 200, 120, 1920, 2, 1), (50, 256, 784, 2048, 0, 0)])
 def test_fused_bf16_accumulator_kernel_output_sets(T, B, F, N, t_begin, rule, outs):
@@ -398,14 +399,18 @@ def test_fused_bf16_accumulator_kernel_output_sets(T, B, F, N, t_begin, rule, ou
     wt = w.t().contiguous().to(torch.bfloat16)
     Tr = T - t_begin
 
+    W = (N + 31) // 32
+
     def outputs():
         o = dict(m=torch.empty(B, N, device=DEV), s=torch.zeros(T, B, N, device=DEV))
-        if outs == "train":
+        if outs != "infer":
             o["pre"] = torch.empty(Tr, B, N, device=DEV)
+        if outs == "train_packed":
+            o["pk"] = torch.zeros(T, B, W, dtype=torch.int32, device=DEV)
         return o
 
     def ptrs(o):
-        return (_lib.ptr(o["m"]), _lib.ptr(o["s"]), _lib.ptr(o.get("pre")), None, None, None)
+        return (_lib.ptr(o["m"]), _lib.ptr(o["s"]), _lib.ptr(o.get("pre")), _lib.ptr(o.get("pk")), None, None)
 
     a = outputs()
     _lib.call("myelin_linear_lif_fwd_bf16", _lib.ptr(xb), _lib.ptr(wt), _lib.ptr(bias), _lib.ptr(m0), *ptrs(a),
@@ -414,8 +419,8 @@ def test_fused_bf16_accumulator_kernel_output_sets(T, B, F, N, t_begin, rule, ou
     cur = torch.empty(T, B, N, device=DEV)
     _gemm(xb, wt, cur, T * B, N, F, F, F, N, False, True, False, _lib.PREC["bf16"], stream, bias=bias, split=False)
     _lib.call("myelin_lif_currents_fwd", _lib.ptr(cur[t_begin:]), _lib.ptr(m0), _lib.ptr(b["m"]), _lib.ptr(b["s"]),
-              _lib.ptr(b.get("pre")), None, None, None, None, T, B, N, t_begin, T, t_begin, t_begin, 1, 0.9, 0.6,
-              -0.1, 5.0, rule, stream)
+              _lib.ptr(b.get("pre")), _lib.ptr(b.get("pk")), None, None, None, T, B, N, t_begin, T, t_begin, t_begin, 1,
+              0.9, 0.6, -0.1, 5.0, rule, stream)
     torch.cuda.synchronize()
     for k in a:
         assert torch.equal(a[k], b[k]), k
