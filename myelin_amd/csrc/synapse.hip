@@ -2580,10 +2580,16 @@ __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int
 // (0), as bf16 rounded as the bf16 GEMMs would round it (1), or as three
 // bf16 planes whose sum is G exactly (2).  V neurons per lane (V = 2: BN
 // even and every operand 8-byte aligned, so each step is one 8-byte load
-// per operand and one store per plane).
+// per operand and one store per plane).  The loads run DEPTH steps ahead:
+// 4 on the wide (V = 2) grids, where a 16-step block costs 150 registers
+// and so occupancy (3 waves per SIMD instead of 8; 524288 neurons x 50
+// steps: 54 -> 42 us, x 256 steps: 310 -> 293 us, 131072 x 225 with the
+// three-plane G: 86 -> 78 us), and kPipe on the narrow ones, whose few
+// waves need every load of a long serial walk in flight.
 template <int SID, bool GS, int GM, int V>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   using VT = typename PreVec<V>::T;
+  constexpr int DEPTH = V == 2 ? 4 : kPipe;
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (i >= p.BN) return;
   const int64_t C = p.C, row = p.BN / V;
@@ -2597,11 +2603,11 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   const VT *pre = reinterpret_cast<const VT *>(p.pre + i);
   const VT *gs = GS ? reinterpret_cast<const VT *>(p.gs + i) : nullptr;
   const VT zero{};
-  const int64_t nblk = (C + kPipe - 1) / kPipe;
-  const int64_t f = C - (nblk - 1) * kPipe;
-  VT pv[kPipe], gv[kPipe];
+  const int64_t nblk = (C + DEPTH - 1) / DEPTH;
+  const int64_t f = C - (nblk - 1) * DEPTH;
+  VT pv[DEPTH], gv[DEPTH];
 #pragma unroll
-  for (int u = 0; u < kPipe; ++u) {
+  for (int u = 0; u < DEPTH; ++u) {
     const int64_t j = C - 1 - (u < f ? u : f - 1);
     pv[u] = pre[j * row];
     if constexpr (GS) gv[u] = gs[j * row];
@@ -2609,36 +2615,36 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   // block 0 (f steps), prefetching block 1 (or re-reading block 0 when alone)
   {
     const int64_t r0 = nblk > 1 ? f : 0;
-    VT np[kPipe], ng[kPipe];
+    VT np[DEPTH], ng[DEPTH];
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u) {
+    for (int u = 0; u < DEPTH; ++u) {
       const int64_t r = r0 + u < C ? r0 + u : C - 1;
       np[u] = pre[(C - 1 - r) * row];
       if constexpr (GS) ng[u] = gs[(C - 1 - r) * row];
     }
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u)
+    for (int u = 0; u < DEPTH; ++u)
       if (u < f) pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u) {
+    for (int u = 0; u < DEPTH; ++u) {
       pv[u] = np[u];
       if constexpr (GS) gv[u] = ng[u];
     }
   }
-  for (int64_t r0 = f; r0 < C; r0 += kPipe) {
-    const int64_t rn = r0 + kPipe < C ? r0 + kPipe : r0;
-    VT np[kPipe], ng[kPipe];
+  for (int64_t r0 = f; r0 < C; r0 += DEPTH) {
+    const int64_t rn = r0 + DEPTH < C ? r0 + DEPTH : r0;
+    VT np[DEPTH], ng[DEPTH];
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u) {
+    for (int u = 0; u < DEPTH; ++u) {
       np[u] = pre[(C - 1 - rn - u) * row];
       if constexpr (GS) ng[u] = gs[(C - 1 - rn - u) * row];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u)
+    for (int u = 0; u < DEPTH; ++u)
       pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u) {
+    for (int u = 0; u < DEPTH; ++u) {
       pv[u] = np[u];
       if constexpr (GS) gv[u] = ng[u];
     }
