@@ -546,15 +546,13 @@ struct BwdArgs {
 
 // Recompute one chunk forward from its checkpointed state: pre[j] = m'_t,
 // cv[j] = c_t = slope*(m'_t - th_t) (for SG_NONE: m'_t - th_t, so that
-// c >= 0 is the plain threshold test), aux[j] = 1/(1 + |c_t|) for the
-// autograd-order quotient forms.  GUARD: only the first `len` steps.
+// c >= 0 is the plain threshold test).  GUARD: only the first `len` steps.
 // FR: 0 for exact 0/1 spikes, else the forward's autograd rule
 // (straight-through / smooth), whose spike values the reset and the
 // adaptation carry.
 template <bool ALIF, int C, int SID, int V, bool GUARD, int FR, bool RZ>
 __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const float (&xb)[C][V], float (&m)[V],
-                                              float (&a)[V], float (&pre)[C][V], float (&cv)[C][V],
-                                              float (&aux)[C][V]) {
+                                              float (&a)[V], float (&pre)[C][V], float (&cv)[C][V]) {
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     if (GUARD && j >= len) break;
@@ -576,7 +574,6 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
           // the reciprocal the reverse walk shares between its quotients
           const float b = 1.0f + fabsf(c);
           const float y = myelin::recip_rn(b);
-          aux[j][v] = y;
           s = spike_value<FR>(c, sg_from_quotient<SID>(myelin::div_by(c, b, y)));
         } else {
           s = autograd_spike<FR>(c);
@@ -614,7 +611,7 @@ __device__ __forceinline__ void bwd_recompute(const BwdArgs &p, int len, const f
 template <bool ALIF, int C, int SID, int V, bool GS, bool GUARD, int FR, bool RZ, int J0 = 0, int J1 = C>
 __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int64_t t0, int len,
                                             const float (&gsb)[C][V], const float (&pre)[C][V],
-                                            const float (&cv)[C][V], const float (&aux)[C][V], float (&gm)[V],
+                                            const float (&cv)[C][V], float (&gm)[V],
                                             float (&ga)[V]) {
 #pragma unroll
   for (int j = J1 - 1; j >= J0; --j) {
@@ -622,7 +619,14 @@ __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int6
     float g[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      const float c = cv[j][v];
+      float c = cv[j][v];
+      // The quotient forms rebuild b, 1/b, q and the spike value from c
+      // here (about 12 VALU per neuron-step) instead of keeping them from
+      // the recompute: the empty asm hides c's origin, so the compiler
+      // cannot carry those values across the phases.  Three more values
+      // per step kept live took 250 VGPRs (2 waves per SIMD) against 149
+      // (3 waves); [256, 128, 4096] ALIF fast_sigmoid: 280 -> 273 us.
+      if constexpr (FR != 0 && sg_quotient_form(SID)) asm volatile("" : "+v"(c));
       const float s = c >= 0.0f ? 1.0f : 0.0f;
       if constexpr (SID == MYELIN_SG_NONE) {
         // where(s, reset, m') passes gradient to m' only where s == 0
@@ -634,7 +638,7 @@ __device__ __forceinline__ void bwd_reverse(const BwdArgs &p, int64_t base, int6
         float sv, b = 0.0f, y = 0.0f, q = 0.0f;
         if constexpr (sg_quotient_form(SID)) {
           b = 1.0f + fabsf(c);
-          y = aux[j][v];
+          y = myelin::recip_rn(b);
           q = myelin::div_by(c, b, y);
           sv = spike_value<FR>(c, sg_from_quotient<SID>(q));
         } else {
@@ -727,7 +731,7 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
     for (int v = 0; v < V; ++v) ga[v] = 0.0f;
   }
 
-  float xb[C][V], gsb[C][V], pre[C][V], cv[C][V], aux[C][V], m[V], a[V];
+  float xb[C][V], gsb[C][V], pre[C][V], cv[C][V], m[V], a[V];
   if (rem > 0) {
     const int64_t t0 = Kf * C;
     bwd_load_ckpt<ALIF, V>(p, Kf, base, m, a);
@@ -739,8 +743,8 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
       for (int j = 0; j < C; ++j)
         if (j < rem) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
     }
-    bwd_recompute<ALIF, C, SID, V, true, FR, RZ>(p, rem, xb, m, a, pre, cv, aux);
-    bwd_reverse<ALIF, C, SID, V, GS, true, FR, RZ>(p, base, t0, rem, gsb, pre, cv, aux, gm, ga);
+    bwd_recompute<ALIF, C, SID, V, true, FR, RZ>(p, rem, xb, m, a, pre, cv);
+    bwd_reverse<ALIF, C, SID, V, GS, true, FR, RZ>(p, base, t0, rem, gsb, pre, cv, gm, ga);
   }
   if (Kf > 0) {
     int64_t k = Kf - 1;
@@ -761,25 +765,25 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
           for (int j = C / 2; j < C; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
         }
         __builtin_amdgcn_sched_barrier(0);
-        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
+        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv);
         __builtin_amdgcn_sched_barrier(0);
         bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
 #pragma unroll
         for (int j = 0; j < C / 2; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 3 * C / 4, C>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 3 * C / 4, C>(p, base, t0, C, gsb, pre, cv, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (GS) {
 #pragma unroll
           for (int j = 0; j < C / 2; ++j) ld_stream<V>(gsb[j], p.gs + (t0 + j) * BN + base);
         }
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, C / 2, 3 * C / 4>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, C / 2, 3 * C / 4>(p, base, t0, C, gsb, pre, cv, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = C / 2; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 0, C / 2>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ, 0, C / 2>(p, base, t0, C, gsb, pre, cv, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
       } else {
         if constexpr (GS) {
@@ -790,13 +794,13 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
         // reverse(k), so the reverse phase waits only for grad_spikes(k) while
         // the loads of chunk k-1 stay in flight
         __builtin_amdgcn_sched_barrier(0);
-        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
+        bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv);
         __builtin_amdgcn_sched_barrier(0);
         bwd_load_ckpt<ALIF, V>(p, k - 1, base, m, a);
 #pragma unroll
         for (int j = 0; j < C; ++j) ld_stream<V>(xb[j], p.x + (t0 - C + j) * BN + base);
         __builtin_amdgcn_sched_barrier(0);
-        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, t0, C, gsb, pre, cv, aux, gm, ga);
+        bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, t0, C, gsb, pre, cv, gm, ga);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -804,8 +808,8 @@ __global__ __launch_bounds__(256) void bwd_chunked(BwdArgs p) {
 #pragma unroll
       for (int j = 0; j < C; ++j) ld_stream<V>(gsb[j], p.gs + j * BN + base);
     }
-    bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv, aux);
-    bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, 0, C, gsb, pre, cv, aux, gm, ga);
+    bwd_recompute<ALIF, C, SID, V, false, FR, RZ>(p, C, xb, m, a, pre, cv);
+    bwd_reverse<ALIF, C, SID, V, GS, false, FR, RZ>(p, base, 0, C, gsb, pre, cv, gm, ga);
   }
   st<V>(p.gm0 + base, gm);
   if constexpr (ALIF) st<V>(p.ga0 + base, ga);
