@@ -476,17 +476,37 @@ void launch_reduce(const GemmArgs &g, hipStream_t s) {
     splitk_reduce<<<dim3((n + 255) / 256), dim3(256), 0, s>>>(g);
 }
 
+// Three bf16 values whose float sum is exactly v: h = bf16(v) (nearest
+// even), m = bf16(v - h), l = v - h - m.  v - h is exact and has at most 16
+// significant bits, so after m at most 8 remain and l is exact as well (for
+// |v| >= 2^-110; below that l would be subnormal in bf16).  Non-finite v:
+// h carries it, m = l = 0.
+__device__ __forceinline__ void split3(float v, uint16_t &h, uint16_t &m, uint16_t &l) {
+  const __bf16 bh = static_cast<__bf16>(v);
+  if (!__builtin_isfinite(v)) {
+    h = __builtin_bit_cast(uint16_t, bh);
+    m = l = 0;
+    return;
+  }
+  const float r1 = v - static_cast<float>(bh);
+  const __bf16 bm = static_cast<__bf16>(r1);
+  const float r2 = r1 - static_cast<float>(bm);
+  h = __builtin_bit_cast(uint16_t, bh);
+  m = __builtin_bit_cast(uint16_t, bm);
+  l = __builtin_bit_cast(uint16_t, static_cast<__bf16>(r2));
+}
+
 // ---------------------------------------------------------------------------
 // Narrow GEMMs for the readout layers: outputs at most 32 columns wide
 // (gemm_narrow: currents I = S W_o and dW_o = S^T G_o) or K at most 32
 // (gemm_smallk: dS = G_o W_o^T, on the vector ALUs, below).  gemm_narrow
 // streams the long operand A from global memory straight into MFMA
 // fragments -- it is read once, so it skips LDS -- with the narrow operand
-// in LDS.  Per-lane k layout of a group of 2*KG consecutive k:
-//   lane l holds k = k0 + KG * (l / 32) + [0, KG)       KG = 8 (bf16) | 4 (fp32)
-// bf16: one v_mfma_f32_32x32x16_bf16 per group; fp32: four
-// v_mfma_f32_32x32x2f32, the i-th taking element i of each lane (lanes < 32
-// give k0 + i, lanes >= 32 give k0 + 4 + i), the same k for A and B.
+// in LDS.  Per-lane k layout of a group of 16 consecutive k:
+//   lane l holds k = k0 + 8 * (l / 32) + [0, 8)
+// and each group is one v_mfma_f32_32x32x16_bf16 (bf16 precision), or three
+// to nine of them on exact bf16 planes of the operands (fp32 precision,
+// gemm_narrow_x3 below).
 // A(m, k) may be fp32 (TA: A[k*lda + m], else A[m*lda + k]) or packed spike
 // bits (PA: bit m%32 of word A[k*lda + m/32] with TA, else bit k%32 of word
 // A[m*lda + k/32]).
@@ -494,19 +514,15 @@ void launch_reduce(const GemmArgs &g, hipStream_t s) {
 #ifndef MYELIN_NARROW_U
 #define MYELIN_NARROW_U 8  // A groups loaded per batch by the narrow kernel
 #endif
-#ifndef MYELIN_NARROW_WGS
-#define MYELIN_NARROW_WGS 512  // workgroups the narrow kernel's K splits aim for
+#ifndef MYELIN_NARROW_KCHUNK
+#define MYELIN_NARROW_KCHUNK 512  // k per K split of the narrow kernel (before rounding to 64)
 #endif
-#ifndef MYELIN_NARROW_KSUB0
-#define MYELIN_NARROW_KSUB0 256  // k per staged B sub-chunk, fp32
+#ifndef MYELIN_NARROW_KSUB3
+#define MYELIN_NARROW_KSUB3 256  // k per staged B sub-chunk, exact-split kernel
 #endif
 
 template <int PREC>
 struct Narrow;
-template <>
-struct Narrow<0> {
-  static constexpr int KG = 4, KSUB = MYELIN_NARROW_KSUB0, PAD = 4;
-};
 template <>
 struct Narrow<1> {
   static constexpr int KG = 8, KSUB = 512, PAD = 8;
@@ -533,26 +549,17 @@ __device__ __forceinline__ float b_elem(const GemmArgs &g, int64_t k, int64_t n)
 template <int PREC>
 struct BFrag;  // a lane's B fragment for one group
 template <>
-struct BFrag<0> {
-  using V = f4;
-};
-template <>
 struct BFrag<1> {
   using V = bf16x8;
 };
 
-// One group: acc += A-fragment (KG fp32 values) x B-fragment.
+// One group: acc += A-fragment (8 fp32 values, rounded to bf16) x B-fragment.
 template <int PREC>
 __device__ __forceinline__ void group_mfma(const float *a, typename BFrag<PREC>::V bv, f32x16 &acc) {
-  if constexpr (PREC == 1) {
-    bf16x8 av;
+  bf16x8 av;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) av[i] = static_cast<__bf16>(a[i]);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[i], acc, 0, 0, 0);
-  }
+  for (int i = 0; i < 8; ++i) av[i] = static_cast<__bf16>(a[i]);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
 }
 
 // A lane's KG values of A for the group starting at k (row m).  FULL: the
@@ -591,13 +598,13 @@ struct NarrowB {
   alignas(16) typename Prec<PREC>::T b[32][LD];
 };
 
-// Stages B(k, n) for k in [ks, ks + kpad), n < N into bs[n][k - ks] (zero
-// past klen; rows past N are never stored, so they stay unwritten).  The
+// Stages B(k, n) for k in [ks, ks + kpad), n < N: put(n, k - ks, value),
+// zero past klen; rows past N are never stored, so they stay unwritten.  The
 // elements are walked flat in memory order -- contiguous when ldb equals the
 // contiguous extent -- 8 loads issued before their LDS writes.
-template <int PREC, bool TB, int LD>
-__device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, int klen, int kpad, int N,
-                                               typename Prec<PREC>::T (*bs)[LD], int tid) {
+template <bool TB, typename Put>
+__device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int klen, int kpad, int N, int tid,
+                                             Put put) {
   constexpr int R = 8;
   const float *B = static_cast<const float *>(g.B);
   const int total = N * klen;
@@ -632,14 +639,20 @@ __device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, in
       if (e < total) {
         int n, kk;
         split(e, n, kk);
-        bs[n][kk] = cvt<PREC>(v[r]);
+        put(n, kk, v[r]);
       }
     }
   }
   for (int e = tid; e < N * (kpad - klen); e += 256) {
     const int n = e / (kpad - klen);
-    bs[n][klen + (e - n * (kpad - klen))] = cvt<PREC>(0.0f);
+    put(n, klen + (e - n * (kpad - klen)), 0.0f);
   }
+}
+
+template <int PREC, bool TB, int LD>
+__device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, int klen, int kpad, int N,
+                                               typename Prec<PREC>::T (*bs)[LD], int tid) {
+  stage_narrow<TB>(g, ks, klen, kpad, N, tid, [&](int n, int kk, float v) { bs[n][kk] = cvt<PREC>(v); });
 }
 
 // C[M, N] (+)= op(A) op(B) (+ bias) for N <= 32.  Workgroup: 4 waves x 32
@@ -698,6 +711,123 @@ __global__ __launch_bounds__(256) void gemm_narrow(GemmArgs g) {
       float t[KG];
       load_group<PREC, TA, PA, VA, false>(g, m, ks + j * GS + kh, ke, t);
       group_mfma<PREC>(t, *reinterpret_cast<const BV *>(brow + j * GS), acc);
+    }
+  }
+  if (!wave_on) return;
+  store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
+}
+
+// gemm_narrow at fp32 precision, on the bf16 MFMA with every product exact.
+// B's staged sub-chunk is split into three bf16 planes (split3: hi + mid +
+// lo == B), and A is packed spike bits (one plane of 0/1 values) or fp32
+// values split the same way as they are loaded.  A product of two bf16
+// values is exact in fp32, so only the fp32 accumulation rounds.  Per group
+// of 16 k the accumulator takes A plane 0 times B planes 0, 1, 2, then A
+// planes 1 and 2 the same way, each skipped (wave-uniformly) when it is zero
+// in every lane: a 0/1 matrix gives the same bits as words or as floats.
+// For a bit operand that is three bf16 MFMAs per 16 k where the fp32 MFMA
+// takes eight 32x32x2 steps at a sixteenth of the bf16 rate; config 4's
+// readout currents (64000 x 4096 bits x 20) and dW_o measured 243 and 208
+// us on the fp32 MFMA.
+struct NarrowB3 {
+  static constexpr int KSUB = MYELIN_NARROW_KSUB3, LD = KSUB + 8;
+  alignas(16) uint16_t b[3][32][LD];
+};
+
+__device__ __forceinline__ bf16x8 bf16_frag(const uint16_t *p) { return *reinterpret_cast<const bf16x8 *>(p); }
+
+template <bool PA>
+__device__ __forceinline__ void group_x3(const float (&a)[8], const uint16_t *b0, const uint16_t *b1,
+                                         const uint16_t *b2, f32x16 &acc) {
+  const bf16x8 v0 = bf16_frag(b0), v1 = bf16_frag(b1), v2 = bf16_frag(b2);
+  bf16x8 ap[3];
+  bool nz1 = false, nz2 = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (PA) {
+      ap[0][i] = static_cast<__bf16>(a[i]);  // 0 or 1
+    } else {
+      uint16_t h, m, l;
+      split3(a[i], h, m, l);
+      ap[0][i] = __builtin_bit_cast(__bf16, h);
+      ap[1][i] = __builtin_bit_cast(__bf16, m);
+      ap[2][i] = __builtin_bit_cast(__bf16, l);
+      nz1 = nz1 || (m & 0x7fffu) != 0;
+      nz2 = nz2 || (l & 0x7fffu) != 0;
+    }
+  }
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v0, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v1, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v2, acc, 0, 0, 0);
+  if constexpr (!PA) {
+    if (__ballot(nz1) != 0) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v2, acc, 0, 0, 0);
+    }
+    if (__ballot(nz2) != 0) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v2, acc, 0, 0, 0);
+    }
+  }
+}
+
+// Same workgroup shape, K split and A streaming as gemm_narrow<1>.
+template <bool TA, bool TB, bool PA, bool VA>
+__global__ __launch_bounds__(256) void gemm_narrow_x3(GemmArgs g) {
+  constexpr int KG = 8, GS = 16, KSUB = NarrowB3::KSUB;
+  constexpr int U = MYELIN_NARROW_U;  // groups in flight per lane
+  __shared__ NarrowB3 sb;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 128 + 32 * w;
+  const bool wave_on = m0 < g.M;  // uniform per wave
+  const int64_t m = (m0 + (lane & 31) < g.M) ? m0 + (lane & 31) : g.M - 1;
+  const int kh = (lane >> 5) * KG;
+  const int N = static_cast<int>(g.N);
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+  for (int64_t ks = kb; ks < ke; ks += KSUB) {
+    const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
+    const int kpad = (klen + GS - 1) / GS * GS;
+    const int ng = kpad / GS;
+    const int nfull = klen / (U * GS);  // batches of U groups wholly below ke
+    float a[U][KG];
+    if (wave_on && nfull > 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_group<1, TA, PA, VA, true>(g, m, ks + u * GS + kh, ke, a[u]);
+    }
+    if (ks != kb) __syncthreads();  // the previous sub-chunk's fragments are read
+    stage_narrow<TB>(g, ks, klen, kpad, N, tid, [&](int n, int kk, float v) {
+      uint16_t h, mid, l;
+      split3(v, h, mid, l);
+      sb.b[0][n][kk] = h;
+      sb.b[1][n][kk] = mid;
+      sb.b[2][n][kk] = l;
+    });
+    __syncthreads();
+    if (!wave_on) continue;
+    const uint16_t *b0 = &sb.b[0][lane & 31][kh], *b1 = &sb.b[1][lane & 31][kh], *b2 = &sb.b[2][lane & 31][kh];
+    for (int bi = 0; bi < nfull; ++bi) {
+      if (bi > 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_group<1, TA, PA, VA, true>(g, m, ks + (bi * U + u) * GS + kh, ke, a[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int o = (bi * U + u) * GS;
+        group_x3<PA>(a[u], b0 + o, b1 + o, b2 + o, acc);
+      }
+    }
+    for (int j = nfull * U; j < ng; ++j) {
+      float t[KG];
+      load_group<1, TA, PA, VA, false>(g, m, ks + j * GS + kh, ke, t);
+      group_x3<PA>(t, b0 + j * GS, b1 + j * GS, b2 + j * GS, acc);
     }
   }
   if (!wave_on) return;
@@ -2450,26 +2580,6 @@ __global__ __launch_bounds__(acc_fwd::NT) __attribute__((amdgpu_waves_per_eu(2))
     }
 }
 
-// Three bf16 values whose float sum is exactly v: h = bf16(v) (nearest
-// even), m = bf16(v - h), l = v - h - m.  v - h is exact and has at most 16
-// significant bits, so after m at most 8 remain and l is exact as well (for
-// |v| >= 2^-110; below that l would be subnormal in bf16).  Non-finite v:
-// h carries it, m = l = 0.
-__device__ __forceinline__ void split3(float v, uint16_t &h, uint16_t &m, uint16_t &l) {
-  const __bf16 bh = static_cast<__bf16>(v);
-  if (!__builtin_isfinite(v)) {
-    h = __builtin_bit_cast(uint16_t, bh);
-    m = l = 0;
-    return;
-  }
-  const float r1 = v - static_cast<float>(bh);
-  const __bf16 bm = static_cast<__bf16>(r1);
-  const float r2 = r1 - static_cast<float>(bm);
-  h = __builtin_bit_cast(uint16_t, bh);
-  m = __builtin_bit_cast(uint16_t, bm);
-  l = __builtin_bit_cast(uint16_t, static_cast<__bf16>(r2));
-}
-
 // v is a bf16 value the MFMA multiplies exactly: its bf16 rounding returns
 // it, and it is zero or normal (denormals may be flushed)
 __device__ __forceinline__ bool bf16_exact(float v) {
@@ -2999,10 +3109,15 @@ void launch_big_t(const GemmArgs &g, int ta, int tb, bool half, dim3 grid, hipSt
 
 // K splits of the narrow kernel: only as many as bring the grid to about
 // 1024 workgroups (each split costs a partial [M, N] in the workspace).
-int64_t narrow_splits(int64_t M, int64_t K) {
-  int64_t s = cdiv(MYELIN_NARROW_WGS, cdiv(M, 128));
-  const int64_t by_k = cdiv(K, 64);
-  if (s > by_k) s = by_k;
+// K splits of the narrow kernel: chunks of about MYELIN_NARROW_KCHUNK k (at
+// most 64 of them), a function of K alone.  Each output element then sums
+// the same k ranges in the same order whatever M is, so a layer's currents
+// come out the same bits however its caller divides the rows (all time
+// steps at once, or a group of checkpoint chunks at a time) -- which keeps
+// two routes through a network whose surrogate adjoint amplifies rounding
+// over thousands of steps on the same trajectory.
+int64_t narrow_splits(int64_t K) {
+  int64_t s = cdiv(K, MYELIN_NARROW_KCHUNK);
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
 }
@@ -3016,6 +3131,29 @@ void launch_narrow_v(const GemmArgs &g, bool va, dim3 grid, hipStream_t s) {
     }
   }
   gemm_narrow<PREC, TA, TB, PA, false><<<grid, dim3(256), 0, s>>>(g);
+}
+
+template <bool TA, bool TB, bool PA>
+void launch_narrow_x3_v(const GemmArgs &g, bool va, dim3 grid, hipStream_t s) {
+  if constexpr (!TA && !PA) {
+    if (va) {
+      gemm_narrow_x3<TA, TB, PA, true><<<grid, dim3(256), 0, s>>>(g);
+      return;
+    }
+  }
+  gemm_narrow_x3<TA, TB, PA, false><<<grid, dim3(256), 0, s>>>(g);
+}
+
+template <bool PA>
+void launch_narrow_x3(const GemmArgs &g, int ta, int tb, bool va, dim3 grid, hipStream_t s) {
+  if (!ta && !tb)
+    launch_narrow_x3_v<false, false, PA>(g, va, grid, s);
+  else if (!ta)
+    launch_narrow_x3_v<false, true, PA>(g, va, grid, s);
+  else if (!tb)
+    launch_narrow_x3_v<true, false, PA>(g, va, grid, s);
+  else
+    launch_narrow_x3_v<true, true, PA>(g, va, grid, s);
 }
 
 template <int PREC, bool PA>
@@ -3073,17 +3211,24 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   constexpr int KS = Prec<PREC>::KS;
   if (!half && g.N <= 32) {
     // narrow output (readout currents, dW_o): stream A once
-    int64_t splits = g.ws != nullptr ? narrow_splits(g.M, g.K) : 1;
+    int64_t splits = g.ws != nullptr ? narrow_splits(g.K) : 1;
     while (splits > 1 && splits * g.M * g.N > ws_elems) --splits;
     g.kchunk = cdiv(cdiv(g.K, splits), 64) * 64;
     splits = cdiv(g.K, g.kchunk);
     g.splits = static_cast<int>(splits);
     const dim3 grid(static_cast<unsigned>(cdiv(g.M, 128)), static_cast<unsigned>(splits));
     const bool va = !bits && al16(g.A) && g.lda % 4 == 0;
-    if (bits)
+    if constexpr (PREC == 0) {
+      // fp32: the exact three-plane split on the bf16 MFMA
+      if (bits)
+        launch_narrow_x3<true>(g, ta, tb, va, grid, s);
+      else
+        launch_narrow_x3<false>(g, ta, tb, va, grid, s);
+    } else if (bits) {
       launch_narrow<PREC, true>(g, ta, tb, va, grid, s);
-    else
+    } else {
       launch_narrow<PREC, false>(g, ta, tb, va, grid, s);
+    }
     if (int rc = myelin::launched("gemm (narrow)")) return rc;
     if (splits > 1) {
       launch_reduce(g, s);
@@ -3255,7 +3400,7 @@ void launch_currents(const CurArgs &a, dim3 grid, hipStream_t s) {
 extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, int precision) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   // the largest split any kernel for this output could use
-  int64_t most = N <= 32 ? narrow_splits(M, K) : 1;
+  int64_t most = N <= 32 ? narrow_splits(K) : 1;
   for (int64_t edge : {static_cast<int64_t>(kTile), static_cast<int64_t>(kBig)}) {
     const int64_t tiles = cdiv(M, edge) * cdiv(N, edge);
     const int64_t s = precision == MYELIN_PREC_BF16 ? plan_splits<1>(tiles, K, MYELIN_SPLIT_WANT) : plan_splits<0>(tiles, K, MYELIN_SPLIT_WANT);

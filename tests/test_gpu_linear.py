@@ -534,6 +534,40 @@ def test_gemm_packed_bit_operand_equals_dense(M, N, K, ta, tb, prec):
         assert torch.equal(bits_wide, dense)
 
 
+@pytest.mark.parametrize("bits", [False, True])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_narrow_gemm_rows_independent_of_m(bits, prec):
+    """The narrow-output kernel (N <= 32) splits K by K alone, so rows
+    computed in a call of their own equal the same rows of one call over all
+    of them, bit for bit: a readout's currents do not depend on how its
+    caller divides the time steps (all at once, or a group of checkpoint
+    chunks at a time).  At fp32 precision it also checks the exact
+    three-plane split against float64."""
+
+    _print_case(test="narrow_rows", bits=bits, prec=prec)
+    M, N, K = 6400, 20, 4096
+    g = seeded(4096 + int(bits) + 2 * (prec == "fp32"))
+    A = (torch.rand(M, K, generator=g) < 0.1).float()
+    W = (torch.rand(K, N, generator=g) - 0.5) / 32
+    Ad, Wd = A.to(DEV), W.to(DEV)
+    op = myelin.pack_spikes(Ad).data if bits else Ad
+    lda = op.shape[1]
+    stream = _lib.stream(torch.device(DEV))
+
+    def run(r0, r1):
+        C = torch.empty(r1 - r0, N, device=DEV)
+        _gemm(op[r0:r1], Wd, C, r1 - r0, N, K, lda, N, N, False, False, False, _lib.PREC[prec], stream,
+              a_bits=bits)
+        return C
+
+    full = run(0, M)
+    for r0, r1 in ((0, 2880), (2880, 5760), (5760, M), (17, 18)):
+        assert torch.equal(run(r0, r1), full[r0:r1]), (r0, r1)
+    if prec == "fp32":
+        ref = A.double() @ W.double()
+        assert_norm_close(full.cpu().double(), ref, 1e-6, "narrow fp32 (exact split) vs float64")
+
+
 def test_gemm_packed_bit_operand_checks():
     stream = _lib.stream(torch.device(DEV))
     words = torch.zeros(16, 2, dtype=torch.int32, device=DEV)
