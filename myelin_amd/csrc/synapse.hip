@@ -604,7 +604,7 @@ struct NarrowB {
 // contiguous extent -- 8 loads issued before their LDS writes.
 template <bool TB, typename Put>
 __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int klen, int kpad, int N, int tid,
-                                             Put put) {
+                                             int nt, Put put) {
   constexpr int R = 8;
   const float *B = static_cast<const float *>(g.B);
   const int total = N * klen;
@@ -623,11 +623,11 @@ __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int 
       n = e - q * N;
     }
   };
-  for (int e0 = tid; e0 < total; e0 += 256 * R) {
+  for (int e0 = tid; e0 < total; e0 += nt * R) {
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      int e = e0 + 256 * r;
+      int e = e0 + nt * r;
       e = e < total ? e : total - 1;  // clamped: every load in range
       int n, kk;
       split(e, n, kk);
@@ -635,7 +635,7 @@ __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int 
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int e = e0 + 256 * r;
+      const int e = e0 + nt * r;
       if (e < total) {
         int n, kk;
         split(e, n, kk);
@@ -643,7 +643,7 @@ __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int 
       }
     }
   }
-  for (int e = tid; e < N * (kpad - klen); e += 256) {
+  for (int e = tid; e < N * (kpad - klen); e += nt) {
     const int n = e / (kpad - klen);
     put(n, klen + (e - n * (kpad - klen)), 0.0f);
   }
@@ -652,7 +652,7 @@ __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int 
 template <int PREC, bool TB, int LD>
 __device__ __forceinline__ void stage_narrow_b(const GemmArgs &g, int64_t ks, int klen, int kpad, int N,
                                                typename Prec<PREC>::T (*bs)[LD], int tid) {
-  stage_narrow<TB>(g, ks, klen, kpad, N, tid, [&](int n, int kk, float v) { bs[n][kk] = cvt<PREC>(v); });
+  stage_narrow<TB>(g, ks, klen, kpad, N, tid, 256, [&](int n, int kk, float v) { bs[n][kk] = cvt<PREC>(v); });
 }
 
 // C[M, N] (+)= op(A) op(B) (+ bias) for N <= 32.  Workgroup: 4 waves x 32
@@ -803,7 +803,7 @@ __global__ __launch_bounds__(256) void gemm_narrow_x3(GemmArgs g) {
       for (int u = 0; u < U; ++u) load_group<1, TA, PA, VA, true>(g, m, ks + u * GS + kh, ke, a[u]);
     }
     if (ks != kb) __syncthreads();  // the previous sub-chunk's fragments are read
-    stage_narrow<TB>(g, ks, klen, kpad, N, tid, [&](int n, int kk, float v) {
+    stage_narrow<TB>(g, ks, klen, kpad, N, tid, 256, [&](int n, int kk, float v) {
       uint16_t h, mid, l;
       split3(v, h, mid, l);
       sb.b[0][n][kk] = h;
@@ -828,6 +828,83 @@ __global__ __launch_bounds__(256) void gemm_narrow_x3(GemmArgs g) {
       float t[KG];
       load_group<1, TA, PA, VA, false>(g, m, ks + j * GS + kh, ke, t);
       group_x3<PA>(t, b0 + j * GS, b1 + j * GS, b2 + j * GS, acc);
+    }
+  }
+  if (!wave_on) return;
+  store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
+}
+
+// Narrow GEMM with row-major packed-bit A (the readout currents I = S W_o
+// from the hidden spikes' packed twin): NP = 3 bf16 planes of B (fp32
+// precision, exact, as gemm_narrow_x3) or NP = 1 (bf16 precision, B rounded,
+// as gemm_narrow<1>), the same MFMAs on the same k in the same order as
+// those kernels, so the bits equal theirs.  Eight waves of 32 rows share one
+// staged sub-chunk of B (the staging and its split cost as much VALU as the
+// MFMA feed at four waves), and a lane turns its 8 bits of a group into
+// the bf16 fragment with integer operations (0/1 -> 0x0000/0x3F80) instead
+// of going through floats.  64000 x 4096 x 20 at fp32: 150 -> 95 us.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t bf16_pair_of_bits(uint32_t t) {
+  // bit 0 -> the low bf16, bit 1 -> the high one
+  return ((t & 1u) | ((t & 2u) << 15)) * 0x3F80u;
+}
+
+template <int NP>
+struct NarrowBits {
+  static constexpr int KSUB = 256, LD = KSUB + 8, WAVES = 8;
+  alignas(16) uint16_t b[NP][32][LD];
+};
+
+template <int NP>
+__global__ __launch_bounds__(64 * NarrowBits<NP>::WAVES) void gemm_narrow_bits(GemmArgs g) {
+  using L = NarrowBits<NP>;
+  constexpr int KG = 8, GS = 16, KSUB = L::KSUB, WAVES = L::WAVES;
+  __shared__ L sb;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * (32 * WAVES) + 32 * w;
+  const bool wave_on = m0 < g.M;  // uniform per wave
+  const int64_t m = (m0 + (lane & 31) < g.M) ? m0 + (lane & 31) : g.M - 1;
+  const int kh = (lane >> 5) * KG;
+  const int N = static_cast<int>(g.N);
+  const int32_t *arow = static_cast<const int32_t *>(g.A) + m * g.lda;
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+  for (int64_t ks = kb; ks < ke; ks += KSUB) {
+    const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
+    const int kpad = (klen + GS - 1) / GS * GS;
+    if (ks != kb) __syncthreads();  // the previous sub-chunk's fragments are read
+    stage_narrow<false>(g, ks, klen, kpad, N, tid, 64 * WAVES, [&](int n, int kk, float v) {
+      if constexpr (NP == 3) {
+        uint16_t h, mid, l;
+        split3(v, h, mid, l);
+        sb.b[0][n][kk] = h;
+        sb.b[1][n][kk] = mid;
+        sb.b[2][n][kk] = l;
+      } else {
+        sb.b[0][n][kk] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+      }
+    });
+    __syncthreads();
+    if (!wave_on) continue;
+    const int ng = kpad / GS, nfull = klen / GS;
+    for (int j = 0; j < ng; ++j) {
+      const int64_t k = ks + j * GS + kh;
+      uint32_t wv = k < ke ? static_cast<uint32_t>(arow[k >> 5]) >> (k & 31) : 0u;
+      if (j >= nfull && k + KG > ke) wv &= k < ke ? (1u << (ke - k)) - 1u : 0u;
+      const u32x4 d = {bf16_pair_of_bits(wv), bf16_pair_of_bits(wv >> 2), bf16_pair_of_bits(wv >> 4),
+                       bf16_pair_of_bits(wv >> 6)};
+      const bf16x8 av = __builtin_bit_cast(bf16x8, d);
+      const int o = j * GS + kh;
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, *reinterpret_cast<const bf16x8 *>(&sb.b[p][lane & 31][o]),
+                                                      acc, 0, 0, 0);
     }
   }
   if (!wave_on) return;
@@ -3218,7 +3295,14 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     g.splits = static_cast<int>(splits);
     const dim3 grid(static_cast<unsigned>(cdiv(g.M, 128)), static_cast<unsigned>(splits));
     const bool va = !bits && al16(g.A) && g.lda % 4 == 0;
-    if constexpr (PREC == 0) {
+    if (bits && !ta && !tb) {
+      // row-major bit rows: eight waves a workgroup
+      const dim3 wide(static_cast<unsigned>(cdiv(g.M, 32 * NarrowBits<1>::WAVES)), static_cast<unsigned>(splits));
+      if constexpr (PREC == 0)
+        gemm_narrow_bits<3><<<wide, dim3(64 * NarrowBits<3>::WAVES), 0, s>>>(g);
+      else
+        gemm_narrow_bits<1><<<wide, dim3(64 * NarrowBits<1>::WAVES), 0, s>>>(g);
+    } else if constexpr (PREC == 0) {
       // fp32: the exact three-plane split on the bf16 MFMA
       if (bits)
         launch_narrow_x3<true>(g, ta, tb, va, grid, s);
