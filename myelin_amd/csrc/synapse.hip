@@ -1528,9 +1528,12 @@ __attribute__((amdgpu_waves_per_eu(WM * WN > 4 ? 1 : 2))) void gemm_big(GemmArgs
 // (32 rows x one k-group per half-wave) on distinct banks.
 //
 // NS stages in LDS; per stage: wait for the stage's loads and barrier; read
-// all of the stage's fragments into registers; issue the loads of stage
+// the fragments of the stage's first k step; issue the loads of stage
 // s + NS - 1 into the buffer stage s - 1 used (whose readers all passed the
-// barrier); run the MFMAs.  Against register staging at 8192 x 4096 x 3 x
+// barrier); run the MFMAs of each k step with the next k step's fragment
+// reads in flight (two register sets of one k step: against reading the
+// stage in halves, 8192 x 4096 x 3 x 1024 on 256 x 256 tiles 188 -> 178
+// us, 218 -> 194 VGPRs, the same bits).  Against register staging at 8192 x 4096 x 3 x
 // 1024 (256 x 128 tiles): 221 -> 208 us; on 128 x 128 tiles (two stages,
 // two workgroups per CU) it measured mixed (12800 x 784 x 2048: 64 -> 69
 // us), so those keep register staging.
@@ -1591,9 +1594,6 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
     GemmArgs g) {
   constexpr int WGN = BN / (32 * WN);
   constexpr int NT = 64 * (BM / (32 * WM)) * WGN;
-  // wave tiles above 64 x 64 read a stage's fragments in two halves (k
-  // steps 0-1, then 2-3) to stay within 256 registers
-  constexpr int KH = WM * WN > 4 ? 2 : 4;
   constexpr int TILE = (BM + BN) * 128;  // bytes of one stage
   // loads per thread per stage; a stage's wait leaves the NS - 2 later
   // stages' loads in flight
@@ -1674,24 +1674,25 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
       // this wave's LDS reads of the previous stage, whose buffer the
       // direct loads issued after this barrier overwrite
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      // the fragments of k step ks + 1 are read while step ks multiplies
+      // (two register sets of one k step each)
+      bf16x8 a[2][WM], b[2][WN];
+      auto rd = [&](int ks, int set) {
 #pragma unroll
-      for (int k0 = 0; k0 < 4; k0 += KH) {
-        bf16x8 a[KH][WM], b[KH][WN];
+        for (int i = 0; i < WM; ++i) a[set][i] = *reinterpret_cast<const bf16x8 *>(cur + fa[i][ks]);
 #pragma unroll
-        for (int ks = 0; ks < KH; ++ks) {
+        for (int j = 0; j < WN; ++j) b[set][j] = *reinterpret_cast<const bf16x8 *>(cur + fb[j][ks]);
+      };
+      rd(0, 0);
+      if (s + NS - 1 < total) issue(nxt);
 #pragma unroll
-          for (int i = 0; i < WM; ++i) a[ks][i] = *reinterpret_cast<const bf16x8 *>(cur + fa[i][k0 + ks]);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
 #pragma unroll
-          for (int j = 0; j < WN; ++j) b[ks][j] = *reinterpret_cast<const bf16x8 *>(cur + fb[j][k0 + ks]);
-        }
-        if (k0 == 0 && s + NS - 1 < total) issue(nxt);
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int ks = 0; ks < KH; ++ks)
-#pragma unroll
-          for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
       }
     };
     issue(l0);
@@ -1802,7 +1803,6 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
   constexpr int NT = 64 * (BM / (32 * WM)) * WGN;
   constexpr int RA = 2 * BM, RB = 2 * BN;    // bytes of an A row and of a B row
   constexpr int TILE = 64 * (RA + RB);       // bytes of one stage: A rows, then B rows
-  constexpr int KH = WM * WN > 4 ? 2 : 4;    // k steps read at a time (as gemm_dma)
   using LA = DmaLoaderMN<BM, NT>;
   using LB = DmaLoaderMN<BN, NT>;
   constexpr int NL = LA::NP + LB::NP;
@@ -1892,24 +1892,24 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       // a tail stage was written with LDS stores: lgkmcnt(0) covers them
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      // k step ks + 1's fragments are read while step ks multiplies
+      bf16x8 a[2][WM], b[2][WN];
+      auto rd = [&](int ks, int set) {
 #pragma unroll
-      for (int k0 = 0; k0 < 4; k0 += KH) {
-        bf16x8 a[KH][WM], b[KH][WN];
+        for (int i = 0; i < WM; ++i) a[set][i] = frag(cur, fa[i][ks][0], fa[i][ks][1]);
 #pragma unroll
-        for (int ks = 0; ks < KH; ++ks) {
+        for (int j = 0; j < WN; ++j) b[set][j] = frag(cur, fb[j][ks][0], fb[j][ks][1]);
+      };
+      rd(0, 0);
+      if (s + NS - 1 < total) issue(nxt);
 #pragma unroll
-          for (int i = 0; i < WM; ++i) a[ks][i] = frag(cur, fa[i][k0 + ks][0], fa[i][k0 + ks][1]);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
 #pragma unroll
-          for (int j = 0; j < WN; ++j) b[ks][j] = frag(cur, fb[j][k0 + ks][0], fb[j][k0 + ks][1]);
-        }
-        if (k0 == 0 && s + NS - 1 < total) issue(nxt);
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int ks = 0; ks < KH; ++ks)
-#pragma unroll
-          for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
       }
     };
     issue(l0);
