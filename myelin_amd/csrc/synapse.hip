@@ -3295,8 +3295,9 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     g.splits = static_cast<int>(splits);
     const dim3 grid(static_cast<unsigned>(cdiv(g.M, 128)), static_cast<unsigned>(splits));
     const bool va = !bits && al16(g.A) && g.lda % 4 == 0;
-    if (bits && !ta && !tb) {
-      // row-major bit rows: eight waves a workgroup
+    if (bits && !ta && !tb && cdiv(g.M, 32 * NarrowBits<1>::WAVES) * splits >= 512) {
+      // row-major bit rows with two rounds of eight-wave workgroups (fewer
+      // measured slower: 12800 x 2048 x 10, 200 workgroups, 13 -> 16 us)
       const dim3 wide(static_cast<unsigned>(cdiv(g.M, 32 * NarrowBits<1>::WAVES)), static_cast<unsigned>(splits));
       if constexpr (PREC == 0)
         gemm_narrow_bits<3><<<wide, dim3(64 * NarrowBits<3>::WAVES), 0, s>>>(g);
