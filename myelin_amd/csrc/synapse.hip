@@ -1547,12 +1547,19 @@ template <int ROWS, int NT>
 struct DmaLoader {
   static constexpr int NP = ROWS * 8 / NT;
   static_assert(ROWS * 8 % NT == 0, "pieces per thread");
-  const uint16_t *q[NP];
+  // a wave-uniform base (scalar registers) and 32-bit byte offsets per
+  // piece: the loads take the base + offset form, so a stage's addresses
+  // cost no 64-bit vector arithmetic (8192 x 4096 x 3 x 1024 on 256 x 256
+  // tiles: 4-8 % faster than 64-bit per-piece pointers; the host keeps
+  // ROWS * ld * 2 bytes below 2^31)
+  const uint16_t *base;
+  uint32_t off[NP];
   int lds_off[NP];  // wave-uniform byte offset of the piece group in the tile
 
-  __device__ __forceinline__ void init(int tid, int w, const uint16_t *base, int64_t mn0, int64_t mn_total,
+  __device__ __forceinline__ void init(int tid, int w, const uint16_t *b, int64_t mn0, int64_t mn_total,
                                        int64_t ld) {
     const int64_t lim = mn_total - mn0;
+    base = b + mn0 * ld;
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       const int idx = e * NT + tid;
@@ -1560,7 +1567,7 @@ struct DmaLoader {
       const int c = pos ^ dma_swz(row);
       // rows past the edge read the last row: they feed discarded outputs
       const int64_t rc = row < lim ? row : lim - 1;
-      q[e] = base + (mn0 + rc) * ld + 8 * c;
+      off[e] = static_cast<uint32_t>((rc * ld + 8 * c) * 2);
       lds_off[e] = (e * NT + w * 64) * 16;
     }
   }
@@ -1570,6 +1577,7 @@ struct DmaLoader {
   // before the epilogue's own loads).  M0 holds the wave's LDS base during
   // each load.
   __device__ __forceinline__ void issue(char *tile, int64_t k0) const {
+    const uint16_t *p = base + k0;
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(tile + lds_off[e])));
@@ -1577,16 +1585,13 @@ struct DmaLoader {
       // reads it at issue)
       uint32_t m0_saved;
       asm volatile(
-          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
           : "=&s"(m0_saved)
-          : "v"(q[e] + k0), "s"(dst)
+          : "v"(off[e]), "s"(p), "s"(dst)
           : "memory");
     }
   }
-  __device__ __forceinline__ void shift(int64_t d) {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) q[e] += d;
-  }
+  __device__ __forceinline__ void shift(int64_t d) { base += d; }
 };
 
 template <int BM, int BN, bool MP, int NS, int WM = 2, int WN = 2>
@@ -1744,14 +1749,19 @@ struct DmaLoaderMN {
   static constexpr int CPR = COLS / 8;  // pieces per row
   static constexpr int NP = 64 * CPR / NT;
   static_assert(64 * CPR % NT == 0, "pieces per thread");
-  const uint16_t *q[NP];  // piece at k = 0 of the stage (row kk[e])
+  // wave-uniform base and 32-bit byte offsets of the pieces at k = 0 of
+  // the stage (row kk[e]), as DmaLoader (the host keeps 64 * ld plus the
+  // row length below 2^30 elements)
+  const uint16_t *base;
+  uint32_t off[NP];
   int kk[NP];
   int lds_off[NP];
   int64_t ld;
 
-  __device__ __forceinline__ void init(int tid, int w, const uint16_t *base, int64_t mn0, int64_t mn_total,
+  __device__ __forceinline__ void init(int tid, int w, const uint16_t *b, int64_t mn0, int64_t mn_total,
                                        int64_t ld_) {
     ld = ld_;
+    base = b;
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       const int idx = e * NT + tid;
@@ -1763,37 +1773,36 @@ struct DmaLoaderMN {
       int64_t col = mn0 + 8 * c;
       if (col + 8 > mn_total) col = mn_total - 8;
       kk[e] = k;
-      q[e] = base + k * ld + col;
+      off[e] = static_cast<uint32_t>((k * ld + col) * 2);
       lds_off[e] = (e * NT + w * 64) * 16;
     }
   }
   // a whole stage: rows k0 .. k0 + 63
   __device__ __forceinline__ void issue(char *tile, int64_t k0) const {
+    const uint16_t *p = base + k0 * ld;
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(tile + lds_off[e])));
       uint32_t m0_saved;
       asm volatile(
-          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
           : "=&s"(m0_saved)
-          : "v"(q[e] + k0 * ld), "s"(dst)
+          : "v"(off[e]), "s"(p), "s"(dst)
           : "memory");
     }
   }
   // a partial stage: rows k0 .. ke - 1, zeros after
   __device__ __forceinline__ void tail(char *tile, int64_t k0, int64_t ke) const {
     const int lane = threadIdx.x & 63;
+    const char *p = reinterpret_cast<const char *>(base + k0 * ld);
 #pragma unroll
     for (int e = 0; e < NP; ++e) {
       u4 v = {0u, 0u, 0u, 0u};
-      if (k0 + kk[e] < ke) v = *reinterpret_cast<const u4 *>(q[e] + k0 * ld);
+      if (k0 + kk[e] < ke) v = *reinterpret_cast<const u4 *>(p + off[e]);
       *reinterpret_cast<u4 *>(tile + lds_off[e] + lane * 16) = v;
     }
   }
-  __device__ __forceinline__ void shift(int64_t d) {
-#pragma unroll
-    for (int e = 0; e < NP; ++e) q[e] += d;
-  }
+  __device__ __forceinline__ void shift(int64_t d) { base += d; }
 };
 
 template <bool MP, int NS, int BM = 128, int BN = 128, int WM = 2, int WN = 2>
@@ -3061,9 +3070,13 @@ bool use_tall(const GemmArgs &g, int ta, int tb, bool half) {
 
 // Direct global -> LDS staging (gemm_dma): bf16 operands, both k-contiguous,
 // 16-byte aligned rows, whole 64-k stages in every part and K split.
+// the direct loaders address a tile's pieces by 32-bit byte offsets from
+// a scalar base: 256 rows of the leading dimension stay below 2^31 bytes
+constexpr int64_t kDmaMaxLd = int64_t{1} << 22;
+
 bool use_dma(const GemmArgs &g, int ta, int tb, bool half) {
   return MYELIN_GEMM_DMA && half && !ta && tb && g.K % 64 == 0 && al16(g.A) && al16(g.B) && g.lda % 8 == 0 &&
-         g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0);
+         g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0) && g.lda < kDmaMaxLd && g.ldb < kDmaMaxLd;
 }
 
 // three 48 KB stages (144 KB of LDS, one workgroup per CU): each stage's
@@ -3080,7 +3093,8 @@ void launch_dma_tall(const GemmArgs &g, dim3 grid, hipStream_t s) {
 // and aligned rows.
 bool use_dma_mn(const GemmArgs &g, int ta, int tb, bool half) {
   return MYELIN_GEMM_DMA && half && ta && !tb && g.M % 8 == 0 && g.N % 8 == 0 && al16(g.A) && al16(g.B) &&
-         g.lda % 8 == 0 && g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0);
+         g.lda % 8 == 0 && g.ldb % 8 == 0 && (g.parts == 1 || g.b_part % 8 == 0) && g.lda < kDmaMaxLd &&
+         g.ldb < kDmaMaxLd;
 }
 
 // two 32 KB stages (two workgroups per CU).  Against register staging,
