@@ -383,7 +383,10 @@ int myelin_split_bf16x3(const float *src, uint16_t *dst, int64_t rows,
  *   d = slope*sigma'(slope*(pre - thr)); gp = gm*((1-s) + (reset-pre)*d)
  *   + g_spike*d; G[j] = gp; gm = gp*decay   (grad_m is in/out)
  * g_spike = grad_spikes[j] (may be NULL) plus grad_rates/T_total (may be
- * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.  G is written
+ * NULL).  gbias_acc [BN] (may be NULL) accumulates sum_j gp.  grad_m NULL
+ * makes the launch a whole reverse pass: gm starts at zero and is not
+ * returned, and gbias_acc receives sum_j gp (written, not accumulated),
+ * so the caller needs no zero-filled buffers.  G is written
  * as g_dtype MYELIN_DT_F32, or MYELIN_DT_BF16 (round to nearest even, the
  * rounding the bf16 GEMMs apply) when only bf16 GEMMs read it, or
  * MYELIN_DT_BF16X3: three bf16 planes [3, C, BN] as myelin_split_bf16x3

@@ -2792,7 +2792,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   float gm[V], gstep[V], gb[V];
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-    gm[e] = p.gm[i + e];
+    gm[e] = p.gm != nullptr ? p.gm[i + e] : 0.0f;
     gstep[e] = p.grate != nullptr ? p.grate[i + e] / p.rate_denominator : 0.0f;
     gb[e] = 0.0f;
   }
@@ -2847,8 +2847,10 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   }
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-    p.gm[i + e] = gm[e];
-    if (p.gbias_acc != nullptr) p.gbias_acc[i + e] = p.gbias_acc[i + e] + gb[e];
+    // no gm: the launch is the whole reverse pass (no carried adjoint in or
+    // out), and the bias accumulator starts from zero here
+    if (p.gm != nullptr) p.gm[i + e] = gm[e];
+    if (p.gbias_acc != nullptr) p.gbias_acc[i + e] = (p.gm != nullptr ? p.gbias_acc[i + e] : 0.0f) + gb[e];
   }
 }
 
@@ -3740,7 +3742,7 @@ extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
                                      int64_t T_total, float decay, float threshold, float reset, float slope,
                                      int surrogate_id, int rule, myelin_stream_t stream) {
   if (C < 1 || BN < 1) return myelin::invalid("linear_pre_bwd: C and BN must be positive");
-  if (pre == nullptr || grad_m == nullptr || G == nullptr) return myelin::invalid("linear_pre_bwd: null pointer");
+  if (pre == nullptr || G == nullptr) return myelin::invalid("linear_pre_bwd: null pointer");
   if (g_dtype != MYELIN_DT_F32 && g_dtype != MYELIN_DT_BF16 && g_dtype != MYELIN_DT_BF16X3)
     return myelin::invalid("linear_pre_bwd: G must be float32, bfloat16 or three bfloat16 planes");
   PreBwdArgs a{pre, grad_spikes, grad_rates, grad_m, G, gbias_acc, C, BN, decay, threshold, reset, slope,

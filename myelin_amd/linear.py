@@ -505,17 +505,6 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
     with torch.cuda.device(dev):
         stream = _lib.stream(dev)
         wg = _cast_bf16(w, stream) if (half and need_x) else w
-        # the zero-started buffers (the membrane adjoint unless given, the bias
-        # gradient's accumulator) share one allocation: one fill launch
-        want_gb = need_b and b is not None
-        zeros = torch.zeros(((g_m is None) + want_gb, B, N), device=dev) if (g_m is None or want_gb) else None
-        gm = g_m.float().contiguous().clone() if g_m is not None else zeros[0]
-        g_out = None if g_out is None else g_out.float().contiguous()
-        g_spikes = None if rate else g_out
-        g_rates = g_out if rate else None
-        gx = torch.empty((T, B, F), device=dev) if need_x else None
-        gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
-        gb_acc = zeros[-1] if want_gb else None
         # the reverse pass walks spans of whole checkpoint chunks, as many as
         # keep a span's trace within _CURRENT_CHUNK_ELEMS: one recompute
         # (from the span's first checkpoint, which the recurrence carries
@@ -523,6 +512,22 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         # launch and one dX / dW GEMM pair per span instead of per chunk
         span = T if checkpoint is None else _span(T, checkpoint, BN)
         per = 1 if checkpoint is None else span // checkpoint  # checkpoint rows per span
+        want_gb = need_b and b is not None
+        # one span and no membrane gradient: the reverse launch is the whole
+        # pass (no adjoint buffer; it writes the bias sums itself), else the
+        # zero-started buffers (the membrane adjoint unless given, the bias
+        # gradient's accumulator) share one allocation: one fill launch
+        whole = g_m is None and span >= T
+        zeros = None
+        if not whole and (g_m is None or want_gb):
+            zeros = torch.zeros(((g_m is None) + want_gb, B, N), device=dev)
+        gm = g_m.float().contiguous().clone() if g_m is not None else (None if whole else zeros[0])
+        g_out = None if g_out is None else g_out.float().contiguous()
+        g_spikes = None if rate else g_out
+        g_rates = g_out if rate else None
+        gx = torch.empty((T, B, F), device=dev) if need_x else None
+        gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
+        gb_acc = (torch.empty((B, N), device=dev) if whole else zeros[-1]) if want_gb else None
         G = torch.empty((min(span, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
         # exact split: dW reads G as three bf16 planes [3, C, B, N] (C the
         # span's steps), written by the reverse pass itself unless dX needs

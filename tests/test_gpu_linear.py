@@ -681,3 +681,32 @@ def test_reverse_pass_two_neurons_per_lane_equals_one(gdt, with_gs):
         outs.append((G.cpu(), m_.cpu(), gb.cpu()))
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("BN", [640, 66002])
+@pytest.mark.parametrize("gdt", ["fp32", "planes"])
+def test_reverse_pass_without_adjoint_buffer_equals_zero_started(BN, gdt):
+    """grad_m NULL makes linear_pre_bwd a whole reverse pass: the adjoint
+    starts at zero and the bias sums are written, not accumulated.  G and
+    the bias sums equal a launch on zero-filled buffers bit for bit (one and
+    two neurons per lane)."""
+
+    _print_case(test="pre_bwd_whole", BN=BN, gdt=gdt)
+    C = 29
+    g = seeded(BN + 7)
+    pre = (torch.randn(C * BN, generator=g) + 0.8).to(DEV)
+    gs = torch.randn(C * BN, generator=g).to(DEV)
+    dt = {"fp32": _lib.DT[torch.float32], "planes": _lib.DT_BF16X3}[gdt]
+    gdtype = torch.float32 if gdt == "fp32" else torch.bfloat16
+    glen = C * BN * (3 if gdt == "planes" else 1)
+    stream = _lib.stream(torch.device(DEV))
+    outs = []
+    for whole in (False, True):
+        gm = None if whole else torch.zeros(BN, device=DEV)
+        gb = torch.full((BN,), float("nan"), device=DEV) if whole else torch.zeros(BN, device=DEV)
+        G = torch.empty(glen, dtype=gdtype, device=DEV)
+        _lib.call("myelin_linear_pre_bwd", _lib.ptr(pre), _lib.ptr(gs), None, _lib.ptr(gm), _lib.ptr(G), dt,
+                  _lib.ptr(gb), C, BN, C, 0.9, 1.0, 0.0, 4.0, 4, 0, stream)
+        outs.append((G.cpu(), gb.cpu()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
