@@ -3134,16 +3134,18 @@ void launch_dma_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
 #endif
 
 // mn-contiguous products on 256 x 256 tiles of eight 128 x 64 waves, the
-// K split filling the CUs: when the 128 x 128 tiles alone would fill under
-// one round of 256 CUs (and a workspace allows the split).  Measured beside
-// the 128 x 128 tiles: config 3's dW, 784 x 2048 x 12800 (112 tiles of
-// 128 x 128), 83 -> 63 us; at a full round (config 4's dW, 1024 x 4096 x 3
-// x 7200, 256 tiles) they measured slower, 174 against 182 us, and without
-// a K split far slower.  Splitting to 512 workgroups measured slower than
-// to 256 on both.
+// K split filling the CUs: when the 128 x 128 tiles alone would fill at
+// most one round of 256 CUs (and a workspace allows the split).  Measured
+// beside the 128 x 128 tiles: config 3's dW, 784 x 2048 x 12800 (112 tiles
+// of 128 x 128), 83 -> 63 us; at a full round (config 4's dW, 1024 x 4096
+// x 3 x 7200, 256 tiles) they first measured slower (174 against 182 us),
+// and since the fragment reads run a k step ahead and the loads take
+// offsets from a scalar base, faster: the config 4 step 7.36-7.39 ->
+// 7.18-7.24 ms on one box.  Without a K split they are far slower;
+// splitting to 512 workgroups measured slower than to 256.
 bool use_dma_mn_wide(const GemmArgs &g, int ta, int tb, bool half) {
   return use_dma_mn(g, ta, tb, half) && g.ws != nullptr && g.M >= 256 && g.N >= 256 &&
-         cdiv(g.M, 128) * cdiv(g.N, 128) < 256 && cdiv(g.M, 256) * cdiv(g.N, 256) >= 32;
+         cdiv(g.M, 128) * cdiv(g.N, 128) <= 256 && cdiv(g.M, 256) * cdiv(g.N, 256) >= 32;
 }
 
 void launch_dma_mn_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
