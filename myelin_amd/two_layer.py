@@ -48,11 +48,14 @@ from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _gemm_pa
 
 # trace budget of a backward span (floats per buffer): the backward walks
 # whole checkpoint chunks, as many at a time as keep each per-span buffer
-# within it.  Half the one-layer budget, since this network is the
-# memory-lean route: at T=2000, B=32, 1024 -> 4096 -> 20 with 45-step chunks,
-# spans of 1 / 2 / 5 chunks measured 19.1 / 17.4 / 16.7 ms per training step
-# at 191 / 303 / 654 MB peak (packed variant).
-_SPAN_ELEMS = 1 << 24
+# within it.  At T=2000, B=32, 1024 -> 4096 -> 20 with 45-step chunks
+# (packed variant, the hidden synapse on the exact bf16 split), budgets of
+# 2^24 / 2^25 / 2^26 floats (spans of 2 / 5 / 11 chunks) measured 8.20-8.30
+# / 7.52-7.59 / 7.42 ms per training step at 502 / 870 / 1527 MB peak: a
+# span's recompute GEMM of 2,880 rows fills 1.5 rounds of 256 x 128 tiles,
+# one of 7,200 rows takes 256 x 256 tiles.  2^25, the one-layer budget,
+# keeps the route at half the modules' peak memory.
+_SPAN_ELEMS = 1 << 25
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
