@@ -726,9 +726,9 @@ __global__ __launch_bounds__(256) void gemm_narrow(GemmArgs g) {
 // planes 1 and 2 the same way, each skipped (wave-uniformly) when it is zero
 // in every lane: a 0/1 matrix gives the same bits as words or as floats.
 // For a bit operand that is three bf16 MFMAs per 16 k where the fp32 MFMA
-// takes eight 32x32x2 steps at a sixteenth of the bf16 rate; config 4's
-// readout currents (64000 x 4096 bits x 20) and dW_o measured 243 and 208
-// us on the fp32 MFMA.
+// takes eight 32x32x2 steps at a sixteenth of the bf16 rate; the 4096 -> 20
+// readout's currents at T=2000, B=32 (64000 x 4096 bits x 20) and its dW_o
+// measured 243 and 208 us on the fp32 MFMA.
 struct NarrowB3 {
   static constexpr int KSUB = MYELIN_NARROW_KSUB3, LD = KSUB + 8;
   alignas(16) uint16_t b[3][32][LD];
@@ -3136,12 +3136,13 @@ void launch_dma_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
 // mn-contiguous products on 256 x 256 tiles of eight 128 x 64 waves, the
 // K split filling the CUs: when the 128 x 128 tiles alone would fill at
 // most one round of 256 CUs (and a workspace allows the split).  Measured
-// beside the 128 x 128 tiles: config 3's dW, 784 x 2048 x 12800 (112 tiles
-// of 128 x 128), 83 -> 63 us; at a full round (config 4's dW, 1024 x 4096
+// beside the 128 x 128 tiles: the 784 -> 2048 layer's dW at T=50, B=256,
+// 784 x 2048 x 12800 (112 tiles of 128 x 128), 83 -> 63 us; at a full round
+// (the split dW of the 1024 -> 4096 layer at T=2000, B=32, 1024 x 4096
 // x 3 x 7200, 256 tiles) they first measured slower (174 against 182 us),
 // and since the fragment reads run a k step ahead and the loads take
-// offsets from a scalar base, faster: the config 4 step 7.36-7.39 ->
-// 7.18-7.24 ms on one box.  Without a K split they are far slower;
+// offsets from a scalar base, faster: that network's training step
+// 7.36-7.39 -> 7.18-7.24 ms on one box.  Without a K split they are far slower;
 // splitting to 512 workgroups measured slower than to 256.
 bool use_dma_mn_wide(const GemmArgs &g, int ta, int tb, bool half) {
   return use_dma_mn(g, ta, tb, half) && g.ws != nullptr && g.M >= 256 && g.N >= 256 &&

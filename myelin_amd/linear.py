@@ -280,8 +280,9 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     # stream one chunk ahead of the recurrence, into two alternating
     # currents buffers.  The bf16 engines (and the split) fill the chip with
     # one workgroup per CU, and beside them the recurrence and the GEMM
-    # slow each other down (config 4's step: 7.92-8.01 ms overlapped, 7.53
-    # serial), so they run in turn on the one stream.
+    # slow each other down (the 1024 -> 4096 -> 20 rate network's step at
+    # T=2000, B=32: 7.92-8.01 ms overlapped, 7.53 serial), so they run in
+    # turn on the one stream.
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
     overlap = n > 1 and not half and main.cuda_stream == stream and side.cuda_stream != stream

@@ -357,8 +357,8 @@ def test_parts_products_do_not_depend_on_the_rows_computed(parts, K, N, M):
 
 
 @pytest.mark.parametrize("M,N,K,parts,accumulate", [
-    (1024, 4096, 1440, 3, True),   # a config 4 span dW at one chunk
-    (784, 2048, 2560, 1, False),   # config 3's dW shape: split, it runs on 256 x 256 tiles
+    (1024, 4096, 1440, 3, True),   # the 1024 -> 4096 layer's span dW at one 45-step chunk, B=32
+    (784, 2048, 2560, 1, False),   # the 784 -> 2048 layer's dW shape: split, it runs on 256 x 256 tiles
     (784, 2048, 2600, 3, False),   # the same on three parts, K ending in a partial stage
     (1024, 2048, 1000, 3, True),   # three parts on 256 x 256 tiles, accumulating, partial stage
     (264, 1032, 1000, 3, True),    # ragged tiles, K ending in a partial stage
