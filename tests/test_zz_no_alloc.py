@@ -64,6 +64,37 @@ def test_noalloc_gemm_equals_workspace_gemm_two_calls():
     assert torch.allclose(got, approx, rtol=1e-4, atol=1e-3)
 
 
+def test_noalloc_narrow_output_two_calls():
+    """Narrow outputs (N <= 32, readout currents and their weight gradient)
+    split K into fixed chunks of at most 512 whatever M is; their partial
+    planes go to the static array too."""
+
+    g = torch.Generator().manual_seed(12)
+    f32 = _lib.DT[torch.float32]
+    print("noalloc narrow case 1: fp32 2048 x 20 x 20000", flush=True)
+    M, N, K = 2048, 20, 20000
+    A = torch.randn(M, K, generator=g).to(DEV)
+    B = torch.randn(K, N, generator=g).to(DEV)
+    C0 = torch.full((M, N), float("nan"), device=DEV)
+    got, ref, need = _pair(A, f32, B, f32, None, C0, M, N, K, K, N, 0, 0, 0, _lib.PREC["fp32"])
+    assert 0 < need <= MAX_ELEMS
+    assert torch.equal(got, ref)
+    approx = (A.double() @ B.double()).float()
+    assert torch.allclose(got, approx, rtol=1e-4, atol=1e-3)
+
+    print("noalloc narrow case 2: fp32 300 x 10 x 3000, B stored [N, K], bias, accumulate (smaller)", flush=True)
+    M, N, K = 300, 10, 3000
+    A = torch.randn(M, K, generator=g).to(DEV)
+    B = torch.randn(N, K, generator=g).to(DEV)
+    bias = torch.randn(N, generator=g).to(DEV)
+    C0 = torch.randn(M, N, generator=g).to(DEV)
+    got, ref, need = _pair(A, f32, B, f32, bias, C0, M, N, K, K, K, 0, 1, 1, _lib.PREC["fp32"])
+    assert 0 < need < 2048 * 20 * 40
+    assert torch.equal(got, ref)
+    approx = (C0.double() + A.double() @ B.double().t() + bias.double()).float()
+    assert torch.allclose(got, approx, rtol=1e-4, atol=1e-3)
+
+
 def test_noalloc_gemm_without_split_and_rejection():
     g = torch.Generator().manual_seed(12)
     f32 = _lib.DT[torch.float32]
