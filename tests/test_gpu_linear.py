@@ -534,19 +534,21 @@ def test_gemm_packed_bit_operand_equals_dense(M, N, K, ta, tb, prec):
         assert torch.equal(bits_wide, dense)
 
 
+@pytest.mark.parametrize("K", [4096, 40000])
 @pytest.mark.parametrize("bits", [False, True])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
-def test_narrow_gemm_rows_independent_of_m(bits, prec):
+def test_narrow_gemm_rows_independent_of_m(bits, prec, K):
     """The narrow-output kernel (N <= 32) splits K by K alone, so rows
     computed in a call of their own equal the same rows of one call over all
     of them, bit for bit: a readout's currents do not depend on how its
     caller divides the time steps (all at once, or a group of checkpoint
     chunks at a time).  At fp32 precision it also checks the exact
-    three-plane split against float64."""
+    three-plane split against float64.  K = 40000 takes the cap of 64
+    splits, so each split spans 640 k and ends in a partial sub-chunk."""
 
-    _print_case(test="narrow_rows", bits=bits, prec=prec)
-    M, N, K = 6400, 20, 4096
-    g = seeded(4096 + int(bits) + 2 * (prec == "fp32"))
+    _print_case(test="narrow_rows", bits=bits, prec=prec, K=K)
+    M, N = (6400 if K == 4096 else 3000), 20
+    g = seeded(K + int(bits) + 2 * (prec == "fp32"))
     A = (torch.rand(M, K, generator=g) < 0.1).float()
     W = (torch.rand(K, N, generator=g) - 0.5) / 32
     Ad, Wd = A.to(DEV), W.to(DEV)
@@ -561,7 +563,7 @@ def test_narrow_gemm_rows_independent_of_m(bits, prec):
         return C
 
     full = run(0, M)
-    for r0, r1 in ((0, 2880), (2880, 5760), (5760, M), (17, 18)):
+    for r0, r1 in ((0, M * 9 // 20), (M * 9 // 20, M * 9 // 10), (M * 9 // 10, M), (17, 18)):
         assert torch.equal(run(r0, r1), full[r0:r1]), (r0, r1)
     if prec == "fp32":
         ref = A.double() @ W.double()
