@@ -15,9 +15,9 @@ workload, each with its own throughput, dominant-kernel roofline (HIP events
 around C-ABI launches of that kernel on the launch stream) and a bounded
 CPU baseline (the oracle's restatement of myelin's torch path on the host
 cores):
-  lif_fwd         LIF forward [100, 64, 1024], tau 10, hard reset (8 input
-                  buffers rotated so the 52 MB working set is not served from
-                  the 256 MB Infinity Cache)
+  lif_fwd         LIF forward [100, 64, 1024], tau 10, hard reset (20 input
+                  buffers of 26.2 MB rotated, 524 MB, twice the 256 MB
+                  Infinity Cache, so each launch reads x from HBM)
   linear_bf16     one training step: LinearSurrogateLIF(784 -> 2048,
                   stream_synapse, atan, bf16 GEMM) + LinearSurrogateLIFRate
                   (2048 -> 10, atan, C=25), CE on spike counts, [50, 256, 784]
@@ -29,7 +29,8 @@ cores):
                   layers interleaved per checkpoint chunk, hidden spikes kept
                   bitpacked); reports peak HBM bytes
   bitpack         pack [512, 64, 8192] spikes, unpack, per-neuron counts over
-                  T, per-sample rates
+                  T, per-sample rates (the 33.5 MB packed input of the counts
+                  and rates rotated over 12 copies, 403 MB)
 ``--workload NAME`` prints only that workload's line (``alif_headline``: only
 the headline).
 """
@@ -114,6 +115,25 @@ def _launch_ms(torch, launch, reps: int) -> float:
     return ev0.elapsed_time(ev1) / reps
 
 
+def _launch_ms_median(torch, launch, reps: int, warmup: int = 10) -> float:
+    """Median duration of `launch()` from one HIP event pair per launch on
+    the current stream (the launch stream), after `warmup` untimed launches:
+    the figure a kernel trace's per-dispatch durations give, insensitive to
+    the few launches a clock change catches."""
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+    for i in range(reps):
+        ev[2 * i].record()
+        launch()
+        ev[2 * i + 1].record()
+    torch.cuda.synchronize()
+    d = sorted(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps))
+    return d[reps // 2] if reps % 2 else 0.5 * (d[reps // 2 - 1] + d[reps // 2])
+
+
 def _traffic(name: str, kernel: str):
     """HBM bytes per launch of `kernel` from profiles/traffic_<name>.json
     (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy), or None."""
@@ -165,9 +185,10 @@ def _none(params):
         q.grad = None
 
 
-def _line(metric, value, unit, ms, args, config, **extra):
+def _line(metric, value, unit, ms, args, config, steps=None, warmup=None, **extra):
     out = {
-        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1,
+        "steps": args.steps if steps is None else steps, "warmup": args.warmup if warmup is None else warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic", "config": config,
     }
@@ -327,14 +348,20 @@ def _workload_lif_fwd(torch, myelin, args, threads):
     Tl, Bl, Nl = 100, 64, 1024
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(1)
-    xs_cpu = [0.3 + 0.5 * torch.randn(Tl, Bl, Nl, generator=g) for _ in range(8)]
-    xs = [x.to(dev) for x in xs_cpu]
+    # 20 inputs of 26.2 MB (524 MB) rotated, and as many outputs for the
+    # kernel timing: twice the 256 MB Infinity Cache, so each launch's x
+    # comes from HBM, not from the cache the previous launches filled
+    nrot = 20
+    x0_cpu = 0.3 + 0.5 * torch.randn(Tl, Bl, Nl, generator=g)
+    xs = [x0_cpu.to(dev)]
+    for r in range(1, nrot):
+        xs.append(0.3 + 0.5 * torch.randn(Tl, Bl, Nl, generator=g).to(dev))
     m0 = myelin.LIFState(torch.zeros(Bl, Nl, device=dev))
     p = myelin.LIFParams(10.0, 1.0, 0.0)
     it = [0]
 
     def step():
-        myelin.lif_forward(xs[it[0] % 8], m0, p)
+        myelin.lif_forward(xs[it[0] % nrot], m0, p)
         it[0] += 1
 
     ms = _timed(torch, step, args.steps, args.warmup)
@@ -343,23 +370,24 @@ def _workload_lif_fwd(torch, myelin, args, threads):
 
     stream = _lib.stream(dev)
     m_final = torch.empty(Bl, Nl, device=dev)
-    spikes = torch.empty(Tl, Bl, Nl, device=dev)
+    spikes = [torch.empty(Tl, Bl, Nl, device=dev) for _ in range(nrot)]
     i = [0]
 
     def launch():
-        _lib.call("myelin_lif_fwd_f32", xs[i[0] % 8].data_ptr(), m0.membrane.data_ptr(), m_final.data_ptr(),
-                  spikes.data_ptr(), None, None, Tl, Bl, Nl, p.decay, p.threshold, p.reset, 0.0,
+        k = i[0] % nrot
+        _lib.call("myelin_lif_fwd_f32", xs[k].data_ptr(), m0.membrane.data_ptr(), m_final.data_ptr(),
+                  spikes[k].data_ptr(), None, None, Tl, Bl, Nl, p.decay, p.threshold, p.reset, 0.0,
                   _lib.RULE_THRESHOLD, 1, stream)
         i[0] += 1
 
-    kern_ms = _launch_ms(torch, launch, max(args.steps, 8) * 8)
+    kern_ms = _launch_ms(torch, launch, max(args.steps, nrot) * 4)
     # algorithmic bytes: read x, write spikes (8 B per neuron-step) + m0 in, m_final out
     nbytes = 8 * E + 8 * Bl * Nl
     gbps = nbytes / (kern_ms * 1e-3) / 1e9
     kernel = "fwd_dense<LIF, threshold, V=1, U=32>"
     line = _line("neuron-steps/sec LIF forward", E / (ms * 1e-3), "neuron-steps/s", ms, args,
                  {"workload": "lif_forward, hard reset", "T": Tl, "B": Bl, "N": Nl, "tau_mem": 10.0,
-                  "x": "N(0.3, 0.5)", "rotated_input_buffers": 8},
+                  "x": "N(0.3, 0.5)", "rotated_input_buffers": nrot},
                  roofline={"bound": "hbm", "kernel": kernel, "achieved": gbps, "peak": HBM_PEAK_GBPS,
                            "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
                            "traffic": _traffic("lif_fwd_T100_B64_N1024", "fwd_dense"),
@@ -371,7 +399,7 @@ def _workload_lif_fwd(torch, myelin, args, threads):
 
         def run():
             t0 = time.perf_counter()
-            R.lif_unroll(xs_cpu[0], z, 10.0, 1.0, 0.0)
+            R.lif_unroll(x0_cpu, z, 10.0, 1.0, 0.0)
             return time.perf_counter() - t0
 
         run()
@@ -522,7 +550,10 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(dev)
     base = torch.cuda.memory_allocated(dev)
-    ms = _timed(torch, step, max(1, args.steps // 5), 1)
+    # a step takes ~7 ms: a fifth of the requested steps (at least 4) after
+    # one more warmup step; the line reports the counts actually timed
+    n_steps, n_warm = max(4, args.steps // 5), 1
+    ms = _timed(torch, step, n_steps, n_warm)
     peak_bytes = torch.cuda.max_memory_allocated(dev) - base
     flops = 3 * 2 * Tl * Bl * F * H + 4 * 2 * Tl * Bl * H * O
     tflops = flops / (ms * 1e-3) / 1e12
@@ -551,7 +582,9 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
         _lib.call("myelin_gemm_parts", xb.data_ptr(), w3.data_ptr(), 3, H * F, bh.data_ptr(), cur.data_ptr(), rows,
                   H, F, F, F, H, 0, 1, 0, None, 0, stream)
 
-    kern_ms = _launch_ms(torch, launch, max(args.steps, 10))
+    # median of per-launch HIP event pairs after 10 warmup launches, the
+    # same in both config-4 workloads
+    kern_ms = _launch_ms_median(torch, launch, 41)
     k_flops = 3 * 2 * rows * H * F
     k_tflops = k_flops / (kern_ms * 1e-3) / 1e12
     name = ("two_layer_surrogate_lif_rate_packed_hidden_forward(1024->4096->20, checkpoint 'memory'=45, "
@@ -561,6 +594,7 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
     line = _line("neuron-steps/sec, long-horizon checkpointed rate training step", E / (ms * 1e-3),
                  "neuron-steps/s", ms, args,
                  {"workload": name, "T": Tl, "B": Bl, "F": F, "N": H, "readout": O, "gflop_per_step": flops / 1e9},
+                 steps=n_steps, warmup=n_warm + 1,
                  roofline={"bound": "mfma",
                            "kernel": "gemm_dma<256 x 256 tiles, 3 bf16 parts> (one forward chunk of the exact "
                                      "bf16 split of the fp32 synapse, 8192 x 4096 x 3*1024)",
@@ -586,11 +620,13 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
             torch.nn.functional.cross_entropy(r * Tl, labels_cpu[:sb]).backward()
             return time.perf_counter() - t0
 
+        run()  # warmup, excluded (baselines.py:72-100 times after warmup runs)
         dt, n, tot = _cpu_mean(run, args.cpu_min_seconds / 3, max_runs=5)
         line["cpu_baseline"] = {
             "value": Tl * sb * H / dt, "unit": "neuron-steps/s", **threads, "kind": "port",
             "sample": f"oracle torch_ref checkpoint + checkpoint-rate Functions (C={C}), one training step on B={sb} "
-                      f"of {Bl} rows at full T/F/N/readout, mean of {n} runs ({tot:.1f} s total), no warmup run"}
+                      f"of {Bl} rows at full T/F/N/readout, mean of {n} runs ({tot:.1f} s total) after one warmup "
+                      f"run"}
     return line
 
 
@@ -604,10 +640,24 @@ def _workload_bitpack(torch, myelin, args, threads):
     s = s_cpu.to(dev)
     pk = myelin.pack_spikes(s)
     E = Tl * Bl * Nl
+    # the counts and rates read only the 33.5 MB of words: 12 copies (403 MB)
+    # rotated, so each call reads them from HBM rather than from the 256 MB
+    # Infinity Cache (pack and unpack move 1.1 GB per call, beyond it)
+    nrot = 12
+    pks = [pk] + [myelin.PackedSpikes(pk.data.clone(), pk.original_shape) for _ in range(nrot - 1)]
+    it = [0]
+
+    def rotated(fn):
+        def call():
+            fn(pks[it[0] % nrot])
+            it[0] += 1
+
+        return call
+
     times = {}
     for name, fn in (("pack", lambda: myelin.pack_spikes(s)), ("unpack", lambda: myelin.unpack_spikes(pk)),
-                     ("count_dim0", lambda: myelin.packed_spike_count(pk, dim=0)),
-                     ("rate_dim0_last", lambda: myelin.packed_spike_rate(pk, dim=(0, -1)))):
+                     ("count_dim0", rotated(lambda q: myelin.packed_spike_count(q, dim=0))),
+                     ("rate_dim0_last", rotated(lambda q: myelin.packed_spike_rate(q, dim=(0, -1))))):
         times[name] = _timed(torch, fn, args.steps, args.warmup)
     ms = sum(times.values())
     from myelin_amd import _lib
@@ -633,7 +683,8 @@ def _workload_bitpack(torch, myelin, args, threads):
                  kernels={**{f"{k}_ms": v for k, v in times.items()}, **{f"{k}_GBps": v for k, v in gbps.items()},
                           "pack_kernel_ms": k_pack, "unpack_kernel_ms": k_unpack,
                           "unpack_kernel_GBps": byte_model["unpack"] / (k_unpack * 1e-3) / 1e9},
-                 dtype="u8")
+                 dtype="i32", dtypes={"spikes": "f32", "words": "i32", "counts": "i64", "rates": "f32"},
+                 rotated_word_buffers=nrot)
     if not args.no_cpu_baseline:
         R = _oracle()
         ts = 64

@@ -69,7 +69,8 @@ typedef struct ihipStream_t *myelin_stream_t;
  * (functional.py:115-189): per step, dL/ds = ((dL/ds_t + dL/da' +
  * dL/dm'' * reset) - dL/dm'' * m'), then the primitive's own backward
  * formulas (quotient rule for fast_sigmoid / superspike, sigmoid_backward,
- * atan's 1/(1+p^2), clamp mask, erf's 2/sqrt(pi)*exp(-z^2)).  Chunk 16 only.
+ * atan's 1/(1+p^2), clamp mask, erf's 2/sqrt(pi)*exp(-z^2)).  Chunk 16 only
+ * (chunk 8 rejects both codes with MYELIN_EINVAL).
  * The other codes (0-6) use the closed-form derivative sigma'(c) of
  * surrogates.py:78-102, as the reference's Triton kernels do
  * (triton/lif.py:225-249) with exact 0/1 spikes. */
@@ -268,7 +269,9 @@ int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K,
  * C (+)= sum over p < parts (1..8) of op(A) op(B_p) (+ bias), B_p = B +
  * p*b_part, all bf16 operands (alignment as myelin_gemm's bf16 operands,
  * for every part) on the bf16 MFMA engines; each part's k range is summed
- * in turn into the same fp32 accumulators.  With A exactly
+ * in turn into the same fp32 accumulators, from the last part to the first
+ * (for the planes of myelin_split_bf16x3, smallest first: only the largest
+ * plane's products round against the full-size sum).  With A exactly
  * representable in bf16 (spikes) and B_p the three planes of
  * myelin_split_bf16x3, every product is exact and the result is an fp32
  * GEMM of the unsplit B to fp32 summation accuracy, at bf16 MFMA rate.

@@ -35,6 +35,15 @@ __device__ __forceinline__ float recip_rn(float b) {
   return __builtin_fmaf(__builtin_fmaf(-b, r, 1.0f), r, r);
 }
 
+// recip_rn for a divisor that may overflow to +inf (a squared 1 + |c|):
+// there the Newton step would form inf * 0 = NaN, and IEEE division gives
+// 0.  Finite divisors past 2^126 have a subnormal reciprocal, returned as 0
+// or that subnormal (never NaN).
+__device__ __forceinline__ float recip_rn_or_zero(float b) {
+  const float y = recip_rn(b);
+  return b < __builtin_huge_valf() ? y : 0.0f;
+}
+
 // x / b from y = recip_rn(b): q0 = x*y, e = x - b*q0 (exact in an fma),
 // q = q0 + e*y rounded once.  With y within half an ulp of 1/b and q0
 // within one ulp of x/b this is x/b rounded to nearest (Markstein's

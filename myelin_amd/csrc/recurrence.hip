@@ -511,16 +511,16 @@ __device__ __forceinline__ float sg_deriv(float c) {
   } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
     // 0.5 / d^2 = 0.5 * (1 / d^2), both rounded once (a power of two)
     float d = 1.0f + fabsf(c);
-    return 0.5f * myelin::recip_rn(d * d);
+    return 0.5f * myelin::recip_rn_or_zero(d * d);
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     float s = 1.5707963267948966f * c;
-    return 0.5f * myelin::recip_rn(1.0f + s * s);
+    return 0.5f * myelin::recip_rn_or_zero(1.0f + s * s);
   } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
     float sg = (c > 0.0f) ? 1.0f : ((c < 0.0f) ? -1.0f : 0.0f);
     return fabsf(c) < 1.0f ? -sg : 0.0f;
   } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
     float d = 1.0f + fabsf(c);
-    return myelin::recip_rn(d * d);
+    return myelin::recip_rn_or_zero(d * d);
   } else if constexpr (SID == MYELIN_SG_NONE) {
     return 0.0f;
   } else {
@@ -970,7 +970,9 @@ int launch_bwd_c(const BwdArgs &a, int code, hipStream_t stream) {
 #define MYELIN_BWD_CASES(SID)                                                                          \
   case SID: return launch_bwd_sid<ALIF, C, SID, 0>(a, stream);                                       \
   case MYELIN_SG_AUTOGRAD + SID:                                                                       \
-    return launch_bwd_sid<ALIF, C, SID, MYELIN_RULE_STRAIGHT_THROUGH + SID>(a, stream);                \
+    if constexpr (C == 16)                                                                             \
+      return launch_bwd_sid<ALIF, C, SID, MYELIN_RULE_STRAIGHT_THROUGH + SID>(a, stream);              \
+    break;                                                                                             \
   case MYELIN_SG_AUTOGRAD_SMOOTH + SID:                                                                \
     if constexpr (C == 16) return launch_bwd_sid<ALIF, C, SID, MYELIN_RULE_SMOOTH + SID>(a, stream);   \
     break;
@@ -984,7 +986,7 @@ int launch_bwd_c(const BwdArgs &a, int code, hipStream_t stream) {
     case MYELIN_SG_NONE: return launch_bwd_sid<ALIF, C, MYELIN_SG_NONE, 0>(a, stream);
     default: return myelin::invalid("unknown surrogate code %d", code);
   }
-  return myelin::invalid("surrogate code %d (smooth forward) needs chunk 16; got %d", code, C);
+  return myelin::invalid("surrogate code %d (autograd order) needs chunk 16; got %d", code, C);
 }
 
 template <bool ALIF>

@@ -335,7 +335,8 @@ struct GemmArgs {
   int64_t M, N, K, lda, ldb, ldc, kchunk;
   int accumulate, splits;
   // bf16 operands on the 128 x 128 kernel only: C (+)= sum over p < parts of
-  // op(A) op(B + p * b_part), each part's k range summed in turn
+  // op(A) op(B + p * b_part), each part's k range summed in turn (B points
+  // at the first part summed; b_part may be negative)
   int parts = 1;
   int64_t b_part = 0;
 };
@@ -678,9 +679,12 @@ __global__ __launch_bounds__(256) void gemm_narrow(GemmArgs g) {
   const int kh = (lane >> 5) * KG;
   const int N = static_cast<int>(g.N);
 
-  f32x16 acc;
+  f32x16 acc, acc_s;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int r = 0; r < 16; ++r) {
+    acc[r] = 0.0f;
+    acc_s[r] = 0.0f;
+  }
 
   for (int64_t ks = kb; ks < ke; ks += KSUB) {
     const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
@@ -721,10 +725,15 @@ __global__ __launch_bounds__(256) void gemm_narrow(GemmArgs g) {
 // B's staged sub-chunk is split into three bf16 planes (split3: hi + mid +
 // lo == B), and A is packed spike bits (one plane of 0/1 values) or fp32
 // values split the same way as they are loaded.  A product of two bf16
-// values is exact in fp32, so only the fp32 accumulation rounds.  Per group
-// of 16 k the accumulator takes A plane 0 times B planes 0, 1, 2, then A
-// planes 1 and 2 the same way, each skipped (wave-uniformly) when it is zero
-// in every lane: a 0/1 matrix gives the same bits as words or as floats.
+// values is exact in fp32, so only the fp32 accumulation rounds.  Two
+// accumulators: one takes the products of the high planes of A and B, the
+// other every smaller product (A planes 2 and 1 times B planes 2, 1, 0,
+// then A plane 0 times B planes 2 and 1, each A plane skipped wave-uniformly
+// when it is zero in every lane: a 0/1 matrix gives the same bits as words
+// or as floats), and they are added once at the end.  Only the high-plane
+// products then round against the full-size sum, as in a plain fp32 GEMM;
+// in one accumulator every plane's products did (the 4096 -> 20 readout's
+// currents and weight gradient lost up to 3x the accuracy of an fp32 GEMM).
 // For a bit operand that is three bf16 MFMAs per 16 k where the fp32 MFMA
 // takes eight 32x32x2 steps at a sixteenth of the bf16 rate; the 4096 -> 20
 // readout's currents at T=2000, B=32 (64000 x 4096 bits x 20) and its dW_o
@@ -738,7 +747,7 @@ __device__ __forceinline__ bf16x8 bf16_frag(const uint16_t *p) { return *reinter
 
 template <bool PA>
 __device__ __forceinline__ void group_x3(const float (&a)[8], const uint16_t *b0, const uint16_t *b1,
-                                         const uint16_t *b2, f32x16 &acc) {
+                                         const uint16_t *b2, f32x16 &acc, f32x16 &acc_s) {
   const bf16x8 v0 = bf16_frag(b0), v1 = bf16_frag(b1), v2 = bf16_frag(b2);
   bf16x8 ap[3];
   bool nz1 = false, nz2 = false;
@@ -756,21 +765,23 @@ __device__ __forceinline__ void group_x3(const float (&a)[8], const uint16_t *b0
       nz2 = nz2 || (l & 0x7fffu) != 0;
     }
   }
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v0, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v1, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v2, acc, 0, 0, 0);
+  // the smaller products, smallest planes first, into acc_s
   if constexpr (!PA) {
-    if (__ballot(nz1) != 0) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v1, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v2, acc, 0, 0, 0);
-    }
     if (__ballot(nz2) != 0) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v1, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v2, acc, 0, 0, 0);
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v2, acc_s, 0, 0, 0);
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v1, acc_s, 0, 0, 0);
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2], v0, acc_s, 0, 0, 0);
+    }
+    if (__ballot(nz1) != 0) {
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v2, acc_s, 0, 0, 0);
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v1, acc_s, 0, 0, 0);
+      acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1], v0, acc_s, 0, 0, 0);
     }
   }
+  acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v2, acc_s, 0, 0, 0);
+  acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v1, acc_s, 0, 0, 0);
+  // the largest (high planes of both operands) into acc
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0], v0, acc, 0, 0, 0);
 }
 
 // Same workgroup shape, K split and A streaming as gemm_narrow<1>.
@@ -788,9 +799,12 @@ __global__ __launch_bounds__(256) void gemm_narrow_x3(GemmArgs g) {
   const int kh = (lane >> 5) * KG;
   const int N = static_cast<int>(g.N);
 
-  f32x16 acc;
+  f32x16 acc, acc_s;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int r = 0; r < 16; ++r) {
+    acc[r] = 0.0f;
+    acc_s[r] = 0.0f;
+  }
 
   for (int64_t ks = kb; ks < ke; ks += KSUB) {
     const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
@@ -821,16 +835,18 @@ __global__ __launch_bounds__(256) void gemm_narrow_x3(GemmArgs g) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int o = (bi * U + u) * GS;
-        group_x3<PA>(a[u], b0 + o, b1 + o, b2 + o, acc);
+        group_x3<PA>(a[u], b0 + o, b1 + o, b2 + o, acc, acc_s);
       }
     }
     for (int j = nfull * U; j < ng; ++j) {
       float t[KG];
       load_group<1, TA, PA, VA, false>(g, m, ks + j * GS + kh, ke, t);
-      group_x3<PA>(t, b0 + j * GS, b1 + j * GS, b2 + j * GS, acc);
+      group_x3<PA>(t, b0 + j * GS, b1 + j * GS, b2 + j * GS, acc, acc_s);
     }
   }
   if (!wave_on) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = acc[r] + acc_s[r];
   store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
 }
 
@@ -871,9 +887,12 @@ __global__ __launch_bounds__(64 * NarrowBits<NP>::WAVES) void gemm_narrow_bits(G
   const int N = static_cast<int>(g.N);
   const int32_t *arow = static_cast<const int32_t *>(g.A) + m * g.lda;
 
-  f32x16 acc;
+  f32x16 acc, acc_s;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int r = 0; r < 16; ++r) {
+    acc[r] = 0.0f;
+    acc_s[r] = 0.0f;
+  }
 
   for (int64_t ks = kb; ks < ke; ks += KSUB) {
     const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
@@ -901,13 +920,20 @@ __global__ __launch_bounds__(64 * NarrowBits<NP>::WAVES) void gemm_narrow_bits(G
                        bf16_pair_of_bits(wv >> 6)};
       const bf16x8 av = __builtin_bit_cast(bf16x8, d);
       const int o = j * GS + kh;
+      // as gemm_narrow_x3: B planes 2 and 1 into acc_s, plane 0 into acc
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, *reinterpret_cast<const bf16x8 *>(&sb.b[p][lane & 31][o]),
-                                                      acc, 0, 0, 0);
+      for (int p = NP - 1; p > 0; --p)
+        acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            av, *reinterpret_cast<const bf16x8 *>(&sb.b[p][lane & 31][o]), acc_s, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, *reinterpret_cast<const bf16x8 *>(&sb.b[0][lane & 31][o]),
+                                                    acc, 0, 0, 0);
     }
   }
   if (!wave_on) return;
+  if constexpr (NP > 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = acc[r] + acc_s[r];
+  }
   store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
 }
 
@@ -2088,16 +2114,16 @@ __device__ __forceinline__ float sg_deriv(float c) {
   } else if constexpr (SID == MYELIN_SG_FAST_SIGMOID) {
     // 0.5 / d^2 = 0.5 * (1 / d^2), both rounded once (a power of two)
     float d = 1.0f + fabsf(c);
-    return 0.5f * myelin::recip_rn(d * d);
+    return 0.5f * myelin::recip_rn_or_zero(d * d);
   } else if constexpr (SID == MYELIN_SG_ATAN) {
     float s = 1.5707963267948966f * c;
-    return 0.5f * myelin::recip_rn(1.0f + s * s);
+    return 0.5f * myelin::recip_rn_or_zero(1.0f + s * s);
   } else if constexpr (SID == MYELIN_SG_TRIANGULAR) {
     float sg = (c > 0.0f) ? 1.0f : ((c < 0.0f) ? -1.0f : 0.0f);
     return fabsf(c) < 1.0f ? -sg : 0.0f;
   } else if constexpr (SID == MYELIN_SG_SUPERSPIKE) {
     float d = 1.0f + fabsf(c);
-    return myelin::recip_rn(d * d);
+    return myelin::recip_rn_or_zero(d * d);
   } else {
     float z = c / 0.5f, r = c - 1.0f, l = c + 1.0f;
     return 0.47873073648171924f * expf(-0.5f * z * z) + 0.07978845608028655f * expf(-0.5f * r * r) +
@@ -2854,9 +2880,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   }
 }
 
-// out[n] (+)= sum_r in[r, n].  A block of 16 waves takes 64 columns; wave
-// q sums rows q, q+16, ... of its column, then wave 0 adds the 16 partials
-// in wave order (fixed order: deterministic).
+// out[n] (+)= sum_r in[r, n], in a fixed order (deterministic).
 // 8 columns per workgroup (a 2048-column sum spreads over 256 CUs): thread
 // (column c = tid % 8, group q = tid / 8) sums rows q, q + 32, ... in order,
 // then the 32 group sums are added in group order
@@ -3203,8 +3227,6 @@ void launch_big_t(const GemmArgs &g, int ta, int tb, bool half, dim3 grid, hipSt
     launch_big<PREC, true, true, BM, BN>(g, half, grid, s);
 }
 
-// K splits of the narrow kernel: only as many as bring the grid to about
-// 1024 workgroups (each split costs a partial [M, N] in the workspace).
 // K splits of the narrow kernel: chunks of about MYELIN_NARROW_KCHUNK k (at
 // most 64 of them), a function of K alone.  Each output element then sums
 // the same k ranges in the same order whatever M is, so a layer's currents
@@ -3572,9 +3594,18 @@ extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts
   if (!bf16_aligned(A, lda, !trans_a) || !bf16_aligned(B, ldb, trans_b != 0) ||
       (parts > 1 && !bf16_aligned(B + b_part, ldb, trans_b != 0)))
     return myelin::invalid("gemm_parts: bfloat16 operand rows must be 16-byte (k-contiguous) or 8-byte aligned");
-  GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
+  // The parts are summed from the last to the first: for the planes of an
+  // exact split (largest first in memory) the smallest plane's products
+  // then accumulate while the running sum is small, and only the largest
+  // plane's products round against the full-size sum, as in a plain fp32
+  // GEMM.  Summed largest first, each of the three planes' products rounds
+  // against the full sum: config 4's currents [8000 x 4096 x 1024] measured
+  // 5.3e-7 (max) / 2.9e-8 (rms) from float64 that way, 6.8e-8 / 6.1e-9 this
+  // way (a CPU sgemm: 1.5e-7 / 1.3e-8).
+  GemmArgs g{A, B + (parts - 1) * b_part, bias, C, workspace_elems > 0 ? workspace : nullptr,
+             M, N, K, lda, ldb, ldc, 0, accumulate, 1};
   g.parts = parts;
-  g.b_part = b_part;
+  g.b_part = -b_part;
   hipStream_t s = myelin::as_hip(stream);
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;

@@ -38,6 +38,11 @@ see ``tests/test_oracle_*.py``):
   against autograd through an explicit ``matmul`` + ``surrogate_lif_unroll``
   composition, ``rate == spikes.mean(0)`` (``tests/test_modules.py:892-936``),
   and golden vectors from the reference.
+* ``linear_rate_adjoint_f64`` -- equal (to float64 rounding) to the
+  checkpoint and rate Functions above run on float64 tensors, where those
+  derive the same rasters themselves, with and without biases, for several
+  surrogates; a raster or an injected gradient changed by one entry moves
+  its result.
 """
 
 from __future__ import annotations
@@ -706,6 +711,86 @@ def linear_surrogate_lif_rate(
         x, w, b, tau, threshold, reset, surrogate, slope, checkpoint_size, True
     )
     return m, (rates.mean() if reduction == "mean" else rates)
+
+
+def linear_rate_adjoint_f64(x, wh, bh, wo, bo, decay, threshold, reset, surrogate, slope, hidden_spikes,
+                            readout_spikes, grad_rates):
+    """Float64 gradients of a checkpointed hidden layer feeding a rate readout,
+    on a float64 forward whose spikes are the given rasters.
+
+    The backward is that of ``LinearSurrogateLIFCheckpointFunction``
+    (autograd.py:629-666: ``gp = gm((1 - s) + (r - m')d) + g_out_t d``,
+    ``gx_t = gp W^T``, ``dW += x_t^T gp``, ``db += sum gp``, ``gm = gp decay``)
+    and of the rate Function (autograd.py:842-875: the injected gradient is
+    ``g_rates / T`` every step), with the readout's input gradient fed to the
+    hidden layer as its ``g_out``.  Every value is a float64 tensor and every
+    product is formed in float64; ``decay`` is passed in (pass the fp32 value
+    an fp32 forward multiplies by, ``float(numpy.float32(d))``, to measure an
+    fp32 evaluation against it).  The spikes are not re-derived from the
+    float64 membranes: they are the fp32 run's own rasters, so this is the
+    exact gradient of the network on that run's spike pattern, which every
+    fp32 evaluation of it approximates.
+
+    x ``[T, B, F]``, wh ``[F, H]``, wo ``[H, O]``, biases or None, rasters
+    ``[T, B, H]`` / ``[T, B, O]`` (``readout_spikes`` None: the readout's
+    spikes follow from its float64 membranes), grad_rates ``[B, O]``.
+    Returns a dict of float64 tensors: gx, gwh, gbh, gwo, gbo, g_hidden (the
+    readout's gradient into the hidden spikes), pre_hidden (the hidden
+    layer's pre-reset membranes) and readout_spikes.
+    """
+
+    f64 = torch.float64
+    T, B = x.shape[:2]
+    xd = x.to(f64)
+    sh = hidden_spikes.to(f64)
+
+    def membranes(inp, w, b, s):
+        """Pre-reset membranes; with s None the spikes are derived from them
+        (m' >= threshold) and returned too."""
+
+        cur = (inp.reshape(T * B, -1) @ w.to(f64)).reshape(T, B, -1)
+        if b is not None:
+            cur = cur + b.to(f64)
+        m = torch.zeros(B, w.shape[1], dtype=f64)
+        pres = torch.empty(T, B, w.shape[1], dtype=f64)
+        derive = s is None
+        if derive:
+            s = torch.empty_like(pres)
+        for t in range(T):
+            m = m * decay + cur[t]
+            pres[t] = m
+            if derive:
+                s[t] = (m >= threshold).to(f64)
+            m = m * (1.0 - s[t]) + reset * s[t]
+        return pres, s
+
+    def reverse(pres, s, g_in, g_step):
+        gm = torch.zeros_like(pres[0])
+        gps = torch.empty_like(pres)
+        for t in range(T - 1, -1, -1):
+            pre = pres[t]
+            d = slope * surrogate_derivative(surrogate, slope * (pre - threshold))
+            gp = gm * ((1.0 - s[t]) + (reset - pre) * d)
+            gp = gp + (g_step if g_in is None else g_in[t]) * d
+            gps[t] = gp
+            gm = gp * decay
+        return gps.reshape(T * B, -1)
+
+    pres_o, so = membranes(sh, wo, bo, None if readout_spikes is None else readout_spikes.to(f64))
+    gp_o = reverse(pres_o, so, None, grad_rates.to(f64) / T)
+    g_hidden = (gp_o @ wo.to(f64).t()).reshape(T, B, -1)
+    pres_h, _ = membranes(xd, wh, bh, sh)
+    gp_h = reverse(pres_h, sh, g_hidden, None)
+    return {
+        "pre_hidden": pres_h,
+        "readout_spikes": so,
+        "gx": (gp_h @ wh.to(f64).t()).reshape(x.shape),
+        "g_hidden": g_hidden,
+        "gwh": xd.reshape(T * B, -1).t() @ gp_h,
+        "gbh": gp_h.sum(0) if bh is not None else None,
+        "gwo": sh.reshape(T * B, -1).t() @ gp_o,
+        "gbo": gp_o.sum(0) if bo is not None else None,
+    }
 
 
 def two_layer_rate(x, wh, bh, wo, bo, tau, threshold, reset, surrogate="fast_sigmoid", slope=5.0,

@@ -31,6 +31,11 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture(scope="session", autouse=True)
 def _oracle_built():
     from oracle import c_ref
+    from tests.hip import build as test_kernels
 
     c_ref.build()
+    # the test-only HIP kernels (tests/hip/*.hip) are built here when absent,
+    # so a fresh checkout needs only `python -m myelin_amd.build`
+    if not test_kernels.LIB.exists():
+        test_kernels.build()
     yield

@@ -71,3 +71,34 @@ def assert_same_bits(a, b, what: str = "") -> None:
     idx = tuple(bad[0].tolist())
     raise AssertionError(f"{what}: {bad.shape[0]} of {a_t.numel()} elements differ; first at {idx}: "
                          f"{a_t[idx].item()!r} vs {b_t[idx].item()!r} (max rel {norm_rel_err(a_t, b_t):.2e})")
+
+
+def f32_params(tau: float, *scalars: float) -> tuple[float, ...]:
+    """(tau', s1', ...) for evaluating an fp32 network in float64: every
+    scalar rounded to the fp32 value an fp32 evaluation multiplies or
+    compares by, and tau' such that the float64 decay 1 - 1/tau' is the
+    fp32-rounded decay of tau (to float64 rounding)."""
+
+    d32 = float(np.float32(1.0 - 1.0 / tau))
+    return (1.0 / (1.0 - d32), *(float(np.float32(s)) for s in scalars))
+
+
+def assert_elementwise_close_or_truer(a, b, truth, rtol: float, what: str = "", floor: float = 1e-3) -> None:
+    """Per element, a within `rtol` of the reference value b (relative,
+    floored at `floor` of max|b|) -- or a no farther from the float64 value
+    `truth` than b itself is, where two fp32 evaluations differ by more
+    than that at elements far below the tensor's largest."""
+
+    a = to_np(a).astype(np.float64)
+    b = to_np(b).astype(np.float64)
+    t = to_np(truth).astype(np.float64)
+    if b.size == 0:
+        return
+    top = np.abs(b).max()
+    scale = np.maximum(np.abs(b), floor * top) if top > 0 else np.ones_like(b)
+    close = np.abs(a - b) <= rtol * scale
+    truer = np.abs(a - t) <= np.abs(b - t)
+    bad = ~(close | truer)
+    assert not bad.any(), (
+        f"{what}: {int(bad.sum())} elements neither within {rtol:.1e} of the reference nor as close as it to "
+        f"float64; worst |a-b|/scale = {float((np.abs(a - b) / scale).max()):.3e}")

@@ -63,10 +63,13 @@ def test_autograd_order_codes_are_validated_without_launching():
     with pytest.raises(ValueError, match="unknown surrogate code 22"):
         _lib.call("myelin_lif_bwd_f32", 1, 1, None, None, 1, 1, 4, 4, 0.9, 1.0, 0.0, 10.0,
                   _lib.SG_AUTOGRAD + _lib.SG_NONE, 16, None)
-    # the smooth-forward backward is built at chunk 16 only
-    with pytest.raises(ValueError, match="needs chunk 16"):
-        _lib.call("myelin_alif_bwd_f32", 1, 1, 1, None, None, None, 1, 1, 1, 4, 4, 0.9, 0.9, 1.0, 1.8, 0.0,
-                  10.0, _lib.SG_AUTOGRAD_SMOOTH + 1, 8, None)
+    # the autograd-order backwards are built at chunk 16 only
+    for code in (_lib.SG_AUTOGRAD_SMOOTH + 1, _lib.SG_AUTOGRAD + 1):
+        with pytest.raises(ValueError, match="needs chunk 16"):
+            _lib.call("myelin_alif_bwd_f32", 1, 1, 1, None, None, None, 1, 1, 1, 4, 4, 0.9, 0.9, 1.0, 1.8, 0.0,
+                      10.0, code, 8, None)
+        with pytest.raises(ValueError, match="needs chunk 16"):
+            _lib.call("myelin_lif_bwd_f32", 1, 1, None, None, 1, 1, 4, 4, 0.9, 1.0, 0.0, 10.0, code, 8, None)
 
 
 def test_error_message_is_per_thread():

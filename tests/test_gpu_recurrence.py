@@ -171,6 +171,27 @@ def test_surrogate_lif_matches_oracles(surrogate, T, B, N):
                             thr=0.7, reset=-0.2, beta=0.0, slope=4.0)
 
 
+@pytest.mark.parametrize("surrogate", ["fast_sigmoid", "superspike", "atan"])
+def test_closed_form_backward_of_huge_membrane(surrogate):
+    """A membrane of 1e20 makes (1 + |c|)^2 overflow: sigma'(c) is 0 there,
+    as in torch and the C oracle, not NaN; the other neuron is unaffected."""
+
+    _print_case(test="closed_form_huge_membrane", surrogate=surrogate)
+    x = torch.tensor([[[1e20, 0.5, 0.9]], [[0.0, 0.7, 0.2]], [[0.3, 0.1, 0.8]]])
+    m0 = torch.zeros(1, 3)
+    gs = torch.ones_like(x)
+    xd = x.to(DEV).requires_grad_()
+    _, s = myelin.surrogate_lif_forward(xd, myelin.LIFState(m0.to(DEV)), myelin.LIFParams(20.0, 1.0, 0.0),
+                                        surrogate=surrogate, surrogate_slope=10.0)
+    s.backward(gs.to(DEV))
+    gx, _ = c_ref.lif_bwd(x.numpy(), m0.numpy(), gs.numpy(), np.zeros((1, 3), np.float32),
+                          np.float32(R.decay_from_tau(20.0)), 1.0, 0.0, 10.0, surrogate)
+    got = to_np(xd.grad)
+    assert np.isfinite(got).all()
+    assert got[0, 0, 0] == 0.0 and gx[0, 0, 0] == 0.0
+    assert_norm_close(got, gx, 1e-6, "grad_x")
+
+
 @pytest.mark.parametrize("surrogate", R.SURROGATE_NAMES)
 @pytest.mark.parametrize("T,B,N", [(4, 2, 5), (50, 3, 129)])
 def test_surrogate_alif_matches_oracles(surrogate, T, B, N):

@@ -4,10 +4,11 @@ packed-hidden variants, kernels.py:779-846).
 Bars (as for the one-layer linear paths): readout rates equal to the
 reference's when the rasters agree (rates are counts / T), gradients within
 1e-5 max-norm relative of the reference's and of the oracle's (measured <=
-1.4e-6) and, against the reference's golden vectors, within 2e-4 per
-element, |a - b| <= 2e-4 * max(|b|, 1e-3 max|b|) (measured <= 8.4e-5: the
-MFMA GEMMs sum in another order than the CPU matmul, and the reference's
-spikes (H + sigma) - sigma can sit an ulp below 1).  The packed
+1.4e-6) and, against the reference's golden vectors, per element within
+2e-4, |a - b| <= 2e-4 * max(|b|, 1e-3 max|b|), or no farther from the
+float64 evaluation of the same network than the golden value is (the MFMA
+GEMMs sum in another order than the CPU matmul, and the reference's spikes
+(H + sigma) - sigma can sit an ulp below 1).  The packed
 variant's readout GEMMs read the hidden spikes as packed bits; for readouts
 narrower than 128 neurons both variants run the same GEMM kernel and K
 split, so they must agree bit for bit (wider: within 1e-5).
@@ -23,7 +24,8 @@ import torch
 
 import myelin_amd as myelin
 from oracle import torch_ref as R
-from tests.helpers import assert_elementwise_close, assert_norm_close, raster_agreement, seeded, to_np
+from tests.helpers import (assert_elementwise_close_or_truer, assert_norm_close, f32_params, raster_agreement, seeded,
+                           to_np)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -64,10 +66,26 @@ def test_two_layer_matches_reference(variant, bias, ck, sg):
     tag = f"{'b' if bias else 'nob'}_c{ck}_{sg}"
     assert np.array_equal(to_np(r), TWO[f"{tag}_r"])
     gx, gwh, gbh, gwo, gbo = _grads(leaves)
+    truth = _truth64(tensors, bias, p, sg, ck, TWO["grate"], TWO[f"{tag}_r"])
     pairs = [(gx, "gx"), (gwh, "gwh"), (gwo, "gwo")] + ([(gbh, "gbh"), (gbo, "gbo")] if bias else [])
     for got, name in pairs:
         assert_norm_close(got, TWO[f"{tag}_{name}"], 1e-5, name)
-        assert_elementwise_close(got, TWO[f"{tag}_{name}"], 2e-4, name)
+        assert_elementwise_close_or_truer(got, TWO[f"{tag}_{name}"], truth[name], 2e-4, name)
+
+
+def _truth64(tensors, bias, p, sg, ck, grate, rates):
+    """The oracle network in float64 on the golden inputs (every scalar at
+    its fp32 value); its rates must equal the golden ones."""
+
+    x, wh, bh, wo, bo = (t.double().requires_grad_() for t in tensors)
+    if not bias:
+        bh = bo = None
+    tau, thr, rst = f32_params(p.tau_mem, p.threshold, p.reset)
+    r = R.two_layer_rate(x, wh, bh, wo, bo, tau, thr, rst, sg, 5.0, ck)
+    assert np.array_equal(to_np(r.float()), rates), "float64 rates differ from the golden ones"
+    r.backward(torch.from_numpy(grate).double())
+    return {"gx": x.grad, "gwh": wh.grad, "gwo": wo.grad, "gbh": None if bh is None else bh.grad,
+            "gbo": None if bo is None else bo.grad}
 
 
 def _random_net(seed, T, B, F, H, O):

@@ -301,6 +301,75 @@ def test_rate_gradient_matches_spike_gradient_with_uniform_weights():
     assert_norm_close(wr.grad, ws.grad, 1e-6, "grad_w")
 
 
+def _two_layer_f64_case(seed, bias, T=40, B=3, F=13, H=19, O=5):
+    g = seeded(seed)
+    x = (torch.rand(T, B, F, generator=g) < 0.3).double()
+    wh = ((torch.rand(F, H, generator=g) - 0.5) * 1.2).double()
+    wo = ((torch.rand(H, O, generator=g) - 0.5) * 1.2).double()
+    bh = (torch.rand(H, generator=g) * 0.2).double() if bias else None
+    bo = (torch.rand(O, generator=g) * 0.2).double() if bias else None
+    labels = torch.randint(0, O, (B,), generator=g)
+    return x, wh, bh, wo, bo, labels
+
+
+@pytest.mark.parametrize("surrogate", ["superspike", "atan", "fast_sigmoid"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_linear_rate_adjoint_f64_matches_float64_functions(surrogate, bias):
+    """linear_rate_adjoint_f64 (one float64 pass over given rasters) against
+    the checkpoint and rate Functions run on float64 tensors, which derive
+    the rasters from their own float64 membranes and recompute per chunk."""
+
+    x, wh, bh, wo, bo, labels = _two_layer_f64_case(21, bias)
+    T = x.shape[0]
+    tau, thr, reset, slope, C = 9.0, 0.7, -0.2, 5.0, 7
+    xr, whr, wor = x.clone().requires_grad_(), wh.clone().requires_grad_(), wo.clone().requires_grad_()
+    bhr = None if bh is None else bh.clone().requires_grad_()
+    bor = None if bo is None else bo.clone().requires_grad_()
+    _, hs = R.linear_surrogate_lif_checkpoint(xr, whr, bhr, tau, thr, reset, surrogate, slope, C)
+    _, rates = R.linear_surrogate_lif_rate(hs, wor, bor, tau, thr, reset, surrogate, slope, C, reduction="none")
+    loss = torch.nn.functional.cross_entropy(rates * T, labels, reduction="sum") / 4
+    loss.backward()
+    _, ro = R.linear_surrogate_lif_checkpoint(hs.detach(), wo, bo, tau, thr, reset, surrogate, slope, C)
+    assert 0 < float(hs.detach().mean()) < 0.9 and 0 < float(ro.mean()) < 0.9, "case must spike and reset"
+    lg = (rates.detach() * T).requires_grad_()
+    (torch.nn.functional.cross_entropy(lg, labels, reduction="sum") / 4).backward()
+    got = R.linear_rate_adjoint_f64(x, wh, bh, wo, bo, R.decay_from_tau(tau), thr, reset, surrogate, slope,
+                                    hs.detach(), ro, lg.grad * T)
+    want = {"gx": xr.grad, "gwh": whr.grad, "gwo": wor.grad,
+            "gbh": None if bhr is None else bhr.grad, "gbo": None if bor is None else bor.grad}
+    for k, v in want.items():
+        if v is None:
+            assert got[k] is None
+        else:
+            assert_norm_close(got[k], v, 1e-12, k)
+    # the readout raster derived from the float64 membranes: the same one here
+    derived = R.linear_rate_adjoint_f64(x, wh, bh, wo, bo, R.decay_from_tau(tau), thr, reset, surrogate, slope,
+                                        hs.detach(), None, lg.grad * T)
+    assert torch.equal(derived["readout_spikes"], ro)
+    for k in ("gx", "gwh", "gwo"):
+        assert torch.equal(derived[k], got[k])
+
+
+def test_linear_rate_adjoint_f64_sees_rasters_and_injection():
+    """A raster entry or the injected rate gradient changed moves the result."""
+
+    x, wh, bh, wo, bo, _ = _two_layer_f64_case(22, True)
+    d = R.decay_from_tau(9.0)
+    _, hs = R.linear_surrogate_lif_checkpoint(x, wh, bh, 9.0, 0.7, -0.2, "superspike", 5.0, 7)
+    _, ro = R.linear_surrogate_lif_checkpoint(hs, wo, bo, 9.0, 0.7, -0.2, "superspike", 5.0, 7)
+    gr = torch.randn(x.shape[1], wo.shape[1], generator=seeded(23), dtype=torch.float64)
+    base = R.linear_rate_adjoint_f64(x, wh, bh, wo, bo, d, 0.7, -0.2, "superspike", 5.0, hs, ro, gr)
+    hs2 = hs.clone()
+    hs2[20, 1, 3] = 1.0 - hs2[20, 1, 3]
+    ro2 = ro.clone()
+    ro2[30, 0, 2] = 1.0 - ro2[30, 0, 2]
+    gr2 = gr.clone()
+    gr2[2, 4] += 0.5
+    for args in ((hs2, ro, gr), (hs, ro2, gr), (hs, ro, gr2)):
+        moved = R.linear_rate_adjoint_f64(x, wh, bh, wo, bo, d, 0.7, -0.2, "superspike", 5.0, *args)
+        assert max(float((moved[k] - base[k]).abs().max()) for k in base) > 1e-6
+
+
 def test_matmul_rounding_knob():
     """The oracle's "exact" matmul rounding (float64 products rounded once to
     fp32) is an equally valid fp32 evaluation: same rasters, gradients within

@@ -150,6 +150,23 @@ def test_surrogate_derivative_is_derivative_of_primitive(name):
     assert abs(float(R.surrogate_derivative(name, torch.tensor([0.5], dtype=torch.float64))) - HAND[name]) < 1e-12
 
 
+@pytest.mark.parametrize("name", ["fast_sigmoid", "superspike", "atan"])
+def test_surrogate_derivative_of_huge_arguments_is_zero(name):
+    """fp32 sigma'(c) once (1 + |c|)^2 (or 1 + (pi c / 2)^2) overflows: 0,
+    not NaN, in both restatements (the kernels' reciprocal is held to the
+    same on the GPU)."""
+
+    c = torch.tensor([3e19, -3e19, 1e30, -1e38, float("inf")], dtype=torch.float32)
+    d = R.surrogate_derivative(name, c)
+    assert torch.equal(d, torch.zeros_like(d))
+    x = np.array([[[1e20]], [[0.0]]], dtype=np.float32)  # c = 10 (m' - 1) ~ 1e21 at step 0
+    zeros = np.zeros((1, 1), dtype=np.float32)
+    gx, _ = c_ref.lif_bwd(x, zeros, np.ones_like(x), zeros, np.float32(R.decay_from_tau(20.0)), 1.0, 0.0, 10.0,
+                          name)
+    assert np.isfinite(gx).all()
+    assert gx[0, 0, 0] == 0.0
+
+
 def test_multi_gaussian_derivative_integrates_to_one():
     c = torch.linspace(-12, 12, 240001, dtype=torch.float64)
     area = torch.trapezoid(R.surrogate_derivative("multi_gaussian", c), c)

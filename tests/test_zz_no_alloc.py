@@ -2,7 +2,10 @@
 myelin_gemm with a caller workspace of the size the split needs: the same
 kernels and split, so the outputs must be equal bit for bit.  Two calls in a
 row, the second on a smaller product, so stale scratch contents from the
-first call would show."""
+first call would show.  Captured in a HIP graph, as the process's first
+call of the entry point (its device address lookup then runs inside the
+capture) and again after eager calls, every replay equals the eager
+result bit for bit."""
 
 from __future__ import annotations
 
@@ -35,6 +38,46 @@ def _pair(A, a_dt, B, b_dt, bias, C0, M, N, K, lda, ldb, ta, tb, acc, prec):
               K, lda, ldb, N, ta, tb, acc, prec, stream)
     torch.cuda.synchronize()
     return got, ref, need
+
+
+def test_noalloc_gemm_under_graph_capture():
+    """Kept first in this file: the capture holds the process's first
+    myelin_gemm_noalloc call, whose device-address lookup runs while the
+    stream is being captured; a second graph is captured after eager calls.
+    Replays run with eager work and synchronisations between them."""
+
+    g = torch.Generator().manual_seed(13)
+    bf16 = _lib.DT[torch.bfloat16]
+    prec = _lib.PREC["bf16"]
+    M, N, K = 784, 2048, 12800  # splits K: the partial planes go to the static array
+    assert _need(M, N, K, prec) > 0
+    A = torch.randn(K, M, generator=g).to(torch.bfloat16).to(DEV)
+    B = torch.randn(K, N, generator=g).to(torch.bfloat16).to(DEV)
+    need = _need(M, N, K, prec)
+    ws = torch.empty(need, device=DEV)
+    ref = torch.empty(M, N, device=DEV)
+    _lib.call("myelin_gemm", A.data_ptr(), bf16, B.data_ptr(), bf16, None, ref.data_ptr(), M, N, K, M, N, N, 1, 0,
+              0, prec, ws.data_ptr(), need, _lib.stream(DEV))
+    torch.cuda.synchronize()
+    for which in ("first call inside the capture", "captured after eager calls"):
+        print(f"noalloc graph capture: {which}", flush=True)
+        out = torch.full((M, N), float("nan"), device=DEV)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            _lib.call("myelin_gemm_noalloc", A.data_ptr(), bf16, B.data_ptr(), bf16, None, out.data_ptr(), M, N,
+                      K, M, N, N, 1, 0, 0, prec, _lib.stream(DEV))
+        for rep in range(3):
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {rep} ({which})"
+            # eager work between replays, on the same scratch array
+            eager = torch.empty(M, N, device=DEV)
+            _lib.call("myelin_gemm_noalloc", A.data_ptr(), bf16, B.data_ptr(), bf16, None, eager.data_ptr(), M,
+                      N, K, M, N, N, 1, 0, 0, prec, _lib.stream(DEV))
+            torch.cuda.synchronize()
+            assert torch.equal(eager, ref)
+        del graph
 
 
 def test_noalloc_gemm_equals_workspace_gemm_two_calls():
