@@ -27,7 +27,12 @@ cores):
   long_rate_packed  the same network and step through
                   two_layer_surrogate_lif_rate_packed_hidden_forward (the two
                   layers interleaved per checkpoint chunk, hidden spikes kept
-                  bitpacked); reports peak HBM bytes
+                  bitpacked); reports peak HBM bytes.  checkpoint_size=
+                  "memory" is the memory-lean policy (buffers of one
+                  checkpoint chunk)
+  long_rate_fast, long_rate_packed_fast  the same two steps with
+                  checkpoint_size=45: the same chunk length, buffers of 2**25
+                  floats
   bitpack         pack [512, 64, 8192] spikes, unpack, per-neuron counts over
                   T, per-sample rates (the 33.5 MB packed input of the counts
                   and rates rotated over 12 copies, 403 MB)
@@ -56,7 +61,8 @@ FP32_PEAK_TFLOPS = 157.3
 FWD_BYTES, BWD_BYTES = 8, 12
 PROFILES = ROOT / "profiles"
 TRAFFIC_FILE = PROFILES / "traffic_alif_fast_sigmoid_T256_B128_N4096.json"
-WORKLOADS = ("lif_fwd", "linear_bf16", "long_rate", "long_rate_packed", "bitpack")
+WORKLOADS = ("lif_fwd", "linear_bf16", "long_rate", "long_rate_fast", "long_rate_packed", "long_rate_packed_fast",
+             "bitpack")
 
 
 def _args():
@@ -514,13 +520,10 @@ def _workload_linear_bf16(torch, myelin, args, threads):
 
 
 # ---------------------------------------------------------------- config: long-horizon rate network
-def _lib_prec_fp32():
+def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False, checkpoint_size="memory"):
     from myelin_amd import _lib
+    from myelin_amd import linear as lin
 
-    return _lib.PREC["fp32"]
-
-
-def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
     Tl, Bl, F, H, O = 2000, 32, 1024, 4096, 20
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(4)
@@ -529,9 +532,9 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
     x, labels = x_cpu.to(dev), labels_cpu.to(dev)
     torch.manual_seed(4)
     hidden = myelin.LinearSurrogateLIF(F, H, surrogate=myelin.superspike_surrogate, stream_synapse=True,
-                                       checkpoint_size="memory").to(dev)
+                                       checkpoint_size=checkpoint_size).to(dev)
     readout = myelin.LinearSurrogateLIFRate(H, O, surrogate=myelin.superspike_surrogate,
-                                            checkpoint_size="memory").to(dev)
+                                            checkpoint_size=checkpoint_size).to(dev)
     params = list(hidden.parameters()) + list(readout.parameters())
     wh, bh, wo, bo = hidden.synapse.weight, hidden.synapse.bias, readout.synapse.weight, readout.synapse.bias
 
@@ -541,11 +544,30 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
         if packed_hidden:
             rates = myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(
                 x, wh, bh, wo, bo, myelin.LIFParams(), surrogate="superspike", surrogate_slope=10.0,
-                checkpoint_size="memory")
+                checkpoint_size=checkpoint_size)
         else:
             rates = readout(hidden(x))
         torch.nn.functional.cross_entropy(rates * Tl, labels).backward()
 
+    # the dominant kernel: one forward chunk of the split synapse, 256 steps
+    # x 32 rows = 8192 x 4096 currents over 3 x 1024 bf16 k (the forward's
+    # 2**25-current chunk; the backward's span recomputes run the same kernel)
+    stream = _lib.stream(dev)
+    rows = (lin._CURRENT_CHUNK_ELEMS // (Bl * H)) * Bl
+    xb = x.reshape(Tl * Bl, F)[:rows].to(torch.bfloat16)
+    w3 = torch.empty((3, H, F), dtype=torch.bfloat16, device=dev)
+    _lib.call("myelin_split_bf16x3", wh.data_ptr(), w3.data_ptr(), F, H, 1, stream)
+    cur = torch.empty(rows, H, device=dev)
+
+    def launch():
+        _lib.call("myelin_gemm_parts", xb.data_ptr(), w3.data_ptr(), 3, H * F, bh.data_ptr(), cur.data_ptr(), rows,
+                  H, F, F, F, H, 0, 1, 0, None, 0, stream)
+
+    # median of per-launch HIP event pairs after 10 warmup launches, timed
+    # before any training step in both config-4 workloads (the same memory
+    # state in each; afterwards the caching allocator's placement differs)
+    kern_ms = _launch_ms_median(torch, launch, 41)
+    del xb, w3, cur
     step()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(dev)
@@ -561,36 +583,18 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
     # the input is spikes, so the hidden synapse GEMMs (forward, recompute,
     # dW) run as the exact three-part bf16 split: 3x their flops on the bf16
     # MFMA; the readout GEMMs stay fp32
-    from myelin_amd import _lib
-    from myelin_amd import linear as lin
-
-    split = lin._split_eligible(_lib_prec_fp32(), Tl, Bl, F, H) and bool(torch.equal(x, x.bfloat16().float()))
+    split = lin._split_eligible(_lib.PREC["fp32"], Tl, Bl, F, H) and bool(torch.equal(x, x.bfloat16().float()))
     hidden_flops = 3 * 2 * Tl * Bl * F * H
     executed = (3 * hidden_flops if split else hidden_flops) + (flops - hidden_flops)
     mfma_tflops = executed / (ms * 1e-3) / 1e12
-    # the dominant kernel: one forward chunk of the split synapse, 256 steps
-    # x 32 rows = 8192 x 4096 currents over 3 x 1024 bf16 k (the forward's
-    # 2**25-current chunk; the backward's span recomputes run the same kernel)
-    stream = _lib.stream(dev)
-    rows = (lin._CURRENT_CHUNK_ELEMS // (Bl * H)) * Bl
-    xb = x.reshape(Tl * Bl, F)[:rows].to(torch.bfloat16)
-    w3 = torch.empty((3, H, F), dtype=torch.bfloat16, device=dev)
-    _lib.call("myelin_split_bf16x3", wh.data_ptr(), w3.data_ptr(), F, H, 1, stream)
-    cur = torch.empty(rows, H, device=dev)
-
-    def launch():
-        _lib.call("myelin_gemm_parts", xb.data_ptr(), w3.data_ptr(), 3, H * F, bh.data_ptr(), cur.data_ptr(), rows,
-                  H, F, F, F, H, 0, 1, 0, None, 0, stream)
-
-    # median of per-launch HIP event pairs after 10 warmup launches, the
-    # same in both config-4 workloads
-    kern_ms = _launch_ms_median(torch, launch, 41)
     k_flops = 3 * 2 * rows * H * F
     k_tflops = k_flops / (kern_ms * 1e-3) / 1e12
-    name = ("two_layer_surrogate_lif_rate_packed_hidden_forward(1024->4096->20, checkpoint 'memory'=45, "
+    ck = ("'memory'=45 (lean: chunk and span buffers of one checkpoint chunk)" if checkpoint_size == "memory"
+          else f"{checkpoint_size} (buffers of 2**25 floats)")
+    name = (f"two_layer_surrogate_lif_rate_packed_hidden_forward(1024->4096->20, checkpoint {ck}, "
             "superspike, fp32) + CE, fwd+bwd" if packed_hidden else
-            "LinearSurrogateLIF(1024->4096, stream_synapse, checkpoint 'memory'=45, superspike, "
-            "fp32) + LinearSurrogateLIFRate(4096->20, 'memory') + CE, fwd+bwd")
+            f"LinearSurrogateLIF(1024->4096, stream_synapse, checkpoint {ck}, superspike, "
+            f"fp32) + LinearSurrogateLIFRate(4096->20, {checkpoint_size!r}) + CE, fwd+bwd")
     line = _line("neuron-steps/sec, long-horizon checkpointed rate training step", E / (ms * 1e-3),
                  "neuron-steps/s", ms, args,
                  {"workload": name, "T": Tl, "B": Bl, "F": F, "N": H, "readout": O, "gflop_per_step": flops / 1e9},
@@ -606,7 +610,7 @@ def _workload_long_rate(torch, myelin, args, threads, packed_hidden=False):
                  fp32_equivalent_tflops=tflops, fp32_equivalent_frac_of_fp32_peak=tflops / FP32_PEAK_TFLOPS,
                  hidden_synapse="exact bf16 split (3 parts)" if split else "fp32",
                  peak_step_bytes=peak_bytes, dense_hidden_spike_bytes=Tl * Bl * H * 4)
-    if not args.no_cpu_baseline and not packed_hidden:
+    if not args.no_cpu_baseline and not packed_hidden and checkpoint_size == "memory":
         R = _oracle()
         sb = 1
         C = R.resolve_checkpoint_size(Tl, "memory")
@@ -731,6 +735,9 @@ def main() -> int:
         del src, dst
     others = {"lif_fwd": _workload_lif_fwd, "linear_bf16": _workload_linear_bf16, "long_rate": _workload_long_rate,
               "long_rate_packed": lambda t, m, a, th: _workload_long_rate(t, m, a, th, packed_hidden=True),
+              "long_rate_fast": lambda t, m, a, th: _workload_long_rate(t, m, a, th, checkpoint_size=45),
+              "long_rate_packed_fast": lambda t, m, a, th: _workload_long_rate(t, m, a, th, packed_hidden=True,
+                                                                                checkpoint_size=45),
               "bitpack": _workload_bitpack}
     if args.workload in others:
         print(json.dumps(others[args.workload](torch, myelin, args, threads)), flush=True)

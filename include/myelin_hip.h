@@ -407,6 +407,29 @@ int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
                           myelin_stream_t stream);
 
 /*
+ * myelin_linear_pre_bwd for the hidden layer [C, B, N] of a two-layer
+ * network, with its spike gradient formed in the kernel from the readout's
+ * G_o = grad_out [C, B, O] and weight w_out [N, O] (row-major, as the
+ * readout's weight [in, out]): g_spike[j, b, n] = sum_o grad_out[j, b, o]
+ * * w_out[n, o], the product myelin_gemm_f32(grad_out, w_out^T) computes
+ * (fused multiply-adds in o order from zero), so G equals that GEMM's dS
+ * fed to myelin_linear_pre_bwd, without dS in memory.  No rate gradient.
+ * Needs 1 <= O <= 32, N a multiple of 256, C x O within the kernel's
+ * 64 KB of staged grad_out rows (C <= 512 at O = 32, <= 819 at O = 20)
+ * and g_dtype MYELIN_DT_F32 or MYELIN_DT_BF16X3; else MYELIN_EINVAL.
+ * Replaces: the readout's grad_inputs[t] = grad_pre_reset @ weight.t()
+ *   (autograd.py:877-878) feeding the hidden layer's reverse loop
+ *   (autograd.py:694-715).
+ */
+int myelin_linear_pre_bwd_readout(const float *pre, const float *grad_out,
+                                  const float *w_out, int O, float *grad_m,
+                                  void *G, int g_dtype, float *gbias_acc,
+                                  int64_t C, int64_t B, int64_t N, float decay,
+                                  float threshold, float reset, float slope,
+                                  int surrogate_id, int rule,
+                                  myelin_stream_t stream);
+
+/*
  * out[n] = (accumulate ? out[n] : 0) + sum_r in[r, n], fixed order per
  * column.  Replaces: _linear_surrogate_lif_backward_bias_kernel
  *   (triton/lif.py:1231-1258) without its atomics.

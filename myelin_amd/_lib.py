@@ -68,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "myelin_gemm_noalloc": [_P, _INT, _P, _INT, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P],
     "myelin_transpose_bf16": [_P, _P, _I64, _I64, _P],
     "myelin_linear_pre_bwd": [_P] * 5 + [_INT, _P] + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
+    "myelin_linear_pre_bwd_readout": [_P] * 3 + [_INT] + [_P] * 2 + [_INT, _P] + [_I64] * 3 + [_F] * 4
+    + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],
     "myelin_lif_currents_fwd": [_P] * 9 + [_I64] * 8 + [_F] * 4 + [_INT, _P],
 }

@@ -2880,6 +2880,102 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   }
 }
 
+// The hidden layer's reverse pass of a two-layer network with its spike
+// gradient formed in the kernel: gs[j, b, n] = sum_o G_o[j, b, o] W_o[n, o]
+// (dS = G_o W_o^T), summed in o order with fused multiply-adds from zero
+// over KMAX terms (zero past O) -- the small-K GEMM's arithmetic, so G is
+// the one dS written by that GEMM and read back gives, without dS's write
+// and read ([C, B, N] floats each way).  A workgroup's 256 V neurons lie in
+// one batch row b (N a multiple of 256 V): it stages that row's G_o [C, O]
+// in LDS, zero-padded to KMAX columns, and each step's row reaches every
+// lane as broadcast 16-byte LDS reads.  A lane holds its V neurons' rows of
+// W_o (V x KMAX registers).  The reverse walk is linear_pre_bwd's, with the
+// pre-reset trace the one operand streamed from HBM.
+template <int SID, int GM, int V, int KMAX>
+__global__ __launch_bounds__(256) void linear_pre_bwd_ds(PreBwdArgs p, const float *go, const float *wo, int O,
+                                                         int64_t N) {
+  extern __shared__ __attribute__((aligned(16))) float s_go[];  // [C][KMAX]
+  using VT = typename PreVec<V>::T;
+  constexpr int DEPTH = V == 2 ? 4 : kPipe;
+  const int64_t C = p.C, row = p.BN / V;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * V);
+  const int64_t bi = base / N, Bn = p.BN / N;
+  for (int64_t q = threadIdx.x; q < C * KMAX; q += 256) {
+    const int64_t j = q / KMAX;
+    const int o = static_cast<int>(q % KMAX);
+    s_go[q] = o < O ? go[(j * Bn + bi) * O + o] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t i = base + static_cast<int64_t>(threadIdx.x) * V;  // < BN: the grid is BN / (256 V) exactly
+  const int64_t n = i - bi * N;
+  float w[V][KMAX];
+#pragma unroll
+  for (int e = 0; e < V; ++e)
+#pragma unroll
+    for (int o = 0; o < KMAX; ++o) w[e][o] = o < O ? wo[(n + e) * O + o] : 0.0f;
+  float gm[V], gstep[V], gb[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    gm[e] = p.gm != nullptr ? p.gm[i + e] : 0.0f;
+    gstep[e] = p.grate != nullptr ? p.grate[i + e] / p.rate_denominator : 0.0f;
+    gb[e] = 0.0f;
+  }
+  auto step = [&](int64_t j, VT pv) {
+    const f4 *r = reinterpret_cast<const f4 *>(s_go + j * KMAX);
+    float acc[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KMAX / 4; ++q) {
+      const f4 g4 = r[q];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[e] = __builtin_fmaf(g4[u], w[e][4 * q + u], acc[e]);
+    }
+    VT gsv;
+    if constexpr (V == 2)
+      gsv = float2{acc[0], acc[1]};
+    else
+      gsv = acc[0];
+    pre_bwd_step<SID, true, GM, V>(p, i, j, pv, gsv, gstep, gm, gb);
+  };
+  const VT *pre = reinterpret_cast<const VT *>(p.pre + i);
+  const int64_t nblk = (C + DEPTH - 1) / DEPTH;
+  const int64_t f = C - (nblk - 1) * DEPTH;
+  VT pv[DEPTH];
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u) pv[u] = pre[(C - 1 - (u < f ? u : f - 1)) * row];
+  // block 0 (f steps), prefetching block 1 (or re-reading block 0 when alone)
+  {
+    const int64_t r0 = nblk > 1 ? f : 0;
+    VT np[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) np[u] = pre[(C - 1 - (r0 + u < C ? r0 + u : C - 1)) * row];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u)
+      if (u < f) step(C - 1 - u, pv[u]);
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) pv[u] = np[u];
+  }
+  for (int64_t r0 = f; r0 < C; r0 += DEPTH) {
+    const int64_t rn = r0 + DEPTH < C ? r0 + DEPTH : r0;
+    VT np[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) np[u] = pre[(C - 1 - rn - u) * row];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) step(C - 1 - r0 - u, pv[u]);
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) pv[u] = np[u];
+  }
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    if (p.gm != nullptr) p.gm[i + e] = gm[e];
+    if (p.gbias_acc != nullptr) p.gbias_acc[i + e] = (p.gm != nullptr ? p.gbias_acc[i + e] : 0.0f) + gb[e];
+  }
+}
+
 // out[n] (+)= sum_r in[r, n], in a fixed order (deterministic).
 // 8 columns per workgroup (a 2048-column sum spreads over 256 CUs): thread
 // (column c = tid % 8, group q = tid / 8) sums rows q, q + 32, ... in order,
@@ -3485,6 +3581,46 @@ void launch_pre_bwd(const PreBwdArgs &a, bool gs, int gm, hipStream_t s) {
     launch_pre_bwd_v<SID, 1>(a, gs, gm, dim3(cdiv(a.BN, 256)), s);
 }
 
+// the spike-gradient-forming reverse pass: KMAX the small-K GEMM's
+// unroll for K = O (8, 12, ..., 24, then 32), so the two sum alike
+constexpr int64_t kPreBwdDsLds = 65536;  // bytes of staged G_o rows per workgroup
+
+int pre_bwd_ds_kmax(int O) { return O <= 8 ? 8 : O <= 12 ? 12 : O <= 16 ? 16 : O <= 20 ? 20 : O <= 24 ? 24 : 32; }
+
+template <int SID, int GM, int V>
+void launch_pre_bwd_ds_k(const PreBwdArgs &a, const float *go, const float *wo, int O, int64_t N, hipStream_t s) {
+  const int kmax = pre_bwd_ds_kmax(O);
+  const dim3 grid(static_cast<unsigned>(a.BN / (256 * V)));
+  const size_t lds = static_cast<size_t>(a.C) * kmax * sizeof(float);
+  switch (kmax) {
+    case 8: linear_pre_bwd_ds<SID, GM, V, 8><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 12: linear_pre_bwd_ds<SID, GM, V, 12><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 16: linear_pre_bwd_ds<SID, GM, V, 16><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 20: linear_pre_bwd_ds<SID, GM, V, 20><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 24: linear_pre_bwd_ds<SID, GM, V, 24><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    default: linear_pre_bwd_ds<SID, GM, V, 32><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+  }
+}
+
+// two neurons per lane on the wide grids, as launch_pre_bwd chooses
+template <int SID>
+void launch_pre_bwd_ds(const PreBwdArgs &a, int gm, const float *go, const float *wo, int O, int64_t N,
+                       hipStream_t s) {
+  const bool v2 = a.BN >= 65536 && N % 512 == 0 && myelin::aligned(a.pre, 8) && myelin::aligned(a.gm, 8) &&
+                  myelin::aligned(a.gbias_acc, 8) && myelin::aligned(a.G, gm == 0 ? 8 : 4);
+  if (v2) {
+    if (gm == 2)
+      launch_pre_bwd_ds_k<SID, 2, 2>(a, go, wo, O, N, s);
+    else
+      launch_pre_bwd_ds_k<SID, 0, 2>(a, go, wo, O, N, s);
+  } else {
+    if (gm == 2)
+      launch_pre_bwd_ds_k<SID, 2, 1>(a, go, wo, O, N, s);
+    else
+      launch_pre_bwd_ds_k<SID, 0, 1>(a, go, wo, O, N, s);
+  }
+}
+
 template <bool PRE, bool SPK, bool PK>
 void launch_cur_rule(const CurArgs &a, dim3 grid, hipStream_t s) {
   const bool ck = a.ckpt != nullptr;
@@ -3795,6 +3931,41 @@ extern "C" int myelin_linear_pre_bwd(const float *pre, const float *grad_spikes,
     default: return myelin::invalid("linear_pre_bwd: unknown surrogate id %d", surrogate_id);
   }
   return myelin::launched("linear_pre_bwd");
+}
+
+extern "C" int myelin_linear_pre_bwd_readout(const float *pre, const float *grad_out, const float *w_out, int O,
+                                             float *grad_m, void *G, int g_dtype, float *gbias_acc, int64_t C,
+                                             int64_t B, int64_t N, float decay, float threshold, float reset,
+                                             float slope, int surrogate_id, int rule, myelin_stream_t stream) {
+  if (C < 1 || B < 1 || N < 1) return myelin::invalid("linear_pre_bwd_readout: C, B and N must be positive");
+  if (pre == nullptr || grad_out == nullptr || w_out == nullptr || G == nullptr)
+    return myelin::invalid("linear_pre_bwd_readout: null pointer");
+  if (O < 1 || O > 32) return myelin::invalid("linear_pre_bwd_readout: O must be in [1, 32]; got %d", O);
+  if (N % 256 != 0) return myelin::invalid("linear_pre_bwd_readout: N must be a multiple of 256; got %lld",
+                                           static_cast<long long>(N));
+  if (g_dtype != MYELIN_DT_F32 && g_dtype != MYELIN_DT_BF16X3)
+    return myelin::invalid("linear_pre_bwd_readout: G must be float32 or three bfloat16 planes");
+  if (C * pre_bwd_ds_kmax(O) * static_cast<int64_t>(sizeof(float)) > kPreBwdDsLds)
+    return myelin::invalid("linear_pre_bwd_readout: C x O too large for the staged rows (C = %lld)",
+                           static_cast<long long>(C));
+  if (B * N / 512 > 0x7fffffff) return myelin::invalid("linear_pre_bwd_readout: B x N too large");
+  PreBwdArgs a{pre, nullptr, nullptr, grad_m, G, gbias_acc, C, B * N, decay, threshold, reset, slope, 1.0f, rule};
+  if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
+    return myelin::invalid("linear_pre_bwd_readout: unknown rule %d", rule);
+  hipStream_t s = myelin::as_hip(stream);
+  const int gh = g_dtype == MYELIN_DT_BF16X3 ? 2 : 0;
+  switch (surrogate_id) {
+    case MYELIN_SG_SIGMOID: launch_pre_bwd_ds<MYELIN_SG_SIGMOID>(a, gh, grad_out, w_out, O, N, s); break;
+    case MYELIN_SG_FAST_SIGMOID: launch_pre_bwd_ds<MYELIN_SG_FAST_SIGMOID>(a, gh, grad_out, w_out, O, N, s); break;
+    case MYELIN_SG_ATAN: launch_pre_bwd_ds<MYELIN_SG_ATAN>(a, gh, grad_out, w_out, O, N, s); break;
+    case MYELIN_SG_TRIANGULAR: launch_pre_bwd_ds<MYELIN_SG_TRIANGULAR>(a, gh, grad_out, w_out, O, N, s); break;
+    case MYELIN_SG_SUPERSPIKE: launch_pre_bwd_ds<MYELIN_SG_SUPERSPIKE>(a, gh, grad_out, w_out, O, N, s); break;
+    case MYELIN_SG_MULTI_GAUSSIAN:
+      launch_pre_bwd_ds<MYELIN_SG_MULTI_GAUSSIAN>(a, gh, grad_out, w_out, O, N, s);
+      break;
+    default: return myelin::invalid("linear_pre_bwd_readout: unknown surrogate id %d", surrogate_id);
+  }
+  return myelin::launched("linear_pre_bwd_readout");
 }
 
 extern "C" int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int64_t cols, int accumulate,

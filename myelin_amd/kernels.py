@@ -276,6 +276,15 @@ def surrogate_alif_forward(
     return ALIFState(membrane=m, adaptation=a), spikes
 
 
+def _lean(checkpoint_size) -> bool:
+    """The memory policy asks for small chunk scratch (checkpointing.py:13-20):
+    the HIP layers then size their chunk and span buffers to one checkpoint
+    chunk instead of 2**25 floats (an int checkpoint size keeps the larger,
+    faster buffers)."""
+
+    return checkpoint_size == "memory"
+
+
 def _resolve(inputs: torch.Tensor, checkpoint_size: CheckpointSize | None) -> int | None:
     if checkpoint_size is None:
         return None
@@ -315,7 +324,8 @@ def linear_surrogate_lif_forward(
     if not hard_forward:
         raise ValueError("HIP linear surrogate LIF currently supports only hard_forward=True")
     ck = _resolve(inputs, checkpoint_size)
-    m, spikes = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, False, synapse_precision)
+    m, spikes = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, False, synapse_precision,
+                               lean=_lean(checkpoint_size))
     return LIFState(membrane=m), spikes
 
 
@@ -373,7 +383,8 @@ def linear_surrogate_lif_rate_forward(
                 inputs, weight, bias, params.decay, params.threshold, params.reset, surrogate_slope, ck, block_b,
                 block_n, block_f)
     else:
-        m, rates = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, True, synapse_precision)
+        m, rates = linear_forward(inputs, weight, bias, params, sid, surrogate_slope, ck, True, synapse_precision,
+                                  lean=_lean(checkpoint_size))
     if reduction == "mean":
         return LIFState(membrane=m), rates.mean()
     return LIFState(membrane=m), rates
@@ -440,7 +451,8 @@ def two_layer_surrogate_lif_rate_recompute_forward(
         raise ValueError("two-layer recompute currently supports only hard_forward=True")
     ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
     return two_layer_rate_forward(inputs, hidden_weight, hidden_bias, output_weight, output_bias, params, sid,
-                                  surrogate_slope, ck, synapse_precision, packed_hidden=False)
+                                  surrogate_slope, ck, synapse_precision, packed_hidden=False,
+                                  lean=_lean(checkpoint_size))
 
 
 def two_layer_surrogate_lif_rate_packed_hidden_forward(
@@ -478,4 +490,5 @@ def two_layer_surrogate_lif_rate_packed_hidden_forward(
         raise ValueError("packed-hidden two-layer rate training requires CUDA tensors")
     ck = resolve_checkpoint_size(int(inputs.shape[0]), checkpoint_size)
     return two_layer_rate_forward(inputs, hidden_weight, hidden_bias, output_weight, output_bias, params, sid,
-                                  surrogate_slope, ck, synapse_precision, packed_hidden=True)
+                                  surrogate_slope, ck, synapse_precision, packed_hidden=True,
+                                  lean=_lean(checkpoint_size))

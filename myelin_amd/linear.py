@@ -36,17 +36,29 @@ import torch
 from myelin_amd import _lib
 
 
+def _workspace(M, N, K, prec, device, split, ws):
+    """(split-K workspace, its size in floats): ``ws``, a float32 buffer the
+    caller has free on the stream (the kernel then splits K no more ways
+    than it holds), else a new one of the size the kernel would use."""
+
+    if not split:
+        return None, 0
+    if ws is not None:
+        return ws, ws.numel()
+    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec)
+    return (torch.empty(n_ws, dtype=torch.float32, device=device) if n_ws > 0 else None), n_ws
+
+
 def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None, a_bits=False,
-          split=True):
+          split=True, ws=None):
     """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16, or
     (``a_bits``) A packed spike words (int32, lda in words) with B float32.
     ``split=False`` gives no workspace, so K is never split: every element is
     then one k-ordered sum that does not depend on M (the synapse currents,
     which a checkpointed backward recomputes over fewer rows and must
-    reproduce bit for bit)."""
+    reproduce bit for bit).  ``ws``: see _workspace."""
 
-    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, prec) if split else 0
-    ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
+    ws, n_ws = _workspace(M, N, K, prec, C.device, split, ws)
     a_dt = _lib.DT_BITS if a_bits else _lib.DT[A.dtype]
     _lib.call("myelin_gemm", _lib.ptr(A), a_dt, _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
               _lib.ptr(C), M, N, K, lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws),
@@ -76,12 +88,11 @@ def _transpose_bf16(w, stream):
 
 
 def _gemm_parts(A, B, parts, b_part, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, stream, bias=None,
-                split=True):
+                split=True, ws=None):
     """C (+)= sum_p op(A) op(B_p) (+ bias), bf16 operands, B_p = B + p*b_part
-    (elements); ``split`` as in _gemm."""
+    (elements); ``split`` and ``ws`` as in _gemm."""
 
-    n_ws = _lib.load().myelin_gemm_workspace_elems(M, N, K, _lib.PREC["bf16"]) if split else 0
-    ws = torch.empty(n_ws, dtype=torch.float32, device=C.device) if n_ws > 0 else None
+    ws, n_ws = _workspace(M, N, K, _lib.PREC["bf16"], C.device, split, ws)
     _lib.call("myelin_gemm_parts", _lib.ptr(A), _lib.ptr(B), parts, b_part, _lib.ptr(bias), _lib.ptr(C), M, N, K,
               lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), _lib.ptr(ws), n_ws, stream)
 
@@ -91,6 +102,31 @@ def _gemm_parts(A, B, parts, b_part, C, M, N, K, lda, ldb, ldc, trans_a, trans_b
 _SPLIT_MIN_MACS = 1 << 32
 
 
+class _LazyBf16:
+    """A bf16 view of an fp32 input ``[T, ...]`` that keeps no whole bf16
+    copy: indexing it with a slice of steps launches the cast of those steps
+    on the current stream and returns a new bf16 tensor.  Used by the
+    memory-lean policy (``checkpoint_size="memory"``), whose GEMMs then read
+    one checkpoint chunk or span of bf16 input at a time."""
+
+    dtype = torch.bfloat16
+
+    def __init__(self, x: torch.Tensor):
+        self.x = x
+        self.shape = x.shape
+        self.device = x.device
+        self._last = (None, None)
+
+    def __getitem__(self, steps: slice) -> torch.Tensor:
+        # the last slice is kept: a backward span's recompute and its weight
+        # gradient read the same steps, one after the other on one stream
+        key = (steps.start, steps.stop, steps.step)
+        if self._last[0] != key:
+            part = self.x[steps]
+            self._last = (key, _cast_bf16(part, _lib.stream(part.device)))
+        return self._last[1]
+
+
 class _Split:
     """The fp32 synapse on the bf16 MFMA, exactly: when every input value is
     a bf16 value (spikes, small integers), ``x @ W = x @ W_hi + x @ W_mid +
@@ -98,16 +134,28 @@ class _Split:
     product is exact and only the fp32 summation rounds -- at the bf16
     engine's rate (about 5x the fp32 one per pass).
 
-    Construction launches the checked bf16 copy of x (``xb``), the split of
-    W into transposed planes ``w3 [3, N, F]`` and an asynchronous copy of
-    the check's flag to pinned host memory, without waiting.  ``exact()``
+    Construction launches the checked bf16 copy of x (``xb``; with ``lean``
+    only the check, ``xb`` then a _LazyBf16 view), the split of W into
+    transposed planes ``w3 [3, N, F]`` and an asynchronous copy of the
+    check's flag to pinned host memory, without waiting.  ``exact()``
     waits for the flag alone (not for later work on the stream) and caches
     the answer; when it is False the fp32 GEMMs must run instead."""
 
-    def __init__(self, x, w, stream):
-        self.xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    def __init__(self, x, w, stream, lean=False):
         flag = torch.zeros(1, dtype=torch.int32, device=x.device)
-        _lib.call("myelin_cast_bf16_checked", _lib.ptr(x), _lib.ptr(self.xb), x.numel(), _lib.ptr(flag), stream)
+        if lean:
+            # no whole bf16 copy: check x slice by slice into one scratch
+            # buffer (the flag is only ever set), and cast per chunk later
+            self.xb = _LazyBf16(x)
+            step = max(1, (1 << 22) // max(1, x[0].numel()))
+            scratch = torch.empty((min(step, x.shape[0]), *x.shape[1:]), dtype=torch.bfloat16, device=x.device)
+            for t0 in range(0, x.shape[0], step):
+                part = x[t0:t0 + step]
+                _lib.call("myelin_cast_bf16_checked", _lib.ptr(part), _lib.ptr(scratch), part.numel(), _lib.ptr(flag),
+                          stream)
+        else:
+            self.xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+            _lib.call("myelin_cast_bf16_checked", _lib.ptr(x), _lib.ptr(self.xb), x.numel(), _lib.ptr(flag), stream)
         self._host = torch.empty(1, dtype=torch.int32, pin_memory=True)
         self._host.copy_(flag, non_blocking=True)
         self._ready = torch.cuda.Event()
@@ -124,10 +172,10 @@ class _Split:
         return self._exact
 
 
-def _split_synapse(x, w, stream):
+def _split_synapse(x, w, stream, lean=False):
     """Start the exact split of ``x @ W`` (see _Split)."""
 
-    return _Split(x, w, stream)
+    return _Split(x, w, stream, lean)
 
 
 def _split_eligible(prec: int, T: int, B: int, F: int, N: int) -> bool:
@@ -214,23 +262,42 @@ def _fused(B: int, N: int) -> bool:
     return N >= 64 and _fused_grid(B, N) >= 1024
 
 
-def _span(T: int, checkpoint: int, BN: int) -> int:
+def _span(T: int, checkpoint: int, BN: int, budget: int = _CURRENT_CHUNK_ELEMS) -> int:
     """Steps per backward span of a checkpointed layer: whole chunks, as
-    many as keep a span's trace within _CURRENT_CHUNK_ELEMS."""
+    many as keep a span's trace within ``budget`` floats."""
 
-    return checkpoint * max(1, min(math.ceil(T / checkpoint), _CURRENT_CHUNK_ELEMS // (checkpoint * BN)))
+    return checkpoint * max(1, min(math.ceil(T / checkpoint), budget // (checkpoint * BN)))
+
+
+# forward chunk budget (floats) of the memory-lean policy: the forward's
+# buffers are transient and never set a checkpointed step's peak, which the
+# backward's span buffers do, so the forward keeps chunks large enough for
+# its GEMMs to fill the chip
+_LEAN_FWD_ELEMS = 1 << 24
+
+
+def _budgets(lean: bool, checkpoint, B: int, N: int) -> tuple[int, int]:
+    """(forward chunk, backward span) buffer budgets in floats.  Under the
+    memory-lean policy (checkpoint_size="memory", whose purpose is to keep
+    the chunk scratch small, checkpointing.py:13-20) a backward span is one
+    checkpoint chunk and forward chunks hold 2**24 currents; otherwise both
+    hold 2**25 -- fewer, larger GEMMs."""
+
+    if lean and checkpoint is not None:
+        return _LEAN_FWD_ELEMS, checkpoint * B * N
+    return _CURRENT_CHUNK_ELEMS, _CURRENT_CHUNK_ELEMS
 
 
 def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, stream, *, m_final=None,
              spikes=None, pre=None, packed=None, rates=None, ckpt=None, ckpt_every=1, wt=None, exact=False,
-             pre_from=None, split=None, x32=None, x_bits=None):
+             pre_from=None, split=None, x32=None, x_bits=None, budget=_CURRENT_CHUNK_ELEMS, cur=None):
     """Synaptic currents + LIF recurrence over steps [t0, t1).
 
     ``x`` is fp32 with ``w [F, N]`` fp32, or bf16 (bf16 synapse) with ``wt``,
     the bf16 transposed weight ``[N, F]``.  Fused (one launch, currents stay
     in LDS) when N >= 64 and the fused grid has >= 1024 workgroups.
     Otherwise each workgroup would walk many chunks serially, so the steps
-    are processed in chunks of up to 2**25 currents: an MFMA GEMM (split-K
+    are processed in chunks of up to ``budget`` currents: an MFMA GEMM (split-K
     when narrow) writes ``x_t @ W + b`` for the chunk, then the recurrence
     kernel consumes it, carrying the membrane and the spike counts across
     chunks; with several chunks, each chunk's GEMM runs on a side stream
@@ -249,6 +316,9 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     ``x_bits``: the input as packed spike words ``[T, B, ceil(F / 32)]``,
     which the chunked route's GEMM reads in place of ``x`` (fp32 synapse
     weights ``w``; the same sums bit for bit).
+    ``cur``: an fp32 buffer of at least one chunk's currents for the chunked
+    route to use instead of allocating its own (when the GEMMs run in turn
+    on the one stream).
     """
 
     if x_bits is not None:
@@ -272,7 +342,7 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
             _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *outs, prec, stream)
         return
     dev = x.device
-    step = max(1, min(t1 - t0, _CURRENT_CHUNK_ELEMS // (B * N)))
+    step = max(1, min(t1 - t0, budget // (B * N)))
     p0 = t0 if pre_from is None else pre_from  # pre holds the steps from p0 on
     bounds = sorted({*range(t0, t1, step), t1} | ({p0} if t0 < p0 < t1 else set()))
     n = len(bounds) - 1
@@ -286,7 +356,10 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
     overlap = n > 1 and not half and main.cuda_stream == stream and side.cuda_stream != stream
-    curs = [torch.empty((step, B, N), dtype=torch.float32, device=dev) for _ in range(2 if overlap else 1)]
+    if cur is not None and not overlap and cur.dtype == torch.float32 and cur.numel() >= step * B * N:
+        curs = [cur.reshape(-1)[:step * B * N].view(step, B, N)]
+    else:
+        curs = [torch.empty((step, B, N), dtype=torch.float32, device=dev) for _ in range(2 if overlap else 1)]
     # the membrane carried across chunks lives in m_final (each lane reads
     # its m0 before writing, so m0 may be m_final); a single chunk needs no
     # carry buffer at all
@@ -415,7 +488,7 @@ class HipLinearLIFFunction(torch.autograd.Function):
     ``(final_membrane, rates)`` where ``rates = spike_count / T``."""
 
     @staticmethod
-    def forward(ctx: Any, x, w, b, decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule):
+    def forward(ctx: Any, x, w, b, decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, lean=False):
         T, B, F = x.shape
         N = w.shape[1]
         dev = x.device
@@ -424,9 +497,10 @@ class HipLinearLIFFunction(torch.autograd.Function):
         half = _half(prec, F, N)
         xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
         bits = _spike_bits(x) if _bits_consumer(B, F, N, prec) else None
+        fwd_budget, budget = _budgets(lean, checkpoint, B, N)
         split = None
         if not half and bits is None and _split_eligible(prec, T, B, F, N):
-            split = _split_synapse(x, w, stream)
+            split = _split_synapse(x, w, stream, lean=lean and checkpoint is not None)
             xs, wt = split.xb, split.w3
         m_final = torch.empty((B, N), dtype=x.dtype, device=dev)
         out = torch.empty((B, N) if rate else (T, B, N), dtype=x.dtype, device=dev)
@@ -446,43 +520,47 @@ class HipLinearLIFFunction(torch.autograd.Function):
                     # the backward starts with the last span, whose trace
                     # this forward computes anyway: keep it (the buffer the
                     # backward would fill) instead of recomputing it there
-                    span = _span(T, checkpoint, B * N)
+                    span = _span(T, checkpoint, B * N, budget)
                     tail = (math.ceil(T / span) - 1) * span
                     pre = torch.empty((T - tail, B, N), dtype=x.dtype, device=dev)
         _lif_fwd(xs, w, b, None, 0, T, decay, threshold, reset, slope, rule, prec, stream, m_final=m_final,
                  spikes=None if rate else out, pre=pre, packed=words, rates=out if rate else None, ckpt=ckpt,
                  ckpt_every=checkpoint or 1, wt=wt, exact=ckpt is not None, pre_from=tail, split=split, x32=x,
-                 x_bits=bits)
+                 x_bits=bits, budget=fwd_budget)
         if split is not None and not split.exact():
             xs, wt = x, None
         if words is not None:
             _attach_bits(out, words)
         if bits is not None:
             xs = bits  # what the backward's weight GEMM reads
+        lazy = isinstance(xs, _LazyBf16)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, b is not None,
-                    F if bits is not None else None)
+                    F if bits is not None else None, budget, lazy)
         if need:
-            # the bf16 synapse keeps the bf16 copies of x and W^T (what its GEMMs read)
-            ctx.save_for_backward(xs, w, b, pre, ckpt, wt)
+            # the bf16 synapse keeps the bf16 copies of x and W^T (what its
+            # GEMMs read); the lean split keeps x and casts per span
+            ctx.save_for_backward(x if lazy else xs, w, b, pre, ckpt, wt)
         return m_final, out
 
     @staticmethod
     def backward(ctx: Any, g_m, g_out):
-        none = (None,) * 12
+        none = (None,) * 13
         if (g_m is None and g_out is None) or not any(ctx.needs_input_grad[:3]):
             return none
-        decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b, bits_f = ctx.meta
+        decay, threshold, reset, sid, slope, checkpoint, rate, prec, rule, has_b, bits_f, budget, lazy = ctx.meta
         xs, w, b, pre, ckpt, wt = ctx.saved_tensors
+        if lazy:
+            xs = _LazyBf16(xs)
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
         gx, gw, gb = linear_backward(xs, w, b if has_b else None, pre, ckpt, wt, g_m, g_out, decay, threshold,
                                      reset, sid, slope, checkpoint, rate, prec, rule, need_x, need_w,
-                                     need_b and has_b, bits_f=bits_f)
-        return gx, gw, gb, None, None, None, None, None, None, None, None, None
+                                     need_b and has_b, bits_f=bits_f, budget=budget)
+        return gx, gw, gb, None, None, None, None, None, None, None, None, None, None
 
 
 def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset, sid, slope, checkpoint, rate,
-                    prec, rule, need_x=True, need_w=True, need_b=True, bits_f=None):
+                    prec, rule, need_x=True, need_w=True, need_b=True, bits_f=None, budget=_CURRENT_CHUNK_ELEMS):
     """Gradients (dX, dW, db) of the streamed-synapse LIF, span by span in
     reverse time: recompute the span's pre-reset trace from its first
     checkpoint (``checkpoint=None``: the saved trace ``pre`` covers all T;
@@ -507,11 +585,11 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         stream = _lib.stream(dev)
         wg = _cast_bf16(w, stream) if (half and need_x) else w
         # the reverse pass walks spans of whole checkpoint chunks, as many as
-        # keep a span's trace within _CURRENT_CHUNK_ELEMS: one recompute
+        # keep a span's trace within `budget` floats: one recompute
         # (from the span's first checkpoint, which the recurrence carries
         # through the later ones exactly as the forward did), one reverse
         # launch and one dX / dW GEMM pair per span instead of per chunk
-        span = T if checkpoint is None else _span(T, checkpoint, BN)
+        span = T if checkpoint is None else _span(T, checkpoint, BN, budget)
         per = 1 if checkpoint is None else span // checkpoint  # checkpoint rows per span
         want_gb = need_b and b is not None
         # one span and no membrane gradient: the reverse launch is the whole
@@ -529,25 +607,42 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         gx = torch.empty((T, B, F), device=dev) if need_x else None
         gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
         gb_acc = (torch.empty((B, N), device=dev) if whole else zeros[-1]) if want_gb else None
-        G = torch.empty((min(span, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
         # exact split: dW reads G as three bf16 planes [3, C, B, N] (C the
         # span's steps), written by the reverse pass itself unless dX needs
         # the fp32 G as well
         G3 = torch.empty(3 * min(span, T) * BN, dtype=torch.bfloat16, device=dev) if parts and need_w else None
         if G3 is not None and not need_x:
             G = G3
+        else:
+            G = torch.empty((min(span, T), B, N), dtype=torch.bfloat16 if half else torch.float32, device=dev)
         n_spans = math.ceil(T / span)
         tail = pre if checkpoint is not None else None  # the last span's trace, from the forward
         if tail is not None and tail.shape[0] != T - (n_spans - 1) * span:
             raise ValueError("the saved trace does not cover the last backward span")
         recomputes = checkpoint is not None and (tail is None or n_spans > 1)
-        scratch = torch.empty((min(span, T), B, N), device=dev) if recomputes else None
         # GEMM recomputes on the fp32 engine run one span ahead on a side
         # stream, into two alternating trace buffers: span k-1's recompute
         # overlaps span k's reverse pass and weight GEMMs (the bf16 engines
         # and the split run in turn, as in the forward).  ready[i]: buffer i
         # holds its span's trace; free[i]: the reverse pass has read buffer i.
         overlap = checkpoint is not None and n_spans > 1 and not (half or parts)
+        # in turn, the trace buffer is spent once the reverse pass has read
+        # it and is refilled only by the next span's recompute: it doubles
+        # as the split-K workspace of the span's dX and dW GEMMs
+        ws = None
+        if recomputes:
+            n_sc = min(span, T) * BN
+            if not overlap:
+                lib, r_span = _lib.load(), min(span, T) * B
+                n_sc = max(n_sc, lib.myelin_gemm_workspace_elems(r_span, F, N, prec) if need_x else 0,
+                           lib.myelin_gemm_workspace_elems(F, N, r_span, _lib.PREC["bf16"] if parts else prec)
+                           if need_w else 0)
+            ws = torch.empty(n_sc, device=dev)
+            scratch = ws[:min(span, T) * BN].view(min(span, T), B, N)
+            if overlap:
+                ws = None
+        else:
+            scratch = None
         if overlap:
             main = torch.cuda.current_stream(dev)
             side = _side_stream(dev)
@@ -562,7 +657,8 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                     if j + 2 < n_spans:
                         side.wait_event(free[i])
                     _lif_fwd(xs, w, b, ckpt[j * per], j * span, min(j * span + span, T), decay, threshold, reset,
-                             slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True, x_bits=x_bits)
+                             slope, rule, prec, side.cuda_stream, pre=bufs[i], wt=wt, exact=True, x_bits=x_bits,
+                             budget=budget)
                     ready[i].record(side)
 
             if tail is None:
@@ -583,8 +679,10 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
                 main.wait_event(ready[k % 2])
                 pre_k = bufs[k % 2]
             else:
+                # the recompute's currents may use G's buffer: the reverse
+                # pass writes G only after the recompute
                 _lif_fwd(xs, w, b, ckpt[k * per], t0, t1, decay, threshold, reset, slope, rule, prec, stream,
-                         pre=scratch, wt=wt, exact=True, x_bits=x_bits)
+                         pre=scratch, wt=wt, exact=True, x_bits=x_bits, budget=budget, cur=G)
                 pre_k = scratch
             _lib.call(
                 "myelin_linear_pre_bwd",
@@ -601,18 +699,18 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             # B=256 went from 0.547 to 0.606 ms)
             if gx is not None:
                 # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
-                _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream)
+                _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream, ws=ws)
             if gw is not None and parts:
                 if G is not G3:
                     _lib.call("myelin_split_bf16x3", _lib.ptr(G), _lib.ptr(G3), rows, N, 0, stream)
                 _gemm_parts(xs[t0:t1], G3, 3, rows * N, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1,
-                            stream)
+                            stream, ws=ws)
             elif gw is not None and x_bits is not None:
                 _gemm(x_bits[t0:t1], G, gw, F, N, rows, x_bits.shape[2], N, N, True, False, k != n_spans - 1, prec,
-                      stream, a_bits=True)
+                      stream, a_bits=True, ws=ws)
             elif gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream)
+                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream, ws=ws)
         if overlap:
             # every side-stream kernel is behind a ready[] the main stream
             # waited on; the buffers' last users include the side stream
@@ -626,9 +724,10 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
 
 
 def linear_forward(x, w, b, params, surrogate_id: int, slope: float, checkpoint, rate: bool, precision: str,
-                   rule: int = _lib.RULE_THRESHOLD):
+                   rule: int = _lib.RULE_THRESHOLD, lean: bool = False):
     """Validate and run the fused streamed-synapse LIF (shared by the public
-    entry points in myelin_amd.kernels)."""
+    entry points in myelin_amd.kernels).  ``lean``: the memory-lean policy
+    (chunk and span buffers of one checkpoint chunk)."""
 
     if x.ndim != 3:
         raise ValueError(f"inputs must be shaped [T, B, F]; got {tuple(x.shape)}")
@@ -654,7 +753,7 @@ def linear_forward(x, w, b, params, surrogate_id: int, slope: float, checkpoint,
         return HipLinearLIFFunction.apply(
             x.contiguous(), w.contiguous(), None if b is None else b.contiguous(), float(params.decay),
             float(params.threshold), float(params.reset), surrogate_id, float(slope), checkpoint, rate,
-            _lib.PREC[precision], rule,
+            _lib.PREC[precision], rule, lean,
         )
 
 

@@ -43,8 +43,8 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _gemm_parts, _half, _keep_trace, _lif_fwd,
-                               _side_stream, _split_eligible, _split_synapse, _transpose_bf16)
+from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _LEAN_FWD_ELEMS, _cast_bf16, _gemm, _gemm_parts, _half, _keep_trace,
+                               _LazyBf16, _lif_fwd, _side_stream, _split_eligible, _split_synapse, _transpose_bf16)
 
 # trace budget of a backward span (floats per buffer): the backward walks
 # whole checkpoint chunks, as many at a time as keep each per-span buffer
@@ -56,6 +56,17 @@ from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _cast_bf16, _gemm, _gemm_pa
 # one of 7,200 rows takes 256 x 256 tiles.  2^25, the one-layer budget,
 # keeps the route at half the modules' peak memory.
 _SPAN_ELEMS = 1 << 25
+
+
+def _ds_fused(prec: int, O: int, H: int, L: int) -> bool:
+    """The hidden reverse pass forms its spike gradient dS = G_o W_o^T
+    itself (myelin_linear_pre_bwd_readout: the fp32 small-K GEMM's sums,
+    without dS in memory) for fp32 products, a readout of at most 32
+    neurons, a hidden width that is a multiple of 256 and a span whose
+    G_o rows fit the kernel's 64 KB of LDS."""
+
+    kmax = next(k for k in (8, 12, 16, 20, 24, 32) if O <= k) if O <= 32 else 0
+    return prec == _lib.PREC["fp32"] and 0 < O <= 32 and H % 256 == 0 and L * kmax * 4 <= 65536
 
 
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
@@ -86,7 +97,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
     """Returns readout rates ``[B, O]`` = readout spike count / T."""
 
     @staticmethod
-    def forward(ctx: Any, x, wh, bh, wo, bo, decay, threshold, reset, sid, slope, C, prec, packed_hidden):
+    def forward(ctx: Any, x, wh, bh, wo, bo, decay, threshold, reset, sid, slope, C, prec, packed_hidden, lean=False):
         T, B, F = x.shape
         H = wh.shape[1]
         O = wo.shape[1]
@@ -106,8 +117,10 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         rates = torch.empty((B, O), device=dev)
         # the forward has no per-chunk state to keep beyond the checkpoints,
         # so it runs whole groups of chunks: a group's hidden currents fill
-        # up to 2**25 elements, as in the one-layer chunked path
-        G = max(1, min(K, _CURRENT_CHUNK_ELEMS // (L0 * B * H)))
+        # up to 2**25 elements, as in the one-layer chunked path (2**24 under
+        # the memory-lean policy: the forward's buffers stay below the
+        # backward's)
+        G = max(1, min(K, (_LEAN_FWD_ELEMS if lean else _CURRENT_CHUNK_ELEMS) // (L0 * B * H)))
         LG = min(G * C, T)
         # the packed variant never forms dense hidden spikes: its readout
         # GEMM reads the words
@@ -122,7 +135,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         # group's forward learns whether the input qualifies)
         split = None
         if not half and _split_eligible(prec, T, B, F, H):
-            split = _split_synapse(x, wh, stream)
+            split = _split_synapse(x, wh, stream, lean=lean)
             xs, wt = split.xb, split.w3
         for k in range(0, K, G):
             t0 = k * C
@@ -132,26 +145,30 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                      m_final=m_h, spikes=None if hs is None else hs[:L],
                      packed=None if words is None else words[t0:t1], ckpt=None if ck_h is None else ck_h[k:],
                      ckpt_every=C, wt=wt, exact=need, split=split if k == 0 else None,
-                     x32=x[t0:t1] if k == 0 else None)
+                     x32=x[t0:t1] if k == 0 else None, budget=LG * B * H)
             if k == 0 and split is not None and not split.exact():
                 xs, wt = x, None
             s_in = words[t0:t1] if hs is None else hs[:L]
             _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None if pre_o is None else pre_o[t0:t1], counts,
                            rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
                            stream, exact=need and not keep)
+        lazy = isinstance(xs, _LazyBf16)
         ctx.set_materialize_grads(False)
-        ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None)
+        ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None, lean, lazy)
         if need:
-            ctx.save_for_backward(xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_o)
+            # the lean split keeps x and casts each span's steps to bf16
+            ctx.save_for_backward(x if lazy else xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_o)
         return rates
 
     @staticmethod
     def backward(ctx: Any, g_rates):
-        none = (None,) * 13
+        none = (None,) * 14
         if g_rates is None or not any(ctx.needs_input_grad[:5]):
             return none
-        decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo = ctx.meta
+        decay, threshold, reset, sid, slope, C, prec, has_bh, has_bo, lean, lazy = ctx.meta
         xs, wh, bh, wo, bo, ck_h, ck_o, words, wt, pre_all = ctx.saved_tensors
+        if lazy:
+            xs = _LazyBf16(xs)
         parts = wt is not None and wt.ndim == 3  # exact split of the hidden synapse
         half = xs.dtype == torch.bfloat16 and not parts
         need_x, need_wh, need_bh, need_wo, need_bo = ctx.needs_input_grad[:5]
@@ -163,8 +180,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         K = math.ceil(T / C)
         # spans of `per` whole chunks (recomputed from the span's first
         # checkpoints, which the recurrences carry through the later ones
-        # exactly as the forward did)
-        per = max(1, min(K, _SPAN_ELEMS // (C * B * max(H, O))))
+        # exactly as the forward did); one chunk under the memory-lean policy
+        per = 1 if lean else max(1, min(K, _SPAN_ELEMS // (C * B * max(H, O))))
         S = per * C
         NS = math.ceil(T / S)
         L0 = min(S, T)
@@ -183,23 +200,44 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             cur = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             pre_o = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             G_o = torch.empty((L0, B, O), device=dev)
-            ghs = torch.empty((L0, B, H), device=dev) if need_hidden else None
-            G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
-                   if need_hidden else None)
+            # the memory-lean policy runs the recompute in turn on the one
+            # stream (one buffer set, and the recompute's currents reuse the
+            # dS buffer, which that span fills only after its recompute),
+            # and the hidden trace and dS (both spent once the hidden
+            # reverse pass has run) share one pool with the split-K
+            # workspace of the dX / dW_h GEMMs that follow it
+            recomputes = need_hidden or words is None
+            nset = 2 if (recomputes and NS > 1 and not lean) else 1
+            # dS formed inside the hidden reverse pass needs no buffer of its
+            # own (the lean recompute still borrows that pool slot)
+            fused_ds = need_hidden and _ds_fused(prec, O, H, L0)
+            pool = None
+            if lean and need_hidden:
+                n_ws = max(_lib.load().myelin_gemm_workspace_elems(F, H, L0 * B, _lib.PREC["bf16"] if parts else prec)
+                           if need_wh else 0,
+                           _lib.load().myelin_gemm_workspace_elems(L0 * B, F, H, prec) if need_x else 0)
+                pool = torch.empty(max(2 * L0 * B * H, n_ws), device=dev)
+                ghs = pool[L0 * B * H:2 * L0 * B * H].view(L0, B, H)
+            else:
+                ghs = torch.empty((L0, B, H), device=dev) if need_hidden and not fused_ds else None
             # exact split: dW_h reads G_h as three bf16 planes [3, L, B, H],
             # written by the reverse pass itself unless dX needs the fp32 G_h
             G3 = torch.empty(3 * L0 * B * H, dtype=torch.bfloat16, device=dev) if parts and need_wh else None
             if G3 is not None and not need_x:
                 G_h = G3
+            else:
+                G_h = (torch.empty((L0, B, H), dtype=torch.bfloat16 if half else torch.float32, device=dev)
+                       if need_hidden else None)
             # The hidden recompute (its trace, and spikes in the dense
             # variant) runs one span ahead on a side stream into two
             # alternating buffer sets, overlapping the current span's
             # readout and hidden reverse passes and GEMMs.  ready[i]: set i
             # holds its span; free[i]: the span using set i is done with it.
-            recomputes = need_hidden or words is None
-            nset = 2 if (recomputes and NS > 1) else 1
             hs_b = [None if words is not None else torch.empty((L0, B, H), device=dev) for _ in range(nset)]
-            pre_b = [torch.empty((L0, B, H), device=dev) if need_hidden else None for _ in range(nset)]
+            if pool is not None:
+                pre_b = [pool[:L0 * B * H].view(L0, B, H)]
+            else:
+                pre_b = [torch.empty((L0, B, H), device=dev) if need_hidden else None for _ in range(nset)]
             main = torch.cuda.current_stream(dev)
             side = _side_stream(dev) if nset == 2 else main
             ready = [torch.cuda.Event() for _ in range(nset)]
@@ -215,13 +253,15 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     if nset == 2 and j + 2 < NS:
                         side.wait_event(free[i])
                     pre_j = None if pre_b[i] is None else pre_b[i][:n]
+                    shared = ghs if (lean and nset == 1) else None
                     if words is not None:
                         _lif_fwd(xs[a0:a1], wh, bh, ck_h[j * per], 0, n, decay, threshold, reset, slope,
-                                 _lib.RULE_THRESHOLD, prec, side.cuda_stream, pre=pre_j, wt=wt, exact=True)
+                                 _lib.RULE_THRESHOLD, prec, side.cuda_stream, pre=pre_j, wt=wt, exact=True,
+                                 budget=L0 * B * H, cur=shared)
                     else:
                         _lif_fwd(xs[a0:a1], wh, bh, ck_h[j * per], 0, n, decay, threshold, reset, slope,
                                  _lib.RULE_THRESHOLD, prec, side.cuda_stream, spikes=hs_b[i][:n], pre=pre_j, wt=wt,
-                                 exact=True)
+                                 exact=True, budget=L0 * B * H, cur=shared)
                     ready[i].record(side)
 
             if recomputes:
@@ -233,8 +273,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 rows = L * B
                 i = k % nset
                 if recomputes:
-                    if nset == 2 and k > 0:
-                        hidden_recompute(k - 1)
+                    if nset == 2:
+                        if k > 0:
+                            hidden_recompute(k - 1)  # one span ahead, on the side stream
+                    elif k < NS - 1:
+                        hidden_recompute(k)  # one buffer set: this span's, in turn
                     main.wait_event(ready[i])
                 hs, pre_h = hs_b[i], pre_b[i]
                 s_in = words[t0:t1] if words is not None else hs[:L]
@@ -262,31 +305,40 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     if nset == 2:
                         free[i].record(main)  # dW_o was the last reader of the spikes
                     continue
-                # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this span
-                _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
-                _lib.call(
-                    "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h),
-                    _lib.DT_BF16X3 if G_h is G3 else _lib.DT[G_h.dtype],
-                    _lib.ptr(gbh_acc),
-                    L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
-                )
+                g_dt = _lib.DT_BF16X3 if G_h is G3 else _lib.DT[G_h.dtype]
+                if fused_ds:
+                    # the hidden reverse pass with dS = G_o @ W_o^T formed in place
+                    _lib.call(
+                        "myelin_linear_pre_bwd_readout",
+                        _lib.ptr(pre_h), _lib.ptr(G_o), _lib.ptr(wo), O, _lib.ptr(gm_h), _lib.ptr(G_h), g_dt,
+                        _lib.ptr(gbh_acc), L, B, H, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                    )
+                else:
+                    # dS[t0:t1] = G_o @ W_o^T, the hidden layer's spike gradient for this span
+                    _gemm(G_o, wo, ghs, rows, H, O, O, O, H, False, True, False, prec, stream)
+                    _lib.call(
+                        "myelin_linear_pre_bwd",
+                        _lib.ptr(pre_h), _lib.ptr(ghs), None, _lib.ptr(gm_h), _lib.ptr(G_h), g_dt,
+                        _lib.ptr(gbh_acc),
+                        L, B * H, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                    )
                 if nset == 2:
                     free[i].record(main)  # the trace's last reader (the spikes' was dW_o)
                 if gx is not None:
-                    _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream)
+                    _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream, ws=pool)
                 if gwh is not None:
                     if parts:
                         if G_h is not G3:
                             _lib.call("myelin_split_bf16x3", _lib.ptr(G_h), _lib.ptr(G3), rows, H, 0, stream)
                         _gemm_parts(xs[t0:t1], G3, 3, rows * H, gwh, F, H, rows, F, H, H, True, False, k != NS - 1,
-                                    stream)
+                                    stream, ws=pool)
                     else:
-                        _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream)
+                        _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream,
+                              ws=pool)
             if nset == 2:
                 # every side-stream kernel is behind a ready[] the main stream
                 # waited on; these tensors' last users include the side stream
-                for t_ in (*hs_b, *pre_b, xs, wh, ck_h, bh, wt):
+                for t_ in (*hs_b, *pre_b, xs.x if lazy else xs, wh, ck_h, bh, wt):
                     if t_ is not None:
                         t_.record_stream(side)
             gbh = gbo = None
@@ -296,12 +348,14 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             if gbo_acc is not None:
                 gbo = torch.empty((O,), device=dev)
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
-        return gx, gwh, gbh, gwo, gbo, None, None, None, None, None, None, None, None
+        return gx, gwh, gbh, gwo, gbo, None, None, None, None, None, None, None, None, None
 
 
 def two_layer_rate_forward(x, wh, bh, wo, bo, params, surrogate_id: int, slope: float, checkpoint: int,
-                           precision: str, packed_hidden: bool):
-    """Validate and run the chunk-interleaved two-layer rate network."""
+                           precision: str, packed_hidden: bool, lean: bool = False):
+    """Validate and run the chunk-interleaved two-layer rate network.
+    ``lean``: the memory-lean policy (forward groups and backward spans of
+    one checkpoint chunk; the split synapse casts the input per chunk)."""
 
     if checkpoint <= 0:
         raise ValueError("checkpoint_size must be positive")
@@ -332,5 +386,5 @@ def two_layer_rate_forward(x, wh, bh, wo, bo, params, surrogate_id: int, slope: 
         return HipTwoLayerRateFunction.apply(
             x.contiguous(), wh.contiguous(), c(bh), wo.contiguous(), c(bo), float(params.decay),
             float(params.threshold), float(params.reset), surrogate_id, float(slope), int(checkpoint),
-            _lib.PREC[precision], packed_hidden,
+            _lib.PREC[precision], packed_hidden, lean,
         )

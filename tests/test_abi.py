@@ -136,6 +136,21 @@ def test_split_synapse_entry_points_validate_on_the_host():
     with pytest.raises(ValueError, match="G must be float32, bfloat16 or three"):
         _lib.call("myelin_linear_pre_bwd", 16, None, None, 16, 16, 99, None, 4, 4, 4, 0.9, 1.0, 0.0, 5.0, 1, 0,
                   None)
+    # the spike-gradient-forming reverse pass: O, N, C x O and G's type
+    ro = ("myelin_linear_pre_bwd_readout", 16, 16, 16)
+    tail = (0.9, 1.0, 0.0, 5.0, 1, 0, None)
+    with pytest.raises(ValueError, match="O must be in"):
+        _lib.call(*ro, 33, 16, 16, 0, None, 4, 2, 256, *tail)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _lib.call(*ro, 20, 16, 16, 0, None, 4, 2, 200, *tail)
+    with pytest.raises(ValueError, match="G must be float32 or three"):
+        _lib.call(*ro, 20, 16, 16, _lib.DT[torch.bfloat16], None, 4, 2, 256, *tail)
+    with pytest.raises(ValueError, match="too large for the staged rows"):
+        _lib.call(*ro, 20, 16, 16, 0, None, 820, 2, 256, *tail)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("myelin_linear_pre_bwd_readout", 16, 16, None, 20, 16, 16, 0, None, 4, 2, 256, *tail)
+    with pytest.raises(ValueError, match="unknown surrogate"):
+        _lib.call(*ro, 20, 16, 16, 0, None, 4, 2, 256, 0.9, 1.0, 0.0, 5.0, 99, 0, None)
     # empty problems are valid no-ops
     assert _lib.load().myelin_split_bf16x3(None, None, 0, 5, 1, None) == 0
     assert _lib.load().myelin_gemm_parts(None, None, 3, 0, None, None, 0, 4, 4, 4, 4, 4, 0, 0, 0, None, 0,

@@ -209,3 +209,43 @@ def test_long_rate_rows_match_oracle(init):
     assert torch.equal(part["rates"].cpu(), full["rates"][:ROWS].cpu())
     _check_grads(init, {k: part[k].cpu() for k in GRADS}, part["hidden"].cpu(), part["rates"].cpu(), ref, truth,
                  GRADS, f"{ROWS} rows")
+
+
+def _packed_step_peak(x, labels, wh, bh, wo, bo, checkpoint_size):
+    """One packed-route training step; returns (rates, grads, peak bytes
+    allocated during the step beyond what was allocated before it)."""
+
+    dev = torch.device(DEV)
+    xd = x.to(dev)
+    whd, bhd, wod, bod = (t.to(dev).requires_grad_() for t in (wh, bh, wo, bo))
+    lab = labels.to(dev)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    rates = myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(
+        xd, whd, bhd, wod, bod, P, surrogate="superspike", surrogate_slope=10.0, checkpoint_size=checkpoint_size)
+    torch.nn.functional.cross_entropy(rates * T, lab, reduction="sum").div(B).backward()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    return rates.detach().cpu(), [t.grad.cpu() for t in (whd, bhd, wod, bod)], peak
+
+
+def test_memory_policy_is_lean_and_equal_to_the_fast_buffers():
+    """checkpoint_size="memory" (45 at T=2000) keeps the packed route's chunk
+    and span buffers to one checkpoint chunk and casts the input to bf16 per
+    chunk: at most 250 MB above the inputs for the whole training step.
+    An explicit checkpoint_size=45 takes the larger, faster buffers; the
+    same rates, and gradients within 1e-5 (the weight gradients sum the
+    spans' products in other groupings)."""
+
+    print("case: long_rate packed route, memory policy vs checkpoint 45", flush=True)
+    x, labels, wh, bh, wo, bo = _case("kaiming")
+    r_lean, g_lean, peak_lean = _packed_step_peak(x, labels, wh, bh, wo, bo, "memory")
+    r_fast, g_fast, peak_fast = _packed_step_peak(x, labels, wh, bh, wo, bo, 45)
+    print(f"peak step bytes: memory policy {peak_lean / 2**20:.0f} MiB, checkpoint 45 {peak_fast / 2**20:.0f} MiB",
+          flush=True)
+    assert peak_lean <= 250 * 10**6
+    assert peak_lean < peak_fast
+    assert torch.equal(r_lean, r_fast)
+    for name, a, b in zip(("gwh", "gbh", "gwo", "gbo"), g_lean, g_fast):
+        assert_norm_close(a, b, 1e-5, name)

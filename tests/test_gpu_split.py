@@ -240,7 +240,7 @@ def test_split_layer_matches_oracle_and_fp32_engine(monkeypatch, ck, rate, need_
     go = torch.randn((B, N) if rate else (T, B, N), generator=g)
     calls = []
     real = L._split_synapse
-    monkeypatch.setattr(L, "_split_synapse", lambda *a: calls.append(1) or real(*a))
+    monkeypatch.setattr(L, "_split_synapse", lambda *a, **k: calls.append(1) or real(*a, **k))
     monkeypatch.setattr(L, "_SPLIT_MIN_MACS", 0)
     got = _run_layer(x, w, b, go, ck, rate, need_x)
     assert calls, "the split path did not run"
@@ -332,7 +332,7 @@ def test_two_layer_hidden_split_matches_fp32_engine_and_oracle(monkeypatch, vari
     p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
     calls = []
     real = TL._split_synapse
-    monkeypatch.setattr(TL, "_split_synapse", lambda *a: calls.append(1) or real(*a))
+    monkeypatch.setattr(TL, "_split_synapse", lambda *a, **k: calls.append(1) or real(*a, **k))
     res = []
     for min_macs in (0, 1 << 62):
         monkeypatch.setattr(L, "_SPLIT_MIN_MACS", min_macs)
@@ -506,7 +506,7 @@ def test_split_synapse_is_not_used_under_graph_capture():
 
     calls = []
     real = L._split_synapse
-    L._split_synapse = lambda *a: calls.append(1) or real(*a)
+    L._split_synapse = lambda *a, **k: calls.append(1) or real(*a, **k)
     try:
         _, s_eager_split = fwd()  # eager: the split runs
         assert calls, "the split path did not run eagerly"

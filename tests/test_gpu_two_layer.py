@@ -206,3 +206,92 @@ def test_two_layer_bf16_synapse_within_tolerance():
     assert abs(loss.item() - (rr * grate).sum().item()) <= 2e-2 * max(1.0, abs(loss.item()))
     for name, a, b in zip(("wh", "bh", "wo", "bo"), leaves[1:], leaves_r[1:]):
         assert_norm_close(to_np(a.grad), b.grad, 2e-2, f"grad_{name}")
+
+
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
+def test_memory_policy_spans_equal_one_span(variant):
+    """checkpoint_size="memory" walks the backward one checkpoint chunk at a
+    time (T=40: 7-step chunks, 6 spans, one buffer set); an explicit
+    checkpoint_size=7 walks one span.  Same rates, gradients within 1e-5."""
+
+    T, B, F, H, O = 40, 3, 24, 37, 5
+    _print_case(test="two_layer_memory_policy", variant=variant)
+    tensors, grate = _random_net(77, T, B, F, H, O)
+    p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
+    out = {}
+    for ck in ("memory", 7):
+        r, leaves = _run(VARIANTS[variant], tensors, True, p, surrogate="fast_sigmoid", surrogate_slope=5.0,
+                         checkpoint_size=ck)
+        r.backward(grate.to(DEV))
+        out[ck] = (to_np(r), _grads(leaves))
+    assert np.array_equal(out["memory"][0], out[7][0])
+    for a, b, name in zip(out["memory"][1], out[7][1], ("gx", "gwh", "gbh", "gwo", "gbo")):
+        assert_norm_close(a, b, 1e-5, name)
+
+
+def test_linear_memory_policy_spans_equal_one_span():
+    """The one-layer streamed-synapse path: "memory" (one-chunk spans) and
+    the explicit chunk size give the same spikes and input gradient, and
+    weight gradients within 1e-6."""
+
+    _print_case(test="linear_memory_policy")
+    (x, wh, bh, _, _), _ = _random_net(78, 40, 3, 24, 37, 5)
+    gs = torch.randn(40, 3, 37, generator=seeded(79))
+    p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
+    out = {}
+    for ck in ("memory", 7):
+        xd, wd, bd = (t.to(DEV).requires_grad_() for t in (x, wh, bh))
+        _, s = myelin.linear_surrogate_lif_forward(xd, wd, bd, p, surrogate="atan", surrogate_slope=5.0,
+                                                   checkpoint_size=ck)
+        s.backward(gs.to(DEV))
+        out[ck] = (to_np(s), to_np(xd.grad), to_np(wd.grad), to_np(bd.grad))
+    assert np.array_equal(out["memory"][0], out[7][0]) and np.array_equal(out["memory"][1], out[7][1])
+    assert_norm_close(out["memory"][2], out[7][2], 1e-6, "grad_w")
+    assert_norm_close(out["memory"][3], out[7][3], 1e-6, "grad_b")
+
+
+# (T, B, F, H, O, checkpoint, split, x_grad): one and two neurons per lane
+# (B x H below / at 65536), G written as fp32 (dX needs it) and as the three
+# bf16 planes of the exact split, readouts of 5, 12, 20 and 32 neurons (the
+# 8-, 12-, 20- and 32-term sums), a ragged last span under "memory"
+DS_CASES = [(23, 4, 40, 256, 5, 5, False, True), (23, 4, 40, 512, 20, "memory", True, False),
+            (19, 128, 32, 512, 32, 5, False, True), (19, 128, 32, 1024, 12, 4, True, False)]
+
+
+@pytest.mark.parametrize("case", DS_CASES)
+def test_fused_spike_gradient_equals_the_ds_gemm(case, monkeypatch):
+    """The hidden reverse pass that forms dS = G_o W_o^T itself
+    (myelin_linear_pre_bwd_readout) takes the small-K GEMM's sums, so the
+    packed network's rates and every gradient equal those of the route that
+    writes dS with that GEMM and reads it back, bit for bit."""
+
+    from myelin_amd import _lib, linear, two_layer
+
+    T, B, F, H, O, ck, split, x_grad = case
+    _print_case(test="fused_ds", case=case)
+    tensors, grate = _random_net(91 + H + O, T, B, F, H, O)
+    tensors[0] = (torch.rand(T, B, F, generator=seeded(92)) < 0.2).float()  # spikes: bf16-exact
+    if split:
+        monkeypatch.setattr(linear, "_SPLIT_MIN_MACS", 0)
+    p = myelin.LIFParams(tau_mem=8.0, threshold=0.7, reset=-0.2)
+    real, names = _lib.call, []
+    monkeypatch.setattr(_lib, "call", lambda name, *a: names.append(name) or real(name, *a))
+
+    def run():
+        names.clear()
+        x, wh, bh, wo, bo = (t.to(DEV) for t in tensors)
+        leaves = [x.requires_grad_(x_grad), *(t.requires_grad_() for t in (wh, bh, wo, bo))]
+        r = myelin.two_layer_surrogate_lif_rate_packed_hidden_forward(*leaves, p, surrogate="superspike",
+                                                                     surrogate_slope=5.0, checkpoint_size=ck)
+        r.backward(grate.to(DEV))
+        torch.cuda.synchronize()
+        return [to_np(r)] + [to_np(t.grad) for t in leaves if t.requires_grad], list(names)
+
+    fused, called = run()
+    assert "myelin_linear_pre_bwd_readout" in called
+    assert ("myelin_split_bf16x3" in called) == split
+    monkeypatch.setattr(two_layer, "_ds_fused", lambda *a: False)
+    gemm, called = run()
+    assert "myelin_linear_pre_bwd_readout" not in called
+    for a, b in zip(fused, gemm):
+        assert np.array_equal(a, b)
