@@ -161,15 +161,21 @@ def _timed(torch, step, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+# eager steps timed beside a graph replay: at least this many, so that the
+# first step's wait for the host's first launches (the timed region starts
+# from an idle GPU) does not stand for the steady state of a training loop
+EAGER_MIN_STEPS = 100
+
+
 def _graph_timed(torch, body, params, steps, warmup):
     """ms per step of `body()` (forward + backward of a training step,
     gradients set to None first) replayed from one captured HIP graph: the
     same kernels in the same order as an eager step, launched without the
     host's per-op work.  The capture follows torch's whole-network recipe:
     warm up on a side stream, drop the gradients, capture.  Returns
-    (ms, eager ms)."""
+    (ms, eager ms over max(steps, EAGER_MIN_STEPS) steps)."""
 
-    eager = _timed(torch, lambda: (_none(params), body()), steps, warmup)
+    eager = _timed(torch, lambda: (_none(params), body()), max(steps, EAGER_MIN_STEPS), warmup)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -493,7 +499,8 @@ def _workload_linear_bf16(torch, myelin, args, threads):
                            "traffic": _traffic("linear_bf16_T50_B256_F784_N2048", "linear_lif_fwd_pipe"),
                            "flops_per_launch": fwd_flops, "kernel_ms": kern_ms},
                  step_tflops=tflops, step_frac_of_bf16_peak=tflops / BF16_PEAK_TFLOPS, dtype="bf16",
-                 timing="HIP graph replay of the whole step (forward, loss, backward)", eager_ms_per_step=eager_ms)
+                 timing="HIP graph replay of the whole step (forward, loss, backward)", eager_ms_per_step=eager_ms,
+                 eager_steps=max(args.steps, EAGER_MIN_STEPS), eager_over_graph=eager_ms / ms)
     if not args.no_cpu_baseline:
         R = _oracle()
         sb = 32

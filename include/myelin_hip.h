@@ -286,6 +286,36 @@ int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts,
                       float *workspace, int64_t workspace_elems,
                       myelin_stream_t stream);
 
+/*
+ * myelin_gemm / myelin_gemm_parts followed by an independent column sum
+ * cs_out[n] = sum_r cs_in[r, n] over [cs_rows, cs_cols] (as
+ * myelin_col_sum_f32 with accumulate = 0, same bits): its workgroups join
+ * the GEMM's split-K reduce launch when K is split, else it runs as a
+ * launch of its own after the GEMM -- the weight and bias gradients of a
+ * layer in one launch fewer.  cs_in must not be written by the GEMM nor
+ * cs_out read by it.  cs_cols = 0 attaches nothing.
+ * Replaces: grad_weight and grad_bias of the Functions' backward
+ *   (autograd.py:553-556,712-715) and
+ *   _linear_surrogate_lif_backward_weight_kernel /
+ *   _linear_surrogate_lif_backward_bias_kernel (triton/lif.py:1136-1258).
+ */
+int myelin_gemm_col_sum(const void *A, int a_dtype, const void *B,
+                        int b_dtype, const float *bias, float *C, int64_t M,
+                        int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                        int64_t ldc, int trans_a, int trans_b, int accumulate,
+                        int precision, float *workspace,
+                        int64_t workspace_elems, const float *cs_in,
+                        float *cs_out, int64_t cs_rows, int64_t cs_cols,
+                        myelin_stream_t stream);
+int myelin_gemm_parts_col_sum(const uint16_t *A, const uint16_t *B, int parts,
+                              int64_t b_part, const float *bias, float *C,
+                              int64_t M, int64_t N, int64_t K, int64_t lda,
+                              int64_t ldb, int64_t ldc, int trans_a,
+                              int trans_b, int accumulate, float *workspace,
+                              int64_t workspace_elems, const float *cs_in,
+                              float *cs_out, int64_t cs_rows, int64_t cs_cols,
+                              myelin_stream_t stream);
+
 /* floats of device scratch myelin_gemm_noalloc holds per GPU (64 MiB) */
 #define MYELIN_NOALLOC_SCRATCH_ELEMS (16LL * 1024 * 1024)
 
@@ -361,6 +391,15 @@ int myelin_cast_bf16(const float *src, uint16_t *dst, int64_t n,
                      myelin_stream_t stream);
 int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows,
                           int64_t cols, myelin_stream_t stream);
+
+/*
+ * myelin_cast_bf16(x, xb, n) and myelin_transpose_bf16(w, wt, rows, cols)
+ * in one launch (same bits): the bf16 synapse's two operand copies.  No
+ * counterpart in the reference.
+ */
+int myelin_cast_transpose_bf16(const float *x, uint16_t *xb, int64_t n,
+                               const float *w, uint16_t *wt, int64_t rows,
+                               int64_t cols, myelin_stream_t stream);
 
 /*
  * myelin_cast_bf16 that also sets *inexact = 1 (never clears it) when some

@@ -59,14 +59,19 @@ SIGNATURES: dict[str, list] = {
     "myelin_counts_to_rate": [_P, _P, _INT, _I64, _I64, _P],
     "myelin_gemm_f32": [_P, _P, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P],
     "myelin_gemm": [_P, _INT, _P, _INT, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P],
+    "myelin_gemm_col_sum": [_P, _INT, _P, _INT, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P, _I64, _P, _P, _I64, _I64,
+                                                                                     _P],
     "myelin_linear_lif_fwd": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_linear_lif_fwd_bf16": [_P] * 10 + [_I64] * 7 + [_F] * 4 + [_INT, _P],
     "myelin_cast_bf16": [_P, _P, _I64, _P],
     "myelin_cast_bf16_checked": [_P, _P, _I64, _P, _P],
     "myelin_split_bf16x3": [_P, _P, _I64, _I64, _INT, _P],
     "myelin_gemm_parts": [_P, _P, _INT, _I64, _P, _P] + [_I64] * 6 + [_INT] * 3 + [_P, _I64, _P],
+    "myelin_gemm_parts_col_sum": [_P, _P, _INT, _I64, _P, _P] + [_I64] * 6 + [_INT] * 3 + [_P, _I64, _P, _P, _I64,
+                                                                                          _I64, _P],
     "myelin_gemm_noalloc": [_P, _INT, _P, _INT, _P, _P] + [_I64] * 6 + [_INT] * 4 + [_P],
     "myelin_transpose_bf16": [_P, _P, _I64, _I64, _P],
+    "myelin_cast_transpose_bf16": [_P, _P, _I64, _P, _P, _I64, _I64, _P],
     "myelin_linear_pre_bwd": [_P] * 5 + [_INT, _P] + [_I64] * 3 + [_F] * 4 + [_INT, _INT, _P],
     "myelin_linear_pre_bwd_readout": [_P] * 3 + [_INT] + [_P] * 2 + [_INT, _P] + [_I64] * 3 + [_F] * 4
     + [_INT, _INT, _P],

@@ -339,6 +339,12 @@ struct GemmArgs {
   // at the first part summed; b_part may be negative)
   int parts = 1;
   int64_t b_part = 0;
+  // an independent column sum cs_out[n] = sum_r cs_in[r, n] ([cs_rows,
+  // cs_cols]) run by extra workgroups of the split-K reduce launch (from
+  // red_blocks on), or after the GEMM when K is not split
+  const float *cs_in = nullptr;
+  float *cs_out = nullptr;
+  int64_t cs_rows = 0, cs_cols = 0, red_blocks = 0;
 };
 
 // Writes one wave's 32 x 32 accumulator tile (rows row0 + acc_row(r, lane),
@@ -425,10 +431,36 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   store_acc(g, acc, m0 + 32 * wm, n0 + 32 * wn + (lane & 31), lane, blockIdx.z);
 }
 
+// out[n] (+)= sum_r in[r, n], in a fixed order (deterministic).
+// 8 columns per workgroup (a 2048-column sum spreads over 256 CUs): thread
+// (column c = tid % 8, group q = tid / 8) sums rows q, q + 32, ... in order,
+// then the 32 group sums are added in group order
+__device__ __forceinline__ void col_sum_block(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
+                                              int64_t cols, int accumulate, int64_t block) {
+  __shared__ float part[32][8];
+  const int c = threadIdx.x & 7, q = threadIdx.x >> 3;
+  const int64_t n = block * 8 + c;
+  float s = 0.0f;
+  if (n < cols)
+    for (int64_t r = q; r < rows; r += 32) s = s + in[r * cols + n];
+  part[q][c] = s;
+  __syncthreads();
+  if (q == 0 && n < cols) {
+    float t = 0.0f;
+    for (int i = 0; i < 32; ++i) t = t + part[i][c];
+    out[n] = accumulate ? out[n] + t : t;
+  }
+}
+
 // C (+)= sum over splits of the workspace planes (+ bias), four consecutive
 // columns per thread (N, ldc, C and the workspace all allow 16-byte
-// access): one 16-byte load per plane, adds in split order.
+// access): one 16-byte load per plane, adds in split order.  Workgroups
+// from g.red_blocks on run the attached column sum instead.
 __global__ __launch_bounds__(256) void splitk_reduce4(GemmArgs g) {
+  if (static_cast<int64_t>(blockIdx.x) >= g.red_blocks) {
+    col_sum_block(g.cs_in, g.cs_out, g.cs_rows, g.cs_cols, 0, blockIdx.x - g.red_blocks);
+    return;
+  }
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (i >= g.M * g.N) return;
   const int64_t row = i / g.N, col = i - row * g.N;
@@ -452,6 +484,10 @@ __global__ __launch_bounds__(256) void splitk_reduce4(GemmArgs g) {
 }
 
 __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
+  if (static_cast<int64_t>(blockIdx.x) >= g.red_blocks) {
+    col_sum_block(g.cs_in, g.cs_out, g.cs_rows, g.cs_cols, 0, blockIdx.x - g.red_blocks);
+    return;
+  }
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= g.M * g.N) return;
   const int64_t row = i / g.N, col = i - row * g.N;
@@ -467,14 +503,17 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs g) {
   *dst = v;
 }
 
-// the split-K reduce: four columns per thread where rows and pointers allow
-void launch_reduce(const GemmArgs &g, hipStream_t s) {
+// the split-K reduce: four columns per thread where rows and pointers allow,
+// with the attached column sum's workgroups after the reduce's
+void launch_reduce(GemmArgs g, hipStream_t s) {
   const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && myelin::aligned(g.C, 16) && myelin::aligned(g.ws, 16);
   const int64_t n = g.M * g.N;
+  g.red_blocks = v4 ? (n / 4 + 255) / 256 : (n + 255) / 256;
+  const int64_t blocks = g.red_blocks + (g.cs_in != nullptr ? (g.cs_cols + 7) / 8 : 0);
   if (v4)
-    splitk_reduce4<<<dim3((n / 4 + 255) / 256), dim3(256), 0, s>>>(g);
+    splitk_reduce4<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(g);
   else
-    splitk_reduce<<<dim3((n + 255) / 256), dim3(256), 0, s>>>(g);
+    splitk_reduce<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(g);
 }
 
 // Three bf16 values whose float sum is exactly v: h = bf16(v) (nearest
@@ -2885,18 +2924,21 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
 // (dS = G_o W_o^T), summed in o order with fused multiply-adds from zero
 // over KMAX terms (zero past O) -- the small-K GEMM's arithmetic, so G is
 // the one dS written by that GEMM and read back gives, without dS's write
-// and read ([C, B, N] floats each way).  A workgroup's 256 V neurons lie in
-// one batch row b (N a multiple of 256 V): it stages that row's G_o [C, O]
-// in LDS, zero-padded to KMAX columns, and each step's row reaches every
-// lane as broadcast 16-byte LDS reads.  A lane holds its V neurons' rows of
-// W_o (V x KMAX registers).  The reverse walk is linear_pre_bwd's, with the
-// pre-reset trace the one operand streamed from HBM.
-template <int SID, int GM, int V, int KMAX>
+// and read ([C, B, N] floats each way).  A workgroup's 256 neurons lie in
+// one batch row b (N a multiple of 256): it stages that row's G_o [C, O] in
+// LDS, zero-padded to KMAX columns, and each step's row reaches every lane
+// as broadcast 16-byte LDS reads.  A lane holds its neuron's row of W_o
+// (KMAX registers).  The reverse walk is linear_pre_bwd's, with the
+// pre-reset trace the one operand streamed from HBM, 8 steps ahead.  One
+// neuron per lane: at 131072 neurons x 225 steps (config 4's hidden span)
+// 79 us, against 100-108 us for two per lane (one wave per SIMD) with 4 or
+// 8 steps ahead; 16 steps ahead 82 us.
+template <int SID, int GM, int KMAX>
 __global__ __launch_bounds__(256) void linear_pre_bwd_ds(PreBwdArgs p, const float *go, const float *wo, int O,
                                                          int64_t N) {
   extern __shared__ __attribute__((aligned(16))) float s_go[];  // [C][KMAX]
+  constexpr int V = 1, DEPTH = 8;
   using VT = typename PreVec<V>::T;
-  constexpr int DEPTH = V == 2 ? 4 : kPipe;
   const int64_t C = p.C, row = p.BN / V;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * V);
   const int64_t bi = base / N, Bn = p.BN / N;
@@ -2933,12 +2975,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd_ds(PreBwdArgs p, const flo
 #pragma unroll
         for (int e = 0; e < V; ++e) acc[e] = __builtin_fmaf(g4[u], w[e][4 * q + u], acc[e]);
     }
-    VT gsv;
-    if constexpr (V == 2)
-      gsv = float2{acc[0], acc[1]};
-    else
-      gsv = acc[0];
-    pre_bwd_step<SID, true, GM, V>(p, i, j, pv, gsv, gstep, gm, gb);
+    pre_bwd_step<SID, true, GM, V>(p, i, j, pv, acc[0], gstep, gm, gb);
   };
   const VT *pre = reinterpret_cast<const VT *>(p.pre + i);
   const int64_t nblk = (C + DEPTH - 1) / DEPTH;
@@ -2976,25 +3013,11 @@ __global__ __launch_bounds__(256) void linear_pre_bwd_ds(PreBwdArgs p, const flo
   }
 }
 
-// out[n] (+)= sum_r in[r, n], in a fixed order (deterministic).
-// 8 columns per workgroup (a 2048-column sum spreads over 256 CUs): thread
-// (column c = tid % 8, group q = tid / 8) sums rows q, q + 32, ... in order,
-// then the 32 group sums are added in group order
+// out[n] (+)= sum_r in[r, n] for the 8 columns of workgroup `block` (see
+// col_sum_block)
 __global__ __launch_bounds__(256) void col_sum(const float *__restrict__ in, float *__restrict__ out, int64_t rows,
                                                int64_t cols, int accumulate) {
-  __shared__ float part[32][8];
-  const int c = threadIdx.x & 7, q = threadIdx.x >> 3;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 8 + c;
-  float s = 0.0f;
-  if (n < cols)
-    for (int64_t r = q; r < rows; r += 32) s = s + in[r * cols + n];
-  part[q][c] = s;
-  __syncthreads();
-  if (q == 0 && n < cols) {
-    float t = 0.0f;
-    for (int i = 0; i < 32; ++i) t = t + part[i][c];
-    out[n] = accumulate ? out[n] + t : t;
-  }
+  col_sum_block(in, out, rows, cols, accumulate, blockIdx.x);
 }
 
 // LIF recurrence over precomputed currents cur [t_end - t_begin, B, N]
@@ -3421,7 +3444,8 @@ void launch_smallk(const GemmArgs &g, int ta, int tb, dim3 grid, hipStream_t s) 
 }
 
 template <int PREC>
-int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s, bool bits = false) {
+int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStream_t s, bool bits = false,
+                bool *reduced = nullptr) {
   constexpr int KS = Prec<PREC>::KS;
   if (!half && g.N <= 32) {
     // narrow output (readout currents, dW_o): stream A once
@@ -3454,6 +3478,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
     if (int rc = myelin::launched("gemm (narrow)")) return rc;
     if (splits > 1) {
       launch_reduce(g, s);
+      if (reduced != nullptr) *reduced = true;
       return myelin::launched("gemm split-k reduce");
     }
     return MYELIN_OK;
@@ -3488,6 +3513,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
         launch_dma_mn_wide(g, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), s);
         if (int rc = myelin::launched("gemm (mn-contiguous, 256 x 256 tiles)")) return rc;
         launch_reduce(g, s);
+        if (reduced != nullptr) *reduced = true;
         return myelin::launched("gemm split-k reduce");
       }
     }
@@ -3541,6 +3567,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   if (int rc = myelin::launched("gemm")) return rc;
   if (splits > 1) {
     launch_reduce(g, s);
+    if (reduced != nullptr) *reduced = true;
     return myelin::launched("gemm split-k reduce");
   }
   return MYELIN_OK;
@@ -3587,38 +3614,28 @@ constexpr int64_t kPreBwdDsLds = 65536;  // bytes of staged G_o rows per workgro
 
 int pre_bwd_ds_kmax(int O) { return O <= 8 ? 8 : O <= 12 ? 12 : O <= 16 ? 16 : O <= 20 ? 20 : O <= 24 ? 24 : 32; }
 
-template <int SID, int GM, int V>
+template <int SID, int GM>
 void launch_pre_bwd_ds_k(const PreBwdArgs &a, const float *go, const float *wo, int O, int64_t N, hipStream_t s) {
   const int kmax = pre_bwd_ds_kmax(O);
-  const dim3 grid(static_cast<unsigned>(a.BN / (256 * V)));
+  const dim3 grid(static_cast<unsigned>(a.BN / 256));
   const size_t lds = static_cast<size_t>(a.C) * kmax * sizeof(float);
   switch (kmax) {
-    case 8: linear_pre_bwd_ds<SID, GM, V, 8><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
-    case 12: linear_pre_bwd_ds<SID, GM, V, 12><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
-    case 16: linear_pre_bwd_ds<SID, GM, V, 16><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
-    case 20: linear_pre_bwd_ds<SID, GM, V, 20><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
-    case 24: linear_pre_bwd_ds<SID, GM, V, 24><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
-    default: linear_pre_bwd_ds<SID, GM, V, 32><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 8: linear_pre_bwd_ds<SID, GM, 8><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 12: linear_pre_bwd_ds<SID, GM, 12><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 16: linear_pre_bwd_ds<SID, GM, 16><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 20: linear_pre_bwd_ds<SID, GM, 20><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    case 24: linear_pre_bwd_ds<SID, GM, 24><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
+    default: linear_pre_bwd_ds<SID, GM, 32><<<grid, dim3(256), lds, s>>>(a, go, wo, O, N); break;
   }
 }
 
-// two neurons per lane on the wide grids, as launch_pre_bwd chooses
 template <int SID>
 void launch_pre_bwd_ds(const PreBwdArgs &a, int gm, const float *go, const float *wo, int O, int64_t N,
                        hipStream_t s) {
-  const bool v2 = a.BN >= 65536 && N % 512 == 0 && myelin::aligned(a.pre, 8) && myelin::aligned(a.gm, 8) &&
-                  myelin::aligned(a.gbias_acc, 8) && myelin::aligned(a.G, gm == 0 ? 8 : 4);
-  if (v2) {
-    if (gm == 2)
-      launch_pre_bwd_ds_k<SID, 2, 2>(a, go, wo, O, N, s);
-    else
-      launch_pre_bwd_ds_k<SID, 0, 2>(a, go, wo, O, N, s);
-  } else {
-    if (gm == 2)
-      launch_pre_bwd_ds_k<SID, 2, 1>(a, go, wo, O, N, s);
-    else
-      launch_pre_bwd_ds_k<SID, 0, 1>(a, go, wo, O, N, s);
-  }
+  if (gm == 2)
+    launch_pre_bwd_ds_k<SID, 2>(a, go, wo, O, N, s);
+  else
+    launch_pre_bwd_ds_k<SID, 0>(a, go, wo, O, N, s);
 }
 
 template <bool PRE, bool SPK, bool PK>
@@ -3676,12 +3693,41 @@ extern "C" int64_t myelin_gemm_workspace_elems(int64_t M, int64_t N, int64_t K, 
   return most > 1 ? most * M * N : 0;
 }
 
-extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype, const float *bias, float *C,
-                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a,
-                           int trans_b, int accumulate, int precision, float *workspace, int64_t workspace_elems,
-                           myelin_stream_t stream) {
+namespace {
+// the column sum attached to a GEMM, as a launch of its own when no split-K
+// reduce launch has run it
+int run_col_sum(const float *in, float *out, int64_t rows, int64_t cols, hipStream_t s) {
+  if (cols == 0) return MYELIN_OK;
+  col_sum<<<dim3(static_cast<unsigned>(cdiv(cols, 8))), dim3(256), 0, s>>>(in, out, rows, cols, 0);
+  return myelin::launched("col_sum");
+}
+
+int col_sum_after(const GemmArgs &g, bool reduced, hipStream_t s) {
+  if (g.cs_in == nullptr || reduced) return MYELIN_OK;
+  return run_col_sum(g.cs_in, g.cs_out, g.cs_rows, g.cs_cols, s);
+}
+
+int check_col_sum(const float *cs_in, float *cs_out, int64_t cs_rows, int64_t cs_cols) {
+  if (cs_rows < 0 || cs_cols < 0) return myelin::invalid("col_sum: negative size");
+  if (cs_cols > 0 && (cs_out == nullptr || (cs_rows > 0 && cs_in == nullptr)))
+    return myelin::invalid("col_sum: null pointer");
+  if (cdiv(cs_cols, 8) > 0x3fffffff) return myelin::invalid("col_sum: too many columns");
+  return MYELIN_OK;
+}
+
+int gemm_impl(const void *A, int a_dtype, const void *B, int b_dtype, const float *bias, float *C, int64_t M,
+              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b, int accumulate,
+              int precision, float *workspace, int64_t workspace_elems, const float *cs_in, float *cs_out,
+              int64_t cs_rows, int64_t cs_cols, myelin_stream_t stream) {
   if (M < 0 || N < 0 || K < 0) return myelin::invalid("gemm: negative size");
-  if (M == 0 || N == 0) return MYELIN_OK;
+  GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
+  if (cs_cols > 0) {
+    g.cs_in = cs_in;
+    g.cs_out = cs_out;
+    g.cs_rows = cs_rows;
+    g.cs_cols = cs_cols;
+  }
+  if (M == 0 || N == 0) return col_sum_after(g, false, myelin::as_hip(stream));
   if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm: null pointer");
   if (ldc < N) return myelin::invalid("gemm: ldc < N");
   if ((a_dtype != MYELIN_DT_BITS && (trans_a ? lda < M : lda < K)) || (trans_b ? ldb < K : ldb < N))
@@ -3703,25 +3749,27 @@ extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtyp
     if (!bf16_aligned(A, lda, !trans_a) || !bf16_aligned(B, ldb, trans_b != 0))
       return myelin::invalid("gemm: bfloat16 operand rows must be 16-byte (k-contiguous) or 8-byte aligned");
   }
-  GemmArgs g{A, B, bias, C, workspace_elems > 0 ? workspace : nullptr, M, N, K, lda, ldb, ldc, 0, accumulate, 1};
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;
     launch_reduce(g, myelin::as_hip(stream));
     return myelin::launched("gemm (K = 0)");
   }
   hipStream_t s = myelin::as_hip(stream);
-  if (precision == MYELIN_PREC_BF16) return launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s, bits);
-  return launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s, bits);
+  bool reduced = false;
+  const int rc = precision == MYELIN_PREC_BF16
+                     ? launch_gemm<1>(g, trans_a, trans_b, half, workspace_elems, s, bits, &reduced)
+                     : launch_gemm<0>(g, trans_a, trans_b, false, workspace_elems, s, bits, &reduced);
+  return rc != MYELIN_OK ? rc : col_sum_after(g, reduced, s);
 }
 
-extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts, int64_t b_part, const float *bias,
-                                 float *C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                 int trans_a, int trans_b, int accumulate, float *workspace, int64_t workspace_elems,
-                                 myelin_stream_t stream) {
+int gemm_parts_impl(const uint16_t *A, const uint16_t *B, int parts, int64_t b_part, const float *bias, float *C,
+                    int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a, int trans_b,
+                    int accumulate, float *workspace, int64_t workspace_elems, const float *cs_in, float *cs_out,
+                    int64_t cs_rows, int64_t cs_cols, myelin_stream_t stream) {
   if (parts < 1 || parts > 8) return myelin::invalid("gemm_parts: parts must be in [1, 8]");
   if (parts > 1 && b_part < 0) return myelin::invalid("gemm_parts: negative part stride");
   if (M < 0 || N < 0 || K < 0) return myelin::invalid("gemm_parts: negative size");
-  if (M == 0 || N == 0) return MYELIN_OK;
+  if (M == 0 || N == 0) return run_col_sum(cs_in, cs_out, cs_rows, cs_cols, myelin::as_hip(stream));
   if (A == nullptr || B == nullptr || C == nullptr) return myelin::invalid("gemm_parts: null pointer");
   if (ldc < N) return myelin::invalid("gemm_parts: ldc < N");
   if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N)) return myelin::invalid("gemm_parts: bad leading dim");
@@ -3735,20 +3783,65 @@ extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts
   // then accumulate while the running sum is small, and only the largest
   // plane's products round against the full-size sum, as in a plain fp32
   // GEMM.  Summed largest first, each of the three planes' products rounds
-  // against the full sum: config 4's currents [8000 x 4096 x 1024] measured
-  // 5.3e-7 (max) / 2.9e-8 (rms) from float64 that way, 6.8e-8 / 6.1e-9 this
-  // way (a CPU sgemm: 1.5e-7 / 1.3e-8).
+  // against the full sum: the currents of a 1024 -> 4096 synapse over 8000
+  // rows of spikes measured 5.3e-7 (max) / 2.9e-8 (rms) from float64 that
+  // way, 6.8e-8 / 6.1e-9 this way (a CPU sgemm: 1.5e-7 / 1.3e-8).
   GemmArgs g{A, B + (parts - 1) * b_part, bias, C, workspace_elems > 0 ? workspace : nullptr,
              M, N, K, lda, ldb, ldc, 0, accumulate, 1};
   g.parts = parts;
   g.b_part = -b_part;
+  if (cs_cols > 0) {
+    g.cs_in = cs_in;
+    g.cs_out = cs_out;
+    g.cs_rows = cs_rows;
+    g.cs_cols = cs_cols;
+  }
   hipStream_t s = myelin::as_hip(stream);
   if (K == 0) {  // C = (accumulate ? C : 0) + bias
     g.splits = 0;
     launch_reduce(g, s);
     return myelin::launched("gemm_parts (K = 0)");
   }
-  return launch_gemm<1>(g, trans_a, trans_b, true, workspace_elems, s);
+  bool reduced = false;
+  const int rc = launch_gemm<1>(g, trans_a, trans_b, true, workspace_elems, s, false, &reduced);
+  return rc != MYELIN_OK ? rc : col_sum_after(g, reduced, s);
+}
+}  // namespace
+
+extern "C" int myelin_gemm(const void *A, int a_dtype, const void *B, int b_dtype, const float *bias, float *C,
+                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_a,
+                           int trans_b, int accumulate, int precision, float *workspace, int64_t workspace_elems,
+                           myelin_stream_t stream) {
+  return gemm_impl(A, a_dtype, B, b_dtype, bias, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, precision,
+                   workspace, workspace_elems, nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int myelin_gemm_col_sum(const void *A, int a_dtype, const void *B, int b_dtype, const float *bias,
+                                   float *C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                   int trans_a, int trans_b, int accumulate, int precision, float *workspace,
+                                   int64_t workspace_elems, const float *cs_in, float *cs_out, int64_t cs_rows,
+                                   int64_t cs_cols, myelin_stream_t stream) {
+  if (int rc = check_col_sum(cs_in, cs_out, cs_rows, cs_cols)) return rc;
+  return gemm_impl(A, a_dtype, B, b_dtype, bias, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, precision,
+                   workspace, workspace_elems, cs_in, cs_out, cs_rows, cs_cols, stream);
+}
+
+extern "C" int myelin_gemm_parts(const uint16_t *A, const uint16_t *B, int parts, int64_t b_part, const float *bias,
+                                 float *C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                 int trans_a, int trans_b, int accumulate, float *workspace, int64_t workspace_elems,
+                                 myelin_stream_t stream) {
+  return gemm_parts_impl(A, B, parts, b_part, bias, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate,
+                         workspace, workspace_elems, nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int myelin_gemm_parts_col_sum(const uint16_t *A, const uint16_t *B, int parts, int64_t b_part,
+                                         const float *bias, float *C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                         int64_t ldb, int64_t ldc, int trans_a, int trans_b, int accumulate,
+                                         float *workspace, int64_t workspace_elems, const float *cs_in, float *cs_out,
+                                         int64_t cs_rows, int64_t cs_cols, myelin_stream_t stream) {
+  if (int rc = check_col_sum(cs_in, cs_out, cs_rows, cs_cols)) return rc;
+  return gemm_parts_impl(A, B, parts, b_part, bias, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate,
+                         workspace, workspace_elems, cs_in, cs_out, cs_rows, cs_cols, stream);
 }
 
 extern "C" int myelin_gemm_f32(const float *A, const float *B, const float *bias, float *C, int64_t M, int64_t N,
@@ -3948,7 +4041,7 @@ extern "C" int myelin_linear_pre_bwd_readout(const float *pre, const float *grad
   if (C * pre_bwd_ds_kmax(O) * static_cast<int64_t>(sizeof(float)) > kPreBwdDsLds)
     return myelin::invalid("linear_pre_bwd_readout: C x O too large for the staged rows (C = %lld)",
                            static_cast<long long>(C));
-  if (B * N / 512 > 0x7fffffff) return myelin::invalid("linear_pre_bwd_readout: B x N too large");
+  if (B * N / 256 > 0x7fffffff) return myelin::invalid("linear_pre_bwd_readout: B x N too large");
   PreBwdArgs a{pre, nullptr, nullptr, grad_m, G, gbias_acc, C, B * N, decay, threshold, reset, slope, 1.0f, rule};
   if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
     return myelin::invalid("linear_pre_bwd_readout: unknown rule %d", rule);
@@ -4030,10 +4123,9 @@ namespace {
 
 __device__ __forceinline__ uint16_t to_bf16(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
 
-// 8 elements per thread, one 32-byte read and one 16-byte write
-__global__ __launch_bounds__(256) void cast_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
-                                                 int64_t n) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+// 8 elements per thread (from element i), one 32-byte read and one 16-byte write
+__device__ __forceinline__ void cast8(const float *__restrict__ src, uint16_t *__restrict__ dst, int64_t n,
+                                      int64_t i) {
   if (i + 8 <= n) {
     const f4 a = *reinterpret_cast<const f4 *>(src + i);
     const f4 b = *reinterpret_cast<const f4 *>(src + i + 4);
@@ -4043,6 +4135,11 @@ __global__ __launch_bounds__(256) void cast_bf16(const float *__restrict__ src, 
   } else {
     for (int64_t j = i; j < n; ++j) dst[j] = to_bf16(src[j]);
   }
+}
+
+__global__ __launch_bounds__(256) void cast_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                 int64_t n) {
+  cast8(src, dst, n, (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8);
 }
 
 // cast_bf16 that also reports whether every element was bf16-exact:
@@ -4110,12 +4207,13 @@ __global__ __launch_bounds__(256) void split_bf16x3_t(const float *__restrict__ 
 }
 
 // dst[c, r] = bf16(src[r, c]) through a 32 x 32 LDS tile (4 elements per
-// thread: a weight-sized matrix still spreads over the whole chip)
-__global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
-                                                      int64_t rows, int64_t cols) {
+// thread: a weight-sized matrix still spreads over the whole chip); this
+// workgroup's tile is column block bx, row block by
+__device__ __forceinline__ void transpose_tile(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                               int64_t rows, int64_t cols, int64_t bx, int64_t by) {
   __shared__ float tile[32][33];
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 32, c0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int64_t r0 = by * 32, c0 = bx * 32;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t r = r0 + ty + 8 * k, c = c0 + tx;
@@ -4127,6 +4225,26 @@ __global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ 
     const int64_t c = c0 + ty + 8 * k, r = r0 + tx;
     if (c < cols && r < rows) dst[c * rows + r] = to_bf16(tile[tx][ty + 8 * k]);
   }
+}
+
+__global__ __launch_bounds__(256) void transpose_bf16(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                      int64_t rows, int64_t cols) {
+  transpose_tile(src, dst, rows, cols, blockIdx.x, blockIdx.y);
+}
+
+// cast_bf16 of x and transpose_bf16 of w in one launch: the first
+// cast_blocks workgroups cast, the rest each transpose one 32 x 32 tile
+__global__ __launch_bounds__(256) void cast_transpose_bf16(const float *__restrict__ x, uint16_t *__restrict__ xb,
+                                                           int64_t n, int64_t cast_blocks,
+                                                           const float *__restrict__ w, uint16_t *__restrict__ wt,
+                                                           int64_t rows, int64_t cols) {
+  const int64_t b = blockIdx.x;
+  if (b < cast_blocks) {
+    cast8(x, xb, n, (b * blockDim.x + threadIdx.x) * 8);
+    return;
+  }
+  const int64_t t = b - cast_blocks, tiles_x = (cols + 31) / 32;
+  transpose_tile(w, wt, rows, cols, t % tiles_x, t / tiles_x);
 }
 
 }  // namespace
@@ -4166,6 +4284,23 @@ extern "C" int myelin_split_bf16x3(const float *src, uint16_t *dst, int64_t rows
     split_bf16x3<<<dim3(cdiv(rows * cols, 256)), dim3(256), 0, s>>>(src, dst, rows * cols);
   }
   return myelin::launched("split_bf16x3");
+}
+
+extern "C" int myelin_cast_transpose_bf16(const float *x, uint16_t *xb, int64_t n, const float *w, uint16_t *wt,
+                                          int64_t rows, int64_t cols, myelin_stream_t stream) {
+  if (n < 0 || rows < 0 || cols < 0) return myelin::invalid("cast_transpose_bf16: negative size");
+  if (n > 0 && (x == nullptr || xb == nullptr)) return myelin::invalid("cast_transpose_bf16: null pointer");
+  if (rows > 0 && cols > 0 && (w == nullptr || wt == nullptr))
+    return myelin::invalid("cast_transpose_bf16: null pointer");
+  if (n > 0 && (!myelin::aligned(x, 16) || !myelin::aligned(xb, 16)))
+    return myelin::invalid("cast_transpose_bf16: x and xb must be 16-byte aligned");
+  const int64_t cast_blocks = cdiv(cdiv(n, 8), 256);
+  const int64_t tiles = rows > 0 && cols > 0 ? cdiv(rows, 32) * cdiv(cols, 32) : 0;
+  if (cast_blocks + tiles == 0) return MYELIN_OK;
+  if (cast_blocks + tiles > 0x7fffffff) return myelin::invalid("cast_transpose_bf16: too large");
+  cast_transpose_bf16<<<dim3(static_cast<unsigned>(cast_blocks + tiles)), dim3(256), 0, myelin::as_hip(stream)>>>(
+      x, xb, n, cast_blocks, w, wt, rows, cols);
+  return myelin::launched("cast_transpose_bf16");
 }
 
 extern "C" int myelin_transpose_bf16(const float *src, uint16_t *dst, int64_t rows, int64_t cols,

@@ -50,19 +50,26 @@ def _workspace(M, N, K, prec, device, split, ws):
 
 
 def _gemm(A, B, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, prec, stream, bias=None, a_bits=False,
-          split=True, ws=None):
+          split=True, ws=None, col_sum=None):
     """C (+)= op(A) op(B) (+ bias); A and B both float32 or both bfloat16, or
     (``a_bits``) A packed spike words (int32, lda in words) with B float32.
     ``split=False`` gives no workspace, so K is never split: every element is
     then one k-ordered sum that does not depend on M (the synapse currents,
     which a checkpointed backward recomputes over fewer rows and must
-    reproduce bit for bit).  ``ws``: see _workspace."""
+    reproduce bit for bit).  ``ws``: see _workspace.  ``col_sum`` = (src
+    [R, Nc], dst [Nc]): also dst = src summed over rows, in the GEMM's
+    split-K reduce launch when it has one (myelin_gemm_col_sum)."""
 
     ws, n_ws = _workspace(M, N, K, prec, C.device, split, ws)
     a_dt = _lib.DT_BITS if a_bits else _lib.DT[A.dtype]
-    _lib.call("myelin_gemm", _lib.ptr(A), a_dt, _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias),
-              _lib.ptr(C), M, N, K, lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws),
-              n_ws, stream)
+    args = (_lib.ptr(A), a_dt, _lib.ptr(B), _lib.DT[B.dtype], _lib.ptr(bias), _lib.ptr(C), M, N, K, lda, ldb, ldc,
+            int(trans_a), int(trans_b), int(accumulate), prec, _lib.ptr(ws), n_ws)
+    if col_sum is None:
+        _lib.call("myelin_gemm", *args, stream)
+    else:
+        src, dst = col_sum
+        _lib.call("myelin_gemm_col_sum", *args, _lib.ptr(src), _lib.ptr(dst), src.numel() // dst.numel(),
+                  dst.numel(), stream)
 
 
 def _half(prec: int, F: int, N: int) -> bool:
@@ -87,14 +94,30 @@ def _transpose_bf16(w, stream):
     return out
 
 
+def _cast_transpose_bf16(x, w, stream):
+    """(bf16 copy of x, [N, F] bf16 transpose of w [F, N]) in one launch."""
+
+    xb = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    wt = torch.empty((w.shape[1], w.shape[0]), dtype=torch.bfloat16, device=w.device)
+    _lib.call("myelin_cast_transpose_bf16", _lib.ptr(x), _lib.ptr(xb), x.numel(), _lib.ptr(w), _lib.ptr(wt),
+              w.shape[0], w.shape[1], stream)
+    return xb, wt
+
+
 def _gemm_parts(A, B, parts, b_part, C, M, N, K, lda, ldb, ldc, trans_a, trans_b, accumulate, stream, bias=None,
-                split=True, ws=None):
+                split=True, ws=None, col_sum=None):
     """C (+)= sum_p op(A) op(B_p) (+ bias), bf16 operands, B_p = B + p*b_part
-    (elements); ``split`` and ``ws`` as in _gemm."""
+    (elements); ``split``, ``ws`` and ``col_sum`` as in _gemm."""
 
     ws, n_ws = _workspace(M, N, K, _lib.PREC["bf16"], C.device, split, ws)
-    _lib.call("myelin_gemm_parts", _lib.ptr(A), _lib.ptr(B), parts, b_part, _lib.ptr(bias), _lib.ptr(C), M, N, K,
-              lda, ldb, ldc, int(trans_a), int(trans_b), int(accumulate), _lib.ptr(ws), n_ws, stream)
+    args = (_lib.ptr(A), _lib.ptr(B), parts, b_part, _lib.ptr(bias), _lib.ptr(C), M, N, K, lda, ldb, ldc,
+            int(trans_a), int(trans_b), int(accumulate), _lib.ptr(ws), n_ws)
+    if col_sum is None:
+        _lib.call("myelin_gemm_parts", *args, stream)
+    else:
+        src, dst = col_sum
+        _lib.call("myelin_gemm_parts_col_sum", *args, _lib.ptr(src), _lib.ptr(dst), src.numel() // dst.numel(),
+                  dst.numel(), stream)
 
 
 # exact bf16 split of an fp32 synapse: tried for products of at least this
@@ -223,11 +246,14 @@ class HipLinearFunction(torch.autograd.Function):
                 gx = torch.empty((M, F), dtype=x2.dtype, device=dev)
                 _gemm(gy2, w, gx, M, F, N, N, N, F, False, True, False, ctx.prec, stream)
                 gx = gx.reshape(ctx.in_shape)
-            if ctx.needs_input_grad[1]:
-                gw = torch.empty_like(w)
-                _gemm(x2, gy2, gw, F, N, M, F, N, N, True, False, False, ctx.prec, stream)
             if ctx.has_b and ctx.needs_input_grad[2]:
                 gb = torch.empty((N,), dtype=x2.dtype, device=dev)
+            if ctx.needs_input_grad[1]:
+                # db rides with dW's launches
+                gw = torch.empty_like(w)
+                _gemm(x2, gy2, gw, F, N, M, F, N, N, True, False, False, ctx.prec, stream,
+                      col_sum=None if gb is None else (gy2, gb))
+            elif gb is not None:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gy2), _lib.ptr(gb), M, N, 0, stream)
         return gx, gw, gb, None
 
@@ -495,7 +521,7 @@ class HipLinearLIFFunction(torch.autograd.Function):
         stream = _lib.stream(dev)
         need = any(ctx.needs_input_grad[:3])
         half = _half(prec, F, N)
-        xs, wt = (_cast_bf16(x, stream), _transpose_bf16(w, stream)) if half else (x, None)
+        xs, wt = _cast_transpose_bf16(x, w, stream) if half else (x, None)
         bits = _spike_bits(x) if _bits_consumer(B, F, N, prec) else None
         fwd_budget, budget = _budgets(lean, checkpoint, B, N)
         split = None
@@ -607,6 +633,7 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
         gx = torch.empty((T, B, F), device=dev) if need_x else None
         gw = torch.empty_like(w) if need_w else None  # the first (last-in-time) span overwrites it
         gb_acc = (torch.empty((B, N), device=dev) if whole else zeros[-1]) if want_gb else None
+        gb = torch.empty((N,), device=dev) if want_gb else None
         # exact split: dW reads G as three bf16 planes [3, C, B, N] (C the
         # span's steps), written by the reverse pass itself unless dX needs
         # the fp32 G as well
@@ -700,25 +727,27 @@ def linear_backward(xs, w, b, pre, ckpt, wt, g_m, g_out, decay, threshold, reset
             if gx is not None:
                 # dX[t0:t1] = G @ W^T : [rows, N] x [N, F]
                 _gemm(G, wg, gx[t0:t1], rows, F, N, N, N, F, False, True, False, prec, stream, ws=ws)
+            # db (the bias sums complete once the first span's reverse pass
+            # has run) rides with that span's dW launches
+            cs = (gb_acc, gb) if k == 0 and gb is not None else None
             if gw is not None and parts:
                 if G is not G3:
                     _lib.call("myelin_split_bf16x3", _lib.ptr(G), _lib.ptr(G3), rows, N, 0, stream)
                 _gemm_parts(xs[t0:t1], G3, 3, rows * N, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1,
-                            stream, ws=ws)
+                            stream, ws=ws, col_sum=cs)
             elif gw is not None and x_bits is not None:
                 _gemm(x_bits[t0:t1], G, gw, F, N, rows, x_bits.shape[2], N, N, True, False, k != n_spans - 1, prec,
-                      stream, a_bits=True, ws=ws)
+                      stream, a_bits=True, ws=ws, col_sum=cs)
             elif gw is not None:
                 # dW (+)= X[t0:t1]^T @ G : [F, rows] x [rows, N]
-                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream, ws=ws)
+                _gemm(xs[t0:t1], G, gw, F, N, rows, F, N, N, True, False, k != n_spans - 1, prec, stream, ws=ws,
+                      col_sum=cs)
         if overlap:
             # every side-stream kernel is behind a ready[] the main stream
             # waited on; the buffers' last users include the side stream
             for t in (*bufs, xs, w, ckpt, *(() if b is None else (b,)), *(() if wt is None else (wt,))):
                 t.record_stream(side)
-        gb = None
-        if gb_acc is not None:
-            gb = torch.empty((N,), device=dev)
+        if gb is not None and gw is None:
             _lib.call("myelin_col_sum_f32", _lib.ptr(gb_acc), _lib.ptr(gb), B, N, 0, stream)
     return gx, gw, gb
 

@@ -43,8 +43,9 @@ from typing import Any
 import torch
 
 from myelin_amd import _lib
-from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _LEAN_FWD_ELEMS, _cast_bf16, _gemm, _gemm_parts, _half, _keep_trace,
-                               _LazyBf16, _lif_fwd, _side_stream, _split_eligible, _split_synapse, _transpose_bf16)
+from myelin_amd.linear import (_CURRENT_CHUNK_ELEMS, _LEAN_FWD_ELEMS, _cast_bf16, _cast_transpose_bf16, _gemm,
+                               _gemm_parts, _half, _keep_trace, _LazyBf16, _lif_fwd, _side_stream, _split_eligible,
+                               _split_synapse)
 
 # trace budget of a backward span (floats per buffer): the backward walks
 # whole checkpoint chunks, as many at a time as keep each per-span buffer
@@ -130,7 +131,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
         half = _half(prec, F, H)
-        xs, wt = (_cast_bf16(x, stream), _transpose_bf16(wh, stream)) if half else (x, None)
+        xs, wt = _cast_transpose_bf16(x, wh, stream) if half else (x, None)
         # spike inputs: the hidden synapse on the exact bf16 split (the first
         # group's forward learns whether the input qualifies)
         split = None
@@ -197,6 +198,11 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gwo = torch.empty_like(wo) if need_wo else None
             gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
             gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
+            # the bias gradients (column sums of the accumulators, complete
+            # once the first span's reverse passes have run) ride with that
+            # span's weight-gradient launches
+            gbh = torch.empty((H,), device=dev) if gbh_acc is not None else None
+            gbo = torch.empty((O,), device=dev) if gbo_acc is not None else None
             cur = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             pre_o = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             G_o = torch.empty((L0, B, O), device=dev)
@@ -296,11 +302,12 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 if gwo is not None:
                     # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
                     acc = k != NS - 1
+                    cs = (gbo_acc, gbo) if k == 0 and gbo is not None else None
                     if words is not None:
                         _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, acc, prec, stream,
-                              a_bits=True)
+                              a_bits=True, col_sum=cs)
                     else:
-                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream)
+                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream, col_sum=cs)
                 if not need_hidden:
                     if nset == 2:
                         free[i].record(main)  # dW_o was the last reader of the spikes
@@ -327,26 +334,24 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 if gx is not None:
                     _gemm(G_h, whg, gx[t0:t1], rows, F, H, H, H, F, False, True, False, prec, stream, ws=pool)
                 if gwh is not None:
+                    cs = (gbh_acc, gbh) if k == 0 and gbh is not None else None
                     if parts:
                         if G_h is not G3:
                             _lib.call("myelin_split_bf16x3", _lib.ptr(G_h), _lib.ptr(G3), rows, H, 0, stream)
                         _gemm_parts(xs[t0:t1], G3, 3, rows * H, gwh, F, H, rows, F, H, H, True, False, k != NS - 1,
-                                    stream, ws=pool)
+                                    stream, ws=pool, col_sum=cs)
                     else:
                         _gemm(xs[t0:t1], G_h, gwh, F, H, rows, F, H, H, True, False, k != NS - 1, prec, stream,
-                              ws=pool)
+                              ws=pool, col_sum=cs)
             if nset == 2:
                 # every side-stream kernel is behind a ready[] the main stream
                 # waited on; these tensors' last users include the side stream
                 for t_ in (*hs_b, *pre_b, xs.x if lazy else xs, wh, ck_h, bh, wt):
                     if t_ is not None:
                         t_.record_stream(side)
-            gbh = gbo = None
-            if gbh_acc is not None:
-                gbh = torch.empty((H,), device=dev)
+            if gbh is not None and gwh is None:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbh_acc), _lib.ptr(gbh), B, H, 0, stream)
-            if gbo_acc is not None:
-                gbo = torch.empty((O,), device=dev)
+            if gbo is not None and gwo is None:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
         return gx, gwh, gbh, gwo, gbo, None, None, None, None, None, None, None, None, None
 

@@ -151,7 +151,26 @@ def test_split_synapse_entry_points_validate_on_the_host():
         _lib.call("myelin_linear_pre_bwd_readout", 16, 16, None, 20, 16, 16, 0, None, 4, 2, 256, *tail)
     with pytest.raises(ValueError, match="unknown surrogate"):
         _lib.call(*ro, 20, 16, 16, 0, None, 4, 2, 256, 0.9, 1.0, 0.0, 5.0, 99, 0, None)
+    # the GEMMs with an attached column sum, and the merged bf16 copies
+    g = ("myelin_gemm_col_sum", 16, 0, 16, 0, None, 16, 4, 4, 4, 4, 4, 4, 0, 0, 0, 0, None, 0)
+    with pytest.raises(ValueError, match="col_sum: negative size"):
+        _lib.call(*g, 16, 16, -1, 4, None)
+    with pytest.raises(ValueError, match="col_sum: null pointer"):
+        _lib.call(*g, 16, None, 3, 4, None)
+    with pytest.raises(ValueError, match="gemm: ldc < N"):
+        _lib.call("myelin_gemm_col_sum", 16, 0, 16, 0, None, 16, 4, 4, 4, 4, 4, 3, 0, 0, 0, 0, None, 0, 16, 16, 3, 4,
+                  None)
+    with pytest.raises(ValueError, match="col_sum: null pointer"):
+        _lib.call("myelin_gemm_parts_col_sum", 16, 16, 3, 64, None, 16, 4, 4, 8, 8, 4, 4, 0, 0, 0, None, 0, None, 16,
+                  2, 4, None)
+    with pytest.raises(ValueError, match="cast_transpose_bf16: negative size"):
+        _lib.call("myelin_cast_transpose_bf16", 16, 16, -8, 16, 16, 4, 4, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _lib.call("myelin_cast_transpose_bf16", 4, 16, 8, 16, 16, 4, 4, None)
     # empty problems are valid no-ops
+    assert _lib.load().myelin_cast_transpose_bf16(None, None, 0, None, None, 0, 5, None) == 0
+    assert _lib.load().myelin_gemm_col_sum(None, 0, None, 0, None, None, 0, 4, 4, 4, 4, 4, 0, 0, 0, 0, None, 0,
+                                           None, None, 0, 0, None) == 0
     assert _lib.load().myelin_split_bf16x3(None, None, 0, 5, 1, None) == 0
     assert _lib.load().myelin_gemm_parts(None, None, 3, 0, None, None, 0, 4, 4, 4, 4, 4, 0, 0, 0, None, 0,
                                          None) == 0

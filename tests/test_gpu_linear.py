@@ -476,6 +476,94 @@ def test_bf16_copies_round_like_torch(rows, cols):
     assert torch.equal(_transpose_bf16(x, stream), x.t().contiguous().to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("n,rows,cols", [(8, 1, 1), (13, 7, 13), (50 * 256 * 784, 784, 2048), (4096, 130, 257),
+                                         (0, 33, 5), (24, 0, 0)])
+def test_cast_transpose_in_one_launch_equals_the_two(n, rows, cols):
+    """myelin_cast_transpose_bf16 gives the bits of myelin_cast_bf16 and
+    myelin_transpose_bf16 (the bf16 synapse's operand copies), either part
+    empty too."""
+
+    _print_case(test="cast_transpose", n=n, rows=rows, cols=cols)
+    from myelin_amd.linear import _cast_bf16, _cast_transpose_bf16, _transpose_bf16
+
+    g = seeded(n + rows + cols)
+    x = (torch.randn(n, generator=g) * 3).to(DEV)
+    w = (torch.randn(rows, cols, generator=g) * 3).to(DEV)
+    stream = _lib.stream(torch.device(DEV))
+    xb, wt = _cast_transpose_bf16(x, w, stream)
+    if n:
+        assert torch.equal(xb, _cast_bf16(x, stream))
+    if rows and cols:
+        assert torch.equal(wt, _transpose_bf16(w, stream))
+
+
+# (M, N, K, prec, bits): dW-shaped products whose K is split (the column sum
+# joins the split-K reduce launch, four-wide and scalar) and ones that are
+# not split (the column sum runs after the GEMM), narrow and wide, fp32,
+# bf16 and packed-bit operands
+COLSUM_CASES = [(784, 2048, 12800, "bf16", False), (2048, 10, 12800, "bf16", True), (2048, 10, 12800, "fp32", True),
+                (300, 17, 784, "fp32", False), (64, 64, 64, "fp32", False), (1024, 4096, 1440, "fp32", False),
+                (37, 5, 9, "fp32", False)]
+
+
+@pytest.mark.parametrize("M,N,K,prec,bits", COLSUM_CASES)
+def test_gemm_with_attached_col_sum_equals_the_two_launches(M, N, K, prec, bits):
+    """myelin_gemm_col_sum: C and the column sum are bit-identical to
+    myelin_gemm followed by myelin_col_sum_f32, whether the column sum ran in
+    the split-K reduce launch or on its own."""
+
+    _print_case(test="gemm_col_sum", M=M, N=N, K=K, prec=prec, bits=bits)
+    g = seeded(M + N + K)
+    stream = _lib.stream(torch.device(DEV))
+    P = _lib.PREC[prec]
+    A = (torch.rand(K, M, generator=g) < 0.3).float().to(DEV)  # x^T layout: [K rows, M] read transposed
+    B = torch.randn(K, N, generator=g).to(DEV)
+    src = torch.randn(97, N + 3, generator=g).to(DEV)
+    if bits:
+        words = myelin.pack_spikes(A).data
+        Aop, lda = words, words.shape[-1]
+    else:
+        Aop, lda = (A.to(torch.bfloat16), M) if prec == "bf16" else (A, M)
+        if prec == "bf16":
+            B = B.to(torch.bfloat16)
+    outs = []
+    for attach in (False, True):
+        C = torch.full((M, N), 7.0, device=DEV)
+        cs = torch.full((N + 3,), -1.0, device=DEV)
+        _gemm(Aop, B, C, M, N, K, lda, N, N, True, False, False, P, stream, a_bits=bits,
+              col_sum=(src, cs) if attach else None)
+        if not attach:
+            _lib.call("myelin_col_sum_f32", _lib.ptr(src), _lib.ptr(cs), 97, N + 3, 0, stream)
+        outs.append((C, cs))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.allclose(outs[1][1], src.sum(0), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 4096, 1440), (784, 2048, 12800), (40, 24, 96)])
+def test_gemm_parts_with_attached_col_sum_equals_the_two_launches(M, N, K):
+    _print_case(test="gemm_parts_col_sum", M=M, N=N, K=K)
+    from myelin_amd.linear import _gemm_parts
+
+    g = seeded(M + N + K + 1)
+    stream = _lib.stream(torch.device(DEV))
+    A = (torch.rand(K, M, generator=g) < 0.3).to(torch.bfloat16).to(DEV)
+    Bf = torch.randn(K, N, generator=g).to(DEV)
+    B3 = torch.empty(3 * K * N, dtype=torch.bfloat16, device=DEV)
+    _lib.call("myelin_split_bf16x3", _lib.ptr(Bf), _lib.ptr(B3), K, N, 0, stream)
+    src = torch.randn(33, N, generator=g).to(DEV)
+    outs = []
+    for attach in (False, True):
+        C = torch.zeros((M, N), device=DEV)
+        cs = torch.zeros((N,), device=DEV)
+        _gemm_parts(A, B3, 3, K * N, C, M, N, K, M, N, N, True, False, False, stream,
+                    col_sum=(src, cs) if attach else None)
+        if not attach:
+            _lib.call("myelin_col_sum_f32", _lib.ptr(src), _lib.ptr(cs), 33, N, 0, stream)
+        outs.append((C, cs))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("M,N,K", [(8, 8, 8), (72, 40, 104), (128, 128, 64), (304, 264, 1000), (256, 384, 3000),
                                    (520, 136, 200), (8200, 1032, 72)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])

@@ -250,10 +250,10 @@ def test_linear_memory_policy_spans_equal_one_span():
     assert_norm_close(out["memory"][3], out[7][3], 1e-6, "grad_b")
 
 
-# (T, B, F, H, O, checkpoint, split, x_grad): one and two neurons per lane
-# (B x H below / at 65536), G written as fp32 (dX needs it) and as the three
-# bf16 planes of the exact split, readouts of 5, 12, 20 and 32 neurons (the
-# 8-, 12-, 20- and 32-term sums), a ragged last span under "memory"
+# (T, B, F, H, O, checkpoint, split, x_grad): small and wide grids, G
+# written as fp32 (dX needs it) and as the three bf16 planes of the exact
+# split, readouts of 5, 12, 20 and 32 neurons (the 8-, 12-, 20- and 32-term
+# sums), a ragged last span under "memory"
 DS_CASES = [(23, 4, 40, 256, 5, 5, False, True), (23, 4, 40, 512, 20, "memory", True, False),
             (19, 128, 32, 512, 32, 5, False, True), (19, 128, 32, 1024, 12, 4, True, False)]
 
