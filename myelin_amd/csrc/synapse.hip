@@ -1605,6 +1605,23 @@ __attribute__((amdgpu_waves_per_eu(WM * WN > 4 ? 1 : 2))) void gemm_big(GemmArgs
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int dma_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
+// Scheduling of one k step of the direct-load kernels: the next k step's
+// NG fragment reads (RPG LDS reads each) are placed one group after each
+// of the first NG of this step's NM MFMAs, the rest of the MFMAs after.
+// Left to itself the scheduler issues all the reads after the last MFMA,
+// so each k step starts by waiting for LDS (8192 x 4096 x 3 x 1024 on
+// 256 x 256 tiles: 165 -> 156 us, the same bits).
+template <int NM, int NG, int RPG>
+__device__ __forceinline__ void interleave_reads() {
+  static_assert(NG <= NM, "one read group per MFMA at most");
+#pragma unroll
+  for (int q = 0; q < NG; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, RPG, 0);  // then RPG LDS reads
+  }
+  if constexpr (NM > NG) __builtin_amdgcn_sched_group_barrier(0x008, NM - NG, 0);
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Loads of one operand tile: ROWS rows x 64 k, NP pieces per thread.
@@ -1763,6 +1780,7 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
 #pragma unroll
           for (int j = 0; j < WN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
+        if (ks + 1 < 4) interleave_reads<WM * WN, WM + WN, 1>();
       }
     };
     issue(l0);
@@ -1984,6 +2002,7 @@ __global__ __launch_bounds__(64 * (BM / (32 * WM)) * (BN / (32 * WN))) __attribu
 #pragma unroll
           for (int j = 0; j < WN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
+        if (ks + 1 < 4) interleave_reads<WM * WN, WM + WN, 2>();  // two transposing reads a fragment
       }
     };
     issue(l0);
