@@ -3216,15 +3216,21 @@ bool bf16_aligned(const void *q, int64_t ld, bool kcontig) {
 // pays on long K when the tiles fill whole rounds of 256 CUs: at 4096
 // columns and K = 3 x 1024, 8192 rows (4 rounds) 274 -> 242 us and 7200
 // rows (3.6) 251 -> 235 us, but 6400 rows (3.1: a last round 1/8 full)
-// 209 -> 224 us.  So they run when the last round is at least half full.
+// 209 -> 224 us.  So the register-staged ones run when the last round is
+// at least half full; the direct-load ones from half a round (below).
 // Short K (784, 12 stages) measured slower (137 vs 113 us).
-// 256 x 128 tiles for a product (bf16 operands, both k-contiguous, long K)
-// whose tiles fill whole-ish rounds of 256 workgroups.  (mn-contiguous
-// operands on these tiles, with a K split filling the rounds, measured
-// slower on the split dW: 348 vs 325 us at 1024 x 4096 x 3*7200.)
+// (mn-contiguous operands on these tiles, with a K split filling the
+// rounds, measured slower on the split dW: 348 vs 325 us at 1024 x 4096 x
+// 3*7200.)
+bool use_dma(const GemmArgs &g, int ta, int tb, bool half);
+
 bool use_tall(const GemmArgs &g, int ta, int tb, bool half) {
   if (!half || ta || !tb || g.M < 256 || g.K * g.parts < MYELIN_TALL_MIN_K) return false;
   const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 128);
+  // direct-load tiles (their fragment reads interleaved with the MFMAs)
+  // pay from half a round: 1440 x 4096 x 3 x 1024 47-48 us against 60-65
+  // on the 128 x 128 tiles
+  if (use_dma(g, ta, tb, half)) return tiles >= 128;
   return tiles >= 256 && (tiles % 256 == 0 || tiles % 256 >= 128);
 }
 
@@ -3278,10 +3284,15 @@ void launch_dma_mn(const GemmArgs &g, dim3 grid, hipStream_t s) {
 // fill whole-ish rounds of 256 workgroups.  Against the 256 x 128 tiles,
 // measured beside them: 8192 x 4096 x 3 x 1024 217 -> 179 us (1154 TF),
 // 7200 rows 201 -> 168 us, 8192 x 4096 x 3072 207 -> 174 us.
+// One workgroup per CU on either direct-load shape, so a product takes
+// ceil(tiles / 256) rounds of the chip; a 256 x 256 tile costs 1.74 tiles of
+// 256 x 128 (7200 x 4096 x 3 x 1024: 148 against 171 us), so the wide tiles
+// run when their rounds cost no more than the tall tiles' (2880 rows: 76
+// against 86 us; 1440 rows take the tall tiles, 48 against 76 us).
 bool use_wide(const GemmArgs &g, int ta, int tb, bool half) {
   if (!use_dma(g, ta, tb, half) || g.M < 256 || g.N < 256 || g.K * g.parts < MYELIN_TALL_MIN_K) return false;
-  const int64_t tiles = cdiv(g.M, 256) * cdiv(g.N, 256);
-  return tiles >= 256 && (tiles % 256 == 0 || tiles % 256 >= 128);
+  const int64_t wide = cdiv(g.M, 256) * cdiv(g.N, 256), tall = cdiv(g.M, 256) * cdiv(g.N, 128);
+  return 174 * cdiv(wide, 256) <= 100 * cdiv(tall, 256);
 }
 
 void launch_dma_wide(const GemmArgs &g, dim3 grid, hipStream_t s) {
