@@ -124,9 +124,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         G = max(1, min(K, (_LEAN_FWD_ELEMS if lean else _CURRENT_CHUNK_ELEMS) // (L0 * B * H)))
         LG = min(G * C, T)
         # the packed variant never forms dense hidden spikes: its readout
-        # GEMM reads the words
+        # GEMM reads the words, and as the words of all T are kept, the
+        # readout runs once after the hidden layer (one currents GEMM and
+        # one recurrence over T instead of one pair per group: a narrow
+        # GEMM's rows do not depend on how many rows it is given, and the
+        # recurrence carries its state exactly, so the results are the same)
         hs = None if packed_hidden else torch.empty((LG, B, H), device=dev)
-        cur = torch.empty((LG, B, O), device=dev)
+        cur = torch.empty((T if packed_hidden else LG, B, O), device=dev)
         pre_o = torch.empty((T, B, O), device=dev) if keep else None
         words = torch.empty((T, B, (H + 31) // 32), dtype=torch.int32, device=dev) if packed_hidden else None
         # bf16 synapse: the hidden GEMMs read bf16 copies of x and W_h^T
@@ -149,10 +153,13 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                      x32=x[t0:t1] if k == 0 else None, budget=LG * B * H)
             if k == 0 and split is not None and not split.exact():
                 xs, wt = x, None
-            s_in = words[t0:t1] if hs is None else hs[:L]
-            _readout_chunk(cur[:L], s_in, wo, bo, m_o, m_o, None if pre_o is None else pre_o[t0:t1], counts,
-                           rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
-                           stream, exact=need and not keep)
+            if hs is not None:
+                _readout_chunk(cur[:L], hs[:L], wo, bo, m_o, m_o, None if pre_o is None else pre_o[t0:t1], counts,
+                               rates if t1 == T else None, ck_o, T, t0, t1, C, decay, threshold, reset, slope, prec,
+                               stream, exact=need and not keep)
+        if hs is None:
+            _readout_chunk(cur, words, wo, bo, m_o, m_o, pre_o, counts, rates, ck_o, T, 0, T, C, decay, threshold,
+                           reset, slope, prec, stream, exact=need and not keep)
         lazy = isinstance(xs, _LazyBf16)
         ctx.set_materialize_grads(False)
         ctx.meta = (decay, threshold, reset, sid, slope, C, prec, bh is not None, bo is not None, lean, lazy)
@@ -205,7 +212,28 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             gbo = torch.empty((O,), device=dev) if gbo_acc is not None else None
             cur = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             pre_o = torch.empty((L0, B, O), device=dev) if pre_all is None else None
-            G_o = torch.empty((L0, B, O), device=dev)
+            # the packed variant with the readout's whole trace kept: the
+            # readout's reverse pass and dW_o run once over all T before the
+            # spans (the reverse pass carries its adjoint exactly as the
+            # span walk does; dW_o reads every step's words at once), and
+            # each hidden span reads its rows of G_o
+            whole_o = words is not None and pre_all is not None
+            G_o_all = None
+            if whole_o:
+                G_o_all = torch.empty((T, B, O), device=dev)
+                _lib.call(
+                    "myelin_linear_pre_bwd",
+                    _lib.ptr(pre_all), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o_all), _lib.DT[torch.float32],
+                    _lib.ptr(gbo_acc), T, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                )
+                if gwo is not None:
+                    _gemm(words, G_o_all, gwo, H, O, T * B, words.shape[-1], O, O, True, False, False, prec, stream,
+                          a_bits=True, col_sum=None if gbo is None else (gbo_acc, gbo))
+                elif gbo is not None:
+                    _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
+                if not need_hidden:
+                    return gx, None, None, gwo, gbo, None, None, None, None, None, None, None, None, None
+            G_o = None if whole_o else torch.empty((L0, B, O), device=dev)
             # the memory-lean policy runs the recompute in turn on the one
             # stream (one buffer set, and the recompute's currents reuse the
             # dS buffer, which that span fills only after its recompute),
@@ -286,28 +314,31 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                         hidden_recompute(k)  # one buffer set: this span's, in turn
                     main.wait_event(ready[i])
                 hs, pre_h = hs_b[i], pre_b[i]
-                s_in = words[t0:t1] if words is not None else hs[:L]
-                if pre_all is not None:
-                    pre_k = pre_all[t0:t1]
+                if whole_o:
+                    G_o = G_o_all[t0:t1]
                 else:
-                    _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k * per], None, pre_o[:L], None, None, None, T, t0,
-                                   t1, C, decay, threshold, reset, slope, prec, stream, exact=True)
-                    pre_k = pre_o
-                _lib.call(
-                    "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_k), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
-                    _lib.ptr(gbo_acc),
-                    L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
-                )
-                if gwo is not None:
-                    # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
-                    acc = k != NS - 1
-                    cs = (gbo_acc, gbo) if k == 0 and gbo is not None else None
-                    if words is not None:
-                        _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, acc, prec, stream,
-                              a_bits=True, col_sum=cs)
+                    s_in = words[t0:t1] if words is not None else hs[:L]
+                    if pre_all is not None:
+                        pre_k = pre_all[t0:t1]
                     else:
-                        _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream, col_sum=cs)
+                        _readout_chunk(cur[:L], s_in, wo, bo, ck_o[k * per], None, pre_o[:L], None, None, None, T,
+                                       t0, t1, C, decay, threshold, reset, slope, prec, stream, exact=True)
+                        pre_k = pre_o
+                    _lib.call(
+                        "myelin_linear_pre_bwd",
+                        _lib.ptr(pre_k), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o), _lib.DT[G_o.dtype],
+                        _lib.ptr(gbo_acc),
+                        L, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
+                    )
+                    if gwo is not None:
+                        # dW_o += S[t0:t1]^T @ G_o (S read as bits in the packed variant)
+                        acc = k != NS - 1
+                        cs = (gbo_acc, gbo) if k == 0 and gbo is not None else None
+                        if words is not None:
+                            _gemm(s_in, G_o, gwo, H, O, rows, s_in.shape[-1], O, O, True, False, acc, prec, stream,
+                                  a_bits=True, col_sum=cs)
+                        else:
+                            _gemm(hs, G_o, gwo, H, O, rows, H, O, O, True, False, acc, prec, stream, col_sum=cs)
                 if not need_hidden:
                     if nset == 2:
                         free[i].record(main)  # dW_o was the last reader of the spikes
@@ -351,7 +382,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                         t_.record_stream(side)
             if gbh is not None and gwh is None:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbh_acc), _lib.ptr(gbh), B, H, 0, stream)
-            if gbo is not None and gwo is None:
+            if gbo is not None and gwo is None and not whole_o:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
         return gx, gwh, gbh, gwo, gbo, None, None, None, None, None, None, None, None, None
 
