@@ -108,11 +108,15 @@ def _cpu_mean(run, min_seconds: float, max_runs: int = 50) -> tuple[float, int, 
 def _launch_ms(torch, launch, reps: int) -> float:
     """Average duration of `launch()` over back-to-back launches bracketed by
     one HIP event pair on the current stream (the launch stream): a pair
-    around each launch would also time the host's launch latency."""
+    around each launch would also time the host's launch latency.  The
+    launches queue up behind a GPU-side spin of about 30 us per launch, so
+    that a short kernel runs back to back even where the host issues
+    launches more slowly than the GPU runs them (under a kernel tracer)."""
 
     launch()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(reps * 30e-6 * 2.5e9))  # spin cycles: ~30 us per launch at 2.5 GHz
     ev0.record()
     for _ in range(reps):
         launch()
@@ -173,9 +177,13 @@ def _graph_timed(torch, body, params, steps, warmup):
     same kernels in the same order as an eager step, launched without the
     host's per-op work.  The capture follows torch's whole-network recipe:
     warm up on a side stream, drop the gradients, capture.  Returns
-    (ms, eager ms over max(steps, EAGER_MIN_STEPS) steps)."""
+    (ms, eager ms over max(steps, EAGER_MIN_STEPS) steps, the same eager
+    timing with torch's autograd engine running the backward on the calling
+    thread instead of its device thread)."""
 
     eager = _timed(torch, lambda: (_none(params), body()), max(steps, EAGER_MIN_STEPS), warmup)
+    with torch.autograd.set_multithreading_enabled(False):
+        eager_one_thread = _timed(torch, lambda: (_none(params), body()), max(steps, EAGER_MIN_STEPS), warmup)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -189,7 +197,7 @@ def _graph_timed(torch, body, params, steps, warmup):
     with torch.cuda.graph(graph):
         body()
     ms = _timed(torch, graph.replay, steps, warmup)
-    return ms, eager
+    return ms, eager, eager_one_thread
 
 
 def _none(params):
@@ -466,7 +474,7 @@ def _workload_linear_bf16(torch, myelin, args, threads):
 
     # the step as a captured HIP graph (about 30 launches whose host-side
     # work, ~0.3-0.45 ms by box, would otherwise exceed the GPU's ~0.37 ms)
-    ms, eager_ms = _graph_timed(torch, body, params, args.steps, args.warmup)
+    ms, eager_ms, eager_1t_ms = _graph_timed(torch, body, params, args.steps, args.warmup)
     flops = 2 * Tl * Bl * F * H * 2 + 4 * 2 * Tl * Bl * H * O
     tflops = flops / (ms * 1e-3) / 1e12
     E = Tl * Bl * H
@@ -511,7 +519,9 @@ def _workload_linear_bf16(torch, myelin, args, threads):
                            "kernel_ms_back_to_back": kern_b2b},
                  step_tflops=tflops, step_frac_of_bf16_peak=tflops / BF16_PEAK_TFLOPS, dtype="bf16",
                  timing="HIP graph replay of the whole step (forward, loss, backward)", eager_ms_per_step=eager_ms,
-                 eager_steps=max(args.steps, EAGER_MIN_STEPS), eager_over_graph=eager_ms / ms)
+                 eager_steps=max(args.steps, EAGER_MIN_STEPS), eager_over_graph=eager_ms / ms,
+                 eager_caller_thread_backward_ms_per_step=eager_1t_ms,
+                 eager_caller_thread_backward_over_graph=eager_1t_ms / ms)
     if not args.no_cpu_baseline:
         R = _oracle()
         sb = 32

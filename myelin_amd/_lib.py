@@ -115,14 +115,19 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_FNS: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Call an entry point; map its return code to ValueError / MyelinHipError."""
 
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc == OK:
         return
-    msg = (lib.myelin_last_error() or b"").decode(errors="replace")
+    msg = (load().myelin_last_error() or b"").decode(errors="replace")
     if rc == EINVAL:
         raise ValueError(f"{name}: {msg}")
     raise MyelinHipError(f"{name}: {msg}")
@@ -133,7 +138,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the current stream of ``device`` (the stream torch
+    launches on, also under graph capture)."""
+
+    idx = device.index
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if idx is None else idx)
 
 
 def require_device(t: torch.Tensor, what: str) -> None:

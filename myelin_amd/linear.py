@@ -379,9 +379,11 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
     # slow each other down (the 1024 -> 4096 -> 20 rate network's step at
     # T=2000, B=32: 7.92-8.01 ms overlapped, 7.53 serial), so they run in
     # turn on the one stream.
-    main = torch.cuda.current_stream(dev)
-    side = _side_stream(dev)
-    overlap = n > 1 and not half and main.cuda_stream == stream and side.cuda_stream != stream
+    overlap = False
+    if n > 1 and not half:
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        overlap = main.cuda_stream == stream and side.cuda_stream != stream
     if cur is not None and not overlap and cur.dtype == torch.float32 and cur.numel() >= step * B * N:
         curs = [cur.reshape(-1)[:step * B * N].view(step, B, N)]
     else:
