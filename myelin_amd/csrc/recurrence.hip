@@ -373,11 +373,34 @@ __device__ __forceinline__ void fwd_ckpt(const FwdArgs &p, int64_t base, int64_t
   if constexpr (ALIF) st<V>(p.ckpt_a + k * p.BN + base, a);
 }
 
+// The last T % U steps (rem, uniform) from registers loaded ahead: step
+// t0 + u for u < rem, checkpoints as in the loop.
+template <bool ALIF, int RULE, int V, int U>
+__device__ __forceinline__ void fwd_tail(const FwdArgs &p, int64_t base, int64_t t0, int rem,
+                                         const float (&cur)[U][V], float (&m)[V], float (&a)[V], int64_t &next_ck,
+                                         int64_t &k) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u >= rem) break;  // uniform
+    const int64_t t = t0 + u;
+    if (p.ckpt_m != nullptr && t == next_ck) {
+      fwd_ckpt<ALIF, V>(p, base, k++, m, a);
+      next_ck += p.chunk;
+    }
+    float sp[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p);
+    st_stream<V>(p.spikes + t * p.BN + base, sp);
+  }
+}
+
 // Dense-spike forward, lane owns neurons [V*gid, V*gid + V) of the flat BN
 // axis.  Checkpoints (when requested) fall on block starts (chunk % U == 0,
 // checked by the host), so every full block of U steps is straight-line code:
 // the compiler keeps the next block's U loads in flight across the current
-// block with exact vmcnt waits.  The last T % U steps run in a guarded tail.
+// block with exact vmcnt waits.  The last T % U steps are loaded in one batch
+// before the last full block runs, so they wait for one load latency rather
+// than one per step.
 template <bool ALIF, int RULE, int V, int U>
 __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -396,7 +419,16 @@ __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
   }
 
   const int64_t Tm = (T / U) * U;
+  const int rem = static_cast<int>(T - Tm);
   int64_t next_ck = 0, k = 0;  // next checkpoint step and its row
+  float tl[U][V];              // the tail's steps
+  auto load_tail = [&]() {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u >= rem) break;  // uniform
+      ld_stream<V>(tl[u], p.x + (Tm + u) * BN + base);
+    }
+  };
   if (Tm > 0) {
     float nxt[U][V];
 #pragma unroll
@@ -416,23 +448,16 @@ __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
       }
       fwd_block<ALIF, RULE, V, U>(p, base, t0, cur, m, a);
     }
+    load_tail();
     if (ck && t0 == next_ck) {
       fwd_ckpt<ALIF, V>(p, base, k++, m, a);
       next_ck += p.chunk;
     }
     fwd_block<ALIF, RULE, V, U>(p, base, t0, nxt, m, a);
+  } else {
+    load_tail();
   }
-  for (int64_t t = Tm; t < T; ++t) {
-    if (ck && t == next_ck) {
-      fwd_ckpt<ALIF, V>(p, base, k++, m, a);
-      next_ck += p.chunk;
-    }
-    float xv[V], sp[V];
-    ld_stream<V>(xv, p.x + t * BN + base);
-#pragma unroll
-    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], xv[v], p);
-    st_stream<V>(p.spikes + t * BN + base, sp);
-  }
+  fwd_tail<ALIF, RULE, V, U>(p, base, Tm, rem, tl, m, a, next_ck, k);
   st<V>(p.m_final + base, m);
   if constexpr (ALIF) st<V>(p.a_final + base, a);
 }
