@@ -500,6 +500,35 @@ int myelin_lif_currents_fwd(const float *currents, const float *m0,
                             float threshold, float reset, float slope, int rule,
                             myelin_stream_t stream);
 
+/*
+ * A narrow layer (N <= 32 neurons) over a packed-spike input, the synapse
+ * currents and the LIF recurrence in one launch: words [T, B, ceil(F/32)]
+ * (bit k % 32 of word k / 32 is input k; bits past F are ignored), w [F, N]
+ * fp32, bias [N] or NULL, for steps [t_begin, t_end).  precision 1 rounds w
+ * to bf16; precision 0 takes fp32 w exactly (the three-plane bf16 split,
+ * exact products, fp32 sums).  Outputs as myelin_lif_currents_fwd: pre
+ * rows are t - t_begin, spikes use absolute t, rates = count / T (only
+ * with the whole range [0, T)); any output may be NULL.  One workgroup per
+ * batch row: for batches that fill the chip (the 10-neuron readout at
+ * B = 256) it replaces the currents GEMM, its split-K reduce and the
+ * recurrence launch, with the same sums bit for bit.  W^T and a chunk of
+ * bit rows are staged in LDS: myelin_narrow_bits_fits (host only) returns
+ * 1 when an (F, N, precision) layer fits, and the entry rejects one that
+ * does not.
+ * Replaces: the rate readout's forward in _linear_surrogate_lif_checkpoint_
+ *   rate_forward_kernel (triton/lif.py:823-889) for a spiking input.
+ */
+int myelin_narrow_bits_fits(int64_t F, int64_t N, int precision);
+int myelin_linear_lif_fwd_narrow_bits(const int32_t *words, const float *w,
+                                      const float *bias, const float *m0,
+                                      float *m_final, float *spikes, float *pre,
+                                      float *rates, int64_t T, int64_t B,
+                                      int64_t F, int64_t N, int64_t t_begin,
+                                      int64_t t_end, float decay,
+                                      float threshold, float reset, float slope,
+                                      int rule, int precision,
+                                      myelin_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,7 @@ SIGNATURES: dict[str, list] = {
     + [_INT, _INT, _P],
     "myelin_col_sum_f32": [_P, _P, _I64, _I64, _INT, _P],
     "myelin_lif_currents_fwd": [_P] * 9 + [_I64] * 8 + [_F] * 4 + [_INT, _P],
+    "myelin_linear_lif_fwd_narrow_bits": [_P] * 8 + [_I64] * 6 + [_F] * 4 + [_INT, _INT, _P],
 }
 
 _lock = threading.Lock()
@@ -105,6 +106,8 @@ def load() -> ctypes.CDLL:
             lib.myelin_abi_version.restype = ctypes.c_int
             lib.myelin_gemm_workspace_elems.argtypes = [_I64, _I64, _I64, _INT]
             lib.myelin_gemm_workspace_elems.restype = ctypes.c_int64
+            lib.myelin_narrow_bits_fits.argtypes = [_I64, _I64, _INT]
+            lib.myelin_narrow_bits_fits.restype = ctypes.c_int
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes

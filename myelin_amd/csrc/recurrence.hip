@@ -381,16 +381,17 @@ __device__ __forceinline__ void fwd_tail(const FwdArgs &p, int64_t base, int64_t
                                          int64_t &k) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (u >= rem) break;  // uniform
-    const int64_t t = t0 + u;
-    if (p.ckpt_m != nullptr && t == next_ck) {
-      fwd_ckpt<ALIF, V>(p, base, k++, m, a);
-      next_ck += p.chunk;
-    }
-    float sp[V];
+    if (u < rem) {  // uniform
+      const int64_t t = t0 + u;
+      if (p.ckpt_m != nullptr && t == next_ck) {
+        fwd_ckpt<ALIF, V>(p, base, k++, m, a);
+        next_ck += p.chunk;
+      }
+      float sp[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p);
-    st_stream<V>(p.spikes + t * p.BN + base, sp);
+      for (int v = 0; v < V; ++v) sp[v] = neuron_step<ALIF, RULE>(m[v], a[v], cur[u][v], p);
+      st_stream<V>(p.spikes + t * p.BN + base, sp);
+    }
   }
 }
 
@@ -424,10 +425,8 @@ __global__ __launch_bounds__(256) void fwd_dense(FwdArgs p) {
   float tl[U][V];              // the tail's steps
   auto load_tail = [&]() {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (u >= rem) break;  // uniform
-      ld_stream<V>(tl[u], p.x + (Tm + u) * BN + base);
-    }
+    for (int u = 0; u < U; ++u)
+      if (u < rem) ld_stream<V>(tl[u], p.x + (Tm + u) * BN + base);  // uniform
   };
   if (Tm > 0) {
     float nxt[U][V];

@@ -4102,6 +4102,313 @@ extern "C" int myelin_col_sum_f32(const float *in, float *out, int64_t rows, int
   return myelin::launched("col_sum");
 }
 
+namespace {
+// ---------------------------------------------------------------------------
+// Narrow layer (N <= 32 neurons) over a packed-spike input, currents and
+// recurrence in one launch: one workgroup per batch row.  W^T is staged
+// once into LDS as NP bf16 planes [p][n][k] (NP = 1: W rounded to bf16;
+// NP = 3: the exact three-plane split of fp32 W); time is walked in chunks
+// of 64 steps whose packed rows are staged into LDS, every load of a stage
+// in flight at once.  The sums are those of the narrow GEMM and its
+// split-K reduce, bit for bit: wave w takes K splits w, w + 4, ... (the
+// same splits, a function of K alone), each split's 16-k MFMA steps in order
+// into fresh accumulators on both 32-row blocks of the chunk (for NP = 3,
+// planes 2 and 1 into a second accumulator, added at the split's end); N
+// lanes of wave 0 then add the splits' sums in order from 0 and the bias
+// and run the chunk's recurrence with the arithmetic of lif_currents_fwd.
+// Replaces the GEMM, its split-K reduce and the recurrence launch when the
+// batch alone fills the chip.  Dynamic LDS: narrow_lds_bytes.
+// ---------------------------------------------------------------------------
+struct NarrowLifArgs {
+  const int32_t *words;  // [T, B, Wx] input spike bits, Wx = ceil(F / 32), bit k % 32 of word k / 32
+  const float *w;        // [F, N]
+  const float *bias;     // [N] or null
+  const float *m0;       // [B, N] or null (zeros)
+  float *m_final;        // [B, N] or null
+  float *spikes;         // [T, B, N] or null (absolute t)
+  float *pre;            // [t_end - t_begin, B, N] or null (relative t)
+  float *rates;          // [B, N] or null: spike count over [t_begin, t_end) / T
+  int64_t T, B, F, N, Wx, t_begin, t_end, kchunk, splits;
+  int ldw, ldx;          // staged row lengths: W^T planes (bf16), bit rows (words)
+  float decay, thr, reset, slope, rate_denominator;
+};
+
+namespace narrow_fwd {
+constexpr int ROWS = 64;  // steps per chunk: two 32-row accumulator blocks
+constexpr int LDP = 33;   // padded row (floats) of a split's partial currents
+// staged k (bf16) per W^T row and words per bit row: 16 k of slack past F
+// (the last MFMA step reads up to 16 k past a partial end), odd word rows
+inline int narrow_ldw(int64_t F) { return static_cast<int>((F + 15) / 16 * 16 + 8); }
+inline int narrow_ldx(int64_t Wx) { return static_cast<int>(Wx | 1); }
+}  // namespace narrow_fwd
+
+int64_t narrow_lds_bytes(int np, int64_t F, int64_t N, int64_t splits) {
+  using namespace narrow_fwd;
+  const int64_t Wx = (F + 31) / 32;
+  return np * N * narrow_ldw(F) * 2 + ROWS * narrow_ldx(Wx) * 4 + splits * ROWS * LDP * 4;
+}
+
+template <int NP, int RULE>
+__global__ __launch_bounds__(256) void narrow_bits_lif_fwd(NarrowLifArgs p) {
+  using namespace narrow_fwd;
+  extern __shared__ __attribute__((aligned(16))) char narrow_lds[];
+  const int64_t B = p.B, F = p.F, N = p.N, Wx = p.Wx;
+  const int nN = static_cast<int>(N), ldw = p.ldw, ldx = p.ldx, S = static_cast<int>(p.splits);
+  uint16_t *ws = reinterpret_cast<uint16_t *>(narrow_lds);  // [NP][N][ldw]
+  int32_t *xs = reinterpret_cast<int32_t *>(narrow_lds + NP * nN * ldw * 2);  // [ROWS][ldx]
+  float *part = reinterpret_cast<float *>(narrow_lds + NP * nN * ldw * 2 + ROWS * ldx * 4);  // [S][ROWS][LDP]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.x;
+  const int n = lane & 31;         // the B fragment's column and the D column
+  const int kh = 8 * (lane >> 5);  // the fragments' k offset in a 16-k step
+  const bool n_on = n < nN;
+  const int64_t BN = B * N;
+
+  // W^T planes: W [F, N] read in flat order, 8 loads of 4 values in flight
+  // per thread at a time (float4 where the layout allows), then zero past F
+  auto put = [&](int flat, float v) {
+    const int kk = flat / nN, nn = flat - kk * nN;
+    if constexpr (NP == 3) {
+      uint16_t h, mid, l;
+      split3(v, h, mid, l);
+      ws[(0 * nN + nn) * ldw + kk] = h;
+      ws[(1 * nN + nn) * ldw + kk] = mid;
+      ws[(2 * nN + nn) * ldw + kk] = l;
+    } else {
+      ws[nn * ldw + kk] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+    }
+  };
+  const int fn = static_cast<int>(F * N);
+  if (fn % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0) {
+    const f4 *w4 = reinterpret_cast<const f4 *>(p.w);
+    for (int e0 = 0; e0 < fn / 4; e0 += 256 * 8) {
+      f4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = e0 + 256 * j + tid;
+        v[j] = i < fn / 4 ? w4[i] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = e0 + 256 * j + tid;
+        if (i < fn / 4) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) put(4 * i + c, v[j][c]);
+        }
+      }
+    }
+  } else {
+    for (int e0 = 0; e0 < fn; e0 += 256 * 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = e0 + 256 * j + tid;
+        v[j] = i < fn ? p.w[i] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = e0 + 256 * j + tid;
+        if (i < fn) put(i, v[j]);
+      }
+    }
+  }
+  for (int e = tid; e < nN * (ldw - static_cast<int>(F)); e += 256) put(static_cast<int>(F) * nN + e, 0.0f);
+  float m = 0.0f, cnt = 0.0f;
+  if (tid < nN && p.m0 != nullptr) m = p.m0[b * N + tid];
+
+  for (int64_t t0 = p.t_begin; t0 < p.t_end; t0 += ROWS) {
+    const int rows = static_cast<int>(p.t_end - t0 < ROWS ? p.t_end - t0 : ROWS);
+    __syncthreads();  // the previous chunk's bit rows and partials are read
+    // the chunk's bit rows (rows past the chunk repeat its last), zero past
+    // Wx, 8 loads in flight per thread at a time
+    for (int e0 = 0; e0 < ROWS * ldx; e0 += 256 * 8) {
+      int32_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 256 * j + tid, r = e / ldx, c = e - r * ldx;
+        const int64_t t = t0 + (r < rows ? r : rows - 1);
+        v[j] = (e < ROWS * ldx && c < Wx) ? p.words[(t * B + b) * Wx + c] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 256 * j + tid;
+        if (e < ROWS * ldx) xs[e] = v[j];
+      }
+    }
+    __syncthreads();
+    for (int sp = wv; sp < S; sp += 4) {
+      const int64_t kb = sp * p.kchunk, ke = kb + p.kchunk < F ? kb + p.kchunk : F;
+      f32x16 acc[2], acc_s[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = acc_s[i][r] = 0.0f;
+      for (int64_t k = kb; k < ke; k += 16) {
+        const int ka = static_cast<int>(k) + kh;
+        bf16x8 bv[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+          if (n_on) {
+            bv[pl] = *reinterpret_cast<const bf16x8 *>(&ws[(pl * nN + n) * ldw + ka]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[pl][e] = static_cast<__bf16>(0.0f);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          // 8 bits at ka (a multiple of 8, so inside one word)
+          const uint32_t bits = (static_cast<uint32_t>(xs[(32 * i + (lane & 31)) * ldx + (ka >> 5)]) >> (ka & 31)) & 0xFFu;
+          const u32x4 d = {bf16_pair_of_bits(bits), bf16_pair_of_bits(bits >> 2), bf16_pair_of_bits(bits >> 4),
+                           bf16_pair_of_bits(bits >> 6)};
+          const bf16x8 av = __builtin_bit_cast(bf16x8, d);
+          // as gemm_narrow_x3: planes 2 and 1 into acc_s, plane 0 into acc
+#pragma unroll
+          for (int pl = NP - 1; pl > 0; --pl)
+            acc_s[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[pl], acc_s[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[0], acc[i], 0, 0, 0);
+        }
+      }
+      // this split's sums of the chunk's rows
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (n_on)
+            part[(sp * ROWS + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LDP + n] =
+                NP > 1 ? acc[i][r] + acc_s[i][r] : acc[i][r];
+    }
+    __syncthreads();
+    // the currents, into split 0's slots: the splits in order from 0 (the
+    // split-K reduce), or the lone split's sum (the GEMM's own store), then
+    // the bias
+    for (int e = tid; e < rows * nN; e += 256) {
+      const int r = e / nN, nn = e - r * nN;
+      float c;
+      if (S > 1) {
+        float s_ = 0.0f;
+        for (int q = 0; q < S; ++q) s_ = s_ + part[(q * ROWS + r) * LDP + nn];
+        c = 0.0f + s_;
+      } else {
+        c = part[r * LDP + nn];
+      }
+      if (p.bias != nullptr) c = c + p.bias[nn];
+      part[r * LDP + nn] = c;
+    }
+    __syncthreads();
+    if (tid < nN) {
+      const int64_t flat = b * N + tid;
+      for (int r = 0; r < rows; ++r) {
+        float mp = m * p.decay;
+        mp = mp + part[r * LDP + tid];
+        bool spk;
+        if constexpr (RULE == MYELIN_RULE_THRESHOLD)
+          spk = mp >= p.thr;
+        else
+          spk = p.slope * (mp - p.thr) >= 0.0f;
+        const int64_t t = t0 + r;
+        if (p.pre != nullptr) p.pre[(t - p.t_begin) * BN + flat] = mp;
+        if (p.spikes != nullptr) p.spikes[t * BN + flat] = spk ? 1.0f : 0.0f;
+        m = spk ? p.reset : mp;
+        cnt = cnt + (spk ? 1.0f : 0.0f);
+      }
+    }
+  }
+  if (tid < nN) {
+    const int64_t flat = b * N + tid;
+    if (p.m_final != nullptr) p.m_final[flat] = m;
+    if (p.rates != nullptr) p.rates[flat] = cnt / p.rate_denominator;
+  }
+}
+}  // namespace
+
+namespace {
+// dynamic LDS of the one-launch narrow layer (of the 160 KB a CU holds)
+constexpr int64_t kNarrowFusedLds = 150 * 1024;
+}  // namespace
+
+extern "C" int myelin_narrow_bits_fits(int64_t F, int64_t N, int precision) {
+  if (F < 1 || N < 1 || N > 32 || (precision != 0 && precision != 1)) return 0;
+  const int64_t splits = cdiv(F, cdiv(cdiv(F, narrow_splits(F)), 64) * 64);
+  return narrow_lds_bytes(precision == 0 ? 3 : 1, F, N, splits) <= kNarrowFusedLds ? 1 : 0;
+}
+
+extern "C" int myelin_linear_lif_fwd_narrow_bits(const int32_t *words, const float *w, const float *bias,
+                                                 const float *m0, float *m_final, float *spikes, float *pre,
+                                                 float *rates, int64_t T, int64_t B, int64_t F, int64_t N,
+                                                 int64_t t_begin, int64_t t_end, float decay, float threshold,
+                                                 float reset, float slope, int rule, int precision,
+                                                 myelin_stream_t stream) {
+  if (T < 1 || B < 1 || F < 1 || N < 1) return myelin::invalid("linear_lif_fwd_narrow_bits: T, B, F, N must be positive");
+  if (N > 32) return myelin::invalid("linear_lif_fwd_narrow_bits: at most 32 neurons (got %lld)", (long long)N);
+  if (t_begin < 0 || t_end > T || t_begin >= t_end) return myelin::invalid("linear_lif_fwd_narrow_bits: bad time range");
+  if (words == nullptr || w == nullptr) return myelin::invalid("linear_lif_fwd_narrow_bits: words and w are required");
+  if (rates != nullptr && (t_begin != 0 || t_end != T))
+    return myelin::invalid("linear_lif_fwd_narrow_bits: rates need the whole range [0, T)");
+  if (rule != MYELIN_RULE_THRESHOLD && rule != MYELIN_RULE_SURROGATE)
+    return myelin::invalid("linear_lif_fwd_narrow_bits: unknown rule %d", rule);
+  if (precision != 0 && precision != 1) return myelin::invalid("linear_lif_fwd_narrow_bits: precision must be 0 or 1");
+  if (B > 0x7fffffff) return myelin::invalid("linear_lif_fwd_narrow_bits: B too large");
+  NarrowLifArgs a{};
+  a.words = words;
+  a.w = w;
+  a.bias = bias;
+  a.m0 = m0;
+  a.m_final = m_final;
+  a.spikes = spikes;
+  a.pre = pre;
+  a.rates = rates;
+  a.T = T;
+  a.B = B;
+  a.F = F;
+  a.N = N;
+  a.Wx = (F + 31) / 32;
+  a.t_begin = t_begin;
+  a.t_end = t_end;
+  // the narrow GEMM's K splits (its workspace always holds them)
+  a.kchunk = cdiv(cdiv(F, narrow_splits(F)), 64) * 64;
+  a.splits = cdiv(F, a.kchunk);
+  a.ldw = narrow_fwd::narrow_ldw(F);
+  a.ldx = narrow_fwd::narrow_ldx(a.Wx);
+  const int64_t lds = narrow_lds_bytes(precision == 0 ? 3 : 1, F, N, a.splits);
+  if (lds > kNarrowFusedLds)
+    return myelin::invalid("linear_lif_fwd_narrow_bits: needs %lld bytes of LDS (at most %lld); see "
+                           "myelin_narrow_bits_fits", (long long)lds, (long long)kNarrowFusedLds);
+  a.decay = decay;
+  a.thr = threshold;
+  a.reset = reset;
+  a.slope = slope;
+  a.rate_denominator = static_cast<float>(T);
+  hipStream_t s = myelin::as_hip(stream);
+  const dim3 grid(static_cast<unsigned>(B)), block(256);
+  const bool thr = rule == MYELIN_RULE_THRESHOLD;
+  const size_t shm = static_cast<size_t>(lds);
+  // dynamic LDS beyond the default 64 KB: raised once per instance
+  static const hipError_t attr[4] = {
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&narrow_bits_lif_fwd<3, MYELIN_RULE_THRESHOLD>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kNarrowFusedLds)),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&narrow_bits_lif_fwd<3, MYELIN_RULE_SURROGATE>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kNarrowFusedLds)),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&narrow_bits_lif_fwd<1, MYELIN_RULE_THRESHOLD>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kNarrowFusedLds)),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&narrow_bits_lif_fwd<1, MYELIN_RULE_SURROGATE>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kNarrowFusedLds))};
+  for (hipError_t e : attr)
+    if (e != hipSuccess) {
+      myelin::set_error("linear_lif_fwd_narrow_bits: LDS attribute: %s", hipGetErrorString(e));
+      return MYELIN_EHIP;
+    }
+  // fp32 (precision 0): the exact three-plane split; bf16: W rounded
+  if (precision == 0)
+    thr ? narrow_bits_lif_fwd<3, MYELIN_RULE_THRESHOLD><<<grid, block, shm, s>>>(a)
+        : narrow_bits_lif_fwd<3, MYELIN_RULE_SURROGATE><<<grid, block, shm, s>>>(a);
+  else
+    thr ? narrow_bits_lif_fwd<1, MYELIN_RULE_THRESHOLD><<<grid, block, shm, s>>>(a)
+        : narrow_bits_lif_fwd<1, MYELIN_RULE_SURROGATE><<<grid, block, shm, s>>>(a);
+  return myelin::launched("linear_lif_fwd_narrow_bits");
+}
+
 extern "C" int myelin_lif_currents_fwd(const float *currents, const float *m0, float *m_final, float *spikes,
                                        float *pre, int32_t *packed, float *rates, float *counts, float *ckpt, int64_t T,
                                        int64_t B, int64_t N, int64_t t_begin, int64_t t_end, int64_t pre_origin,

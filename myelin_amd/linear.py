@@ -295,6 +295,12 @@ def _span(T: int, checkpoint: int, BN: int, budget: int = _CURRENT_CHUNK_ELEMS) 
     return checkpoint * max(1, min(math.ceil(T / checkpoint), budget // (checkpoint * BN)))
 
 
+# a narrow layer (<= 32 neurons) over packed spikes takes the one-launch
+# currents + recurrence kernel from this batch size on: one workgroup per
+# batch row, so smaller batches leave the chip idle and the GEMM + recurrence
+# launches are faster
+_NARROW_FUSED_MIN_B = 128
+
 # forward chunk budget (floats) of the memory-lean policy: the forward's
 # buffers are transient and never set a checkpointed step's peak, which the
 # backward's span buffers do, so the forward keeps chunks large enough for
@@ -368,8 +374,18 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
             _lib.call("myelin_linear_lif_fwd", _lib.ptr(x), _lib.ptr(w), *outs, prec, stream)
         return
     dev = x.device
-    step = max(1, min(t1 - t0, budget // (B * N)))
     p0 = t0 if pre_from is None else pre_from  # pre holds the steps from p0 on
+    if (x_bits is not None and N <= 32 and B >= _NARROW_FUSED_MIN_B and not exact and packed is None
+            and ckpt is None and p0 == t0 and (rates is None or (t0 == 0 and t1 == T))
+            and rule in (_lib.RULE_THRESHOLD, _lib.RULE_SURROGATE) and _lib.load().myelin_narrow_bits_fits(F, N, prec)):
+        # a narrow layer over spikes with a batch that fills the chip: the
+        # currents and the recurrence in one launch (never for a layer whose
+        # backward recomputes, which must repeat its forward's GEMM)
+        _lib.call("myelin_linear_lif_fwd_narrow_bits", _lib.ptr(x_bits), _lib.ptr(w), _lib.ptr(b), _lib.ptr(m0),
+                  _lib.ptr(m_final), _lib.ptr(spikes), _lib.ptr(pre), _lib.ptr(rates), T, B, F, N, t0, t1, decay,
+                  threshold, reset, slope, rule, prec, stream)
+        return
+    step = max(1, min(t1 - t0, budget // (B * N)))
     bounds = sorted({*range(t0, t1, step), t1} | ({p0} if t0 < p0 < t1 else set()))
     n = len(bounds) - 1
     # several chunks on the fp32 engine: each chunk's GEMM runs on the side

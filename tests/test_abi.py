@@ -174,3 +174,34 @@ def test_split_synapse_entry_points_validate_on_the_host():
     assert _lib.load().myelin_split_bf16x3(None, None, 0, 5, 1, None) == 0
     assert _lib.load().myelin_gemm_parts(None, None, 3, 0, None, None, 0, 4, 4, 4, 4, 4, 0, 0, 0, None, 0,
                                          None) == 0
+
+
+def test_narrow_one_launch_entry_validates_on_the_host():
+    nb = "myelin_linear_lif_fwd_narrow_bits"
+    # words, w, bias, m0, m_final, spikes, pre, rates, T, B, F, N, t0, t1, decay, thr, reset, slope, rule, prec
+    with pytest.raises(ValueError, match="at most 32 neurons"):
+        _lib.call(nb, 16, 16, None, None, None, None, 16, None, 4, 4, 8, 33, 0, 4, 0.9, 1.0, 0.0, 10.0, 0, 1, None)
+    with pytest.raises(ValueError, match="words and w are required"):
+        _lib.call(nb, None, 16, None, None, None, None, 16, None, 4, 4, 8, 4, 0, 4, 0.9, 1.0, 0.0, 10.0, 0, 1, None)
+    with pytest.raises(ValueError, match="whole range"):
+        _lib.call(nb, 16, 16, None, None, None, None, None, 16, 4, 4, 8, 4, 1, 4, 0.9, 1.0, 0.0, 10.0, 0, 1, None)
+    with pytest.raises(ValueError, match="bad time range"):
+        _lib.call(nb, 16, 16, None, None, None, None, 16, None, 4, 4, 8, 4, 3, 3, 0.9, 1.0, 0.0, 10.0, 0, 1, None)
+    with pytest.raises(ValueError, match="unknown rule"):
+        _lib.call(nb, 16, 16, None, None, None, None, 16, None, 4, 4, 8, 4, 0, 4, 0.9, 1.0, 0.0, 10.0, 17, 1, None)
+    with pytest.raises(ValueError, match="precision must be"):
+        _lib.call(nb, 16, 16, None, None, None, None, 16, None, 4, 4, 8, 4, 0, 4, 0.9, 1.0, 0.0, 10.0, 0, 2, None)
+
+
+def test_narrow_one_launch_size_query_is_host_only():
+    lib = _lib.load()
+    # the 2048 -> 10 bf16 readout fits (91,552 bytes of LDS), its fp32
+    # form (three W planes) does not; 2048 -> 5 at fp32 does; the 4096 -> 20
+    # fp32 readout does not; no layer over 32 neurons or with a bad precision
+    assert lib.myelin_narrow_bits_fits(2048, 10, _lib.PREC["bf16"]) == 1
+    assert lib.myelin_narrow_bits_fits(2048, 10, _lib.PREC["fp32"]) == 0
+    assert lib.myelin_narrow_bits_fits(2048, 5, _lib.PREC["fp32"]) == 1
+    assert lib.myelin_narrow_bits_fits(4096, 20, _lib.PREC["fp32"]) == 0
+    assert lib.myelin_narrow_bits_fits(100, 33, _lib.PREC["bf16"]) == 0
+    assert lib.myelin_narrow_bits_fits(100, 10, 2) == 0
+    assert lib.myelin_narrow_bits_fits(0, 10, 1) == 0
