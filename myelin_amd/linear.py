@@ -470,18 +470,18 @@ def _lif_fwd(x, w, b, m0, t0, t1, decay, threshold, reset, slope, rule, prec, st
                 t_.record_stream(side)
 
 
-_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+_SIDE_STREAMS: dict[tuple[int, int], torch.cuda.Stream] = {}
 
 
-def _side_stream(dev: torch.device) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for work that overlaps
-    the current stream's, created once."""
+def _side_stream(dev: torch.device, which: int = 0) -> torch.cuda.Stream:
+    """Side stream `which` of a device (default priority) for work that
+    overlaps the current stream's, created once."""
 
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    s = _SIDE_STREAMS.get(idx)
+    s = _SIDE_STREAMS.get((idx, which))
     if s is None:
         s = torch.cuda.Stream(device=idx)
-        _SIDE_STREAMS[idx] = s
+        _SIDE_STREAMS[(idx, which)] = s
     return s
 
 

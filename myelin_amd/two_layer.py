@@ -213,24 +213,52 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
             cur = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             pre_o = torch.empty((L0, B, O), device=dev) if pre_all is None else None
             # the packed variant with the readout's whole trace kept: the
-            # readout's reverse pass and dW_o run once over all T before the
-            # spans (the reverse pass carries its adjoint exactly as the
-            # span walk does; dW_o reads every step's words at once), and
-            # each hidden span reads its rows of G_o
+            # readout's reverse pass runs span by span from the last on a
+            # stream of its own (a few waves walking T: beside the hidden
+            # spans it costs them nothing), each hidden span waiting for its
+            # rows of G_o only; dW_o reads every step's words at once, after
+            # the spans (the reverse pass carries its adjoint across spans
+            # exactly).  The memory-lean policy (one-chunk spans) runs the
+            # reverse pass as one launch and dW_o before the spans, on the
+            # one stream: there the blocks the side stream holds raise the
+            # peak and the many short spans gain nothing from the overlap
+            main = torch.cuda.current_stream(dev)
             whole_o = words is not None and pre_all is not None
             G_o_all = None
+            o_side = whole_o and not lean
             if whole_o:
                 G_o_all = torch.empty((T, B, O), device=dev)
-                _lib.call(
-                    "myelin_linear_pre_bwd",
-                    _lib.ptr(pre_all), None, _lib.ptr(g_rates), _lib.ptr(gm_o), _lib.ptr(G_o_all), _lib.DT[torch.float32],
-                    _lib.ptr(gbo_acc), T, B * O, T, decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, stream,
-                )
-                if gwo is not None:
-                    _gemm(words, G_o_all, gwo, H, O, T * B, words.shape[-1], O, O, True, False, False, prec, stream,
-                          a_bits=True, col_sum=None if gbo is None else (gbo_acc, gbo))
-                elif gbo is not None:
-                    _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
+                o_stream = _side_stream(dev, 1) if o_side else main
+                o_ready = [torch.cuda.Event() for _ in range(NS)] if o_side else None
+                if o_side:
+                    o_stream.wait_stream(main)
+                with torch.cuda.stream(o_stream):
+                    for k in (range(NS - 1, -1, -1) if o_side else (None,)):
+                        a0, a1 = (k * S, min(k * S + S, T)) if o_side else (0, T)
+                        _lib.call(
+                            "myelin_linear_pre_bwd",
+                            _lib.ptr(pre_all[a0:a1]), None, _lib.ptr(g_rates), _lib.ptr(gm_o),
+                            _lib.ptr(G_o_all[a0:a1]), _lib.DT[torch.float32], _lib.ptr(gbo_acc), a1 - a0, B * O, T,
+                            decay, threshold, reset, slope, sid, _lib.RULE_THRESHOLD, o_stream.cuda_stream,
+                        )
+                        if o_side:
+                            o_ready[k].record(o_stream)
+                if o_side:
+                    for t_ in (pre_all, g_rates, gm_o, G_o_all, gbo_acc):
+                        if t_ is not None:
+                            t_.record_stream(o_stream)
+
+                def readout_weight_grads():
+                    if o_side:
+                        main.wait_event(o_ready[0])
+                    if gwo is not None:
+                        _gemm(words, G_o_all, gwo, H, O, T * B, words.shape[-1], O, O, True, False, False, prec,
+                              stream, a_bits=True, col_sum=None if gbo is None else (gbo_acc, gbo))
+                    elif gbo is not None:
+                        _lib.call("myelin_col_sum_f32", _lib.ptr(gbo_acc), _lib.ptr(gbo), B, O, 0, stream)
+
+                if not o_side or not need_hidden:
+                    readout_weight_grads()
                 if not need_hidden:
                     return gx, None, None, gwo, gbo, None, None, None, None, None, None, None, None, None
             G_o = None if whole_o else torch.empty((L0, B, O), device=dev)
@@ -272,7 +300,6 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 pre_b = [pool[:L0 * B * H].view(L0, B, H)]
             else:
                 pre_b = [torch.empty((L0, B, H), device=dev) if need_hidden else None for _ in range(nset)]
-            main = torch.cuda.current_stream(dev)
             side = _side_stream(dev) if nset == 2 else main
             ready = [torch.cuda.Event() for _ in range(nset)]
             free = [torch.cuda.Event() for _ in range(nset)]
@@ -315,6 +342,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                     main.wait_event(ready[i])
                 hs, pre_h = hs_b[i], pre_b[i]
                 if whole_o:
+                    if o_side:
+                        main.wait_event(o_ready[k])
                     G_o = G_o_all[t0:t1]
                 else:
                     s_in = words[t0:t1] if words is not None else hs[:L]
@@ -380,6 +409,8 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
                 for t_ in (*hs_b, *pre_b, xs.x if lazy else xs, wh, ck_h, bh, wt):
                     if t_ is not None:
                         t_.record_stream(side)
+            if o_side:
+                readout_weight_grads()
             if gbh is not None and gwh is None:
                 _lib.call("myelin_col_sum_f32", _lib.ptr(gbh_acc), _lib.ptr(gbh), B, H, 0, stream)
             if gbo is not None and gwo is None and not whole_o:
