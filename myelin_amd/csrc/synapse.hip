@@ -641,11 +641,10 @@ struct NarrowB {
 // Stages B(k, n) for k in [ks, ks + kpad), n < N: put(n, k - ks, value),
 // zero past klen; rows past N are never stored, so they stay unwritten.  The
 // elements are walked flat in memory order -- contiguous when ldb equals the
-// contiguous extent -- 8 loads issued before their LDS writes.
-template <bool TB, typename Put>
+// contiguous extent -- R loads issued before their LDS writes.
+template <bool TB, typename Put, int R = 8>
 __device__ __forceinline__ void stage_narrow(const GemmArgs &g, int64_t ks, int klen, int kpad, int N, int tid,
                                              int nt, Put put) {
-  constexpr int R = 8;
   const float *B = static_cast<const float *>(g.B);
   const int total = N * klen;
   // e / d as a multiply-high by ceil(2^32 / d) (d >= 2; d = 1 is e
@@ -974,6 +973,200 @@ __global__ __launch_bounds__(64 * NarrowBits<NP>::WAVES) void gemm_narrow_bits(G
     for (int r = 0; r < 16; ++r) acc[r] = acc[r] + acc_s[r];
   }
   store_acc(g, acc, m0, lane & 31, lane, blockIdx.y);
+}
+
+// Narrow GEMM with transposed packed-bit A: dW_o = S^T G_o, A(m, k) = bit
+// m%32 of word A[k*lda + m/32] (k a batch-step row, m a hidden neuron), the
+// same MFMAs on the same k in the same order as gemm_narrow_x3 / gemm_narrow
+// with that operand, so the bits equal theirs.  A lane of the MFMA needs 8
+// k of one m: 8 rows' words, one bit each, which those kernels load and
+// test one by one.  Here each lane of a wave loads one row's words of the
+// wave's four 32-neuron word columns (one 16-byte load), 64 rows a wave;
+// per column the two 32 x 32 bit blocks (lanes 0-31 and 32-63) are turned
+// around with a 5-stage butterfly across lanes (stage D: lanes l and l ^ D
+// swap the off-diagonal D x D blocks of their rows, a lane shuffle, a
+// rotate and a bit-field insert), after which lane m holds one word of 32
+// rows' bits of its neuron.  The rows are loaded in the order
+// rho(j) = 16 (j%16 / 4) + 2 (j%4) + j/16 (+ 8 in lanes 32-63), so that
+// bits b and b + 16 of that word are the rows of the lo and hi bf16 of
+// fragment pair b%4 of group b/4: one mask and one 24-bit multiply by
+// 0x3F80 make a pair of 0/1 bf16 values.  Four waves of four word columns
+// each share one staged sub-chunk of B (NP planes, as gemm_narrow_bits);
+// two workgroups per CU, so one stages while the other runs its MFMAs, and
+// the 64000-row, 4096-neuron dW_o (8 workgroups per K split, 63 splits)
+// fits the chip in one round.  A lane's words are loaded two 64-row blocks
+// ahead of their MFMAs.  That dW_o (fp32, three planes) measured 168 -> 66
+// us, with its split-K reduce 176 -> 75 us; bf16 precision 51 us.  Counters
+// of the fp32 kernel: MFMA busy 31 %, VALU busy ~37 %, a third of each
+// wave's cycles waiting (two waves a SIMD: the transposes' lane shuffles
+// and the loads are latency the other wave only partly covers).
+template <int NP>
+struct NarrowBitsT {
+  static constexpr int KSUB = 256, LD = KSUB + 8, WAVES = 4, TILES = 4, COLS = WAVES * TILES;
+  alignas(16) uint16_t b[NP][32][LD];
+};
+
+// One butterfly stage of the transpose (the rotate amount and the mask are
+// the lane's own: rows with bit D of the lane index clear keep their
+// columns with bit D clear).
+template <int D>
+__device__ __forceinline__ uint32_t xpose_stage(uint32_t w, uint32_t rot, uint32_t keep) {
+  uint32_t p;
+  if constexpr (D == 1)
+    p = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(w), 0xB1, 0xF, 0xF, true));
+  else if constexpr (D == 2)
+    p = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(w), 0x4E, 0xF, 0xF, true));
+  else
+    p = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(w), 0x1F | (D << 10)));
+  const uint32_t q = __builtin_amdgcn_alignbit(p, p, rot);
+  return (w & keep) | (q & ~keep);
+}
+
+template <int NP>
+__global__ __launch_bounds__(64 * NarrowBitsT<NP>::WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_narrow_bits_t(GemmArgs g) {
+  using L = NarrowBitsT<NP>;
+  constexpr int GS = 16, KSUB = L::KSUB, WAVES = L::WAVES, TILES = L::TILES;
+  __shared__ L sb;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * g.kchunk;
+  const int64_t ke = (kb + g.kchunk < g.K) ? kb + g.kchunk : g.K;
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * L::COLS + TILES * w;  // the wave's first word column
+  const int N = static_cast<int>(g.N);
+  const int kh = (lane >> 5) * 8;
+  const int j = lane & 31;
+  const int rho = 16 * ((j & 15) >> 2) + 2 * (j & 3) + (j >> 4) + kh;  // the lane's row of a 64-row block
+  const int32_t *A = static_cast<const int32_t *>(g.A);
+  bool on[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) on[t] = 32 * (col0 + t) < g.M;  // uniform per wave
+  // the lane's rotate amounts and kept-column masks, stages 16, 8, 4, 2, 1
+  uint32_t rot[5], keep[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int D = 16 >> i;
+    const uint32_t m = i == 0 ? 0x0000FFFFu : i == 1 ? 0x00FF00FFu : i == 2 ? 0x0F0F0F0Fu : i == 3 ? 0x33333333u : 0x55555555u;
+    const bool top = (lane & D) == 0;
+    rot[i] = top ? 32 - D : D;
+    keep[i] = top ? m : ~m;
+  }
+  // a 64-row block's words per lane (rows past ke read as 0): the wave's
+  // four columns of a row in one 16-byte load where rows allow it
+  const bool vec = on[TILES - 1] && g.lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  auto load_words = [&](int64_t row, uint32_t (&wd)[TILES]) {
+    static_assert(TILES == 4, "one 16-byte load holds the four tiles' words");
+    if (vec) {
+      const u32x4 v = row < ke ? *reinterpret_cast<const u32x4 *>(A + row * g.lda + col0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) wd[t] = v[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+        wd[t] = (on[t] && row < ke) ? static_cast<uint32_t>(A[row * g.lda + col0 + t]) : 0u;
+    }
+  };
+
+  f32x16 acc[TILES], acc_s[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc[t][r] = 0.0f;
+      acc_s[t][r] = 0.0f;
+    }
+
+  // the 32 x 32 bit blocks of a 64-row block turned around: x[t] the
+  // lane's word of 32 rows of its neuron, x8[t] the same shifted down by 8
+  auto transpose = [&](const uint32_t (&wd)[TILES], uint32_t (&x)[TILES], uint32_t (&x8)[TILES]) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      uint32_t v = wd[t];
+      v = xpose_stage<16>(v, rot[0], keep[0]);
+      v = xpose_stage<8>(v, rot[1], keep[1]);
+      v = xpose_stage<4>(v, rot[2], keep[2]);
+      v = xpose_stage<2>(v, rot[3], keep[3]);
+      v = xpose_stage<1>(v, rot[4], keep[4]);
+      x[t] = v;
+      x8[t] = v >> 8;
+    }
+  };
+  // group jg of the sub-chunk (16 k) for every tile: groups 0-1 of a block
+  // take bits 0-7 (and 16-23) of the word, groups 2-3 bits 8-15 (24-31),
+  // from the word shifted down by 8.  A tile past M runs on zero words and
+  // is not stored.
+  auto group = [&](int jg, int q, const uint32_t (&x)[TILES], const uint32_t (&x8)[TILES]) {
+    const int o = jg * GS + kh;
+    bf16x8 bv[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) bv[p] = *reinterpret_cast<const bf16x8 *>(&sb.b[p][lane & 31][o]);
+    bf16x8 av[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const uint32_t xb = q >= 2 ? x8[t] : x[t];
+      u32x4 d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int bp = (4 * q + i) & 7;
+        d[i] = __umul24(xb & (0x10001u << bp), 0x3F80u >> bp);
+      }
+      av[t] = __builtin_bit_cast(bf16x8, d);
+    }
+    // as gemm_narrow_x3: B planes 2 and 1 into acc_s, plane 0 into acc
+#pragma unroll
+    for (int p = NP - 1; p > 0; --p)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+        acc_s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[t], bv[p], acc_s[t], 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < TILES; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[t], bv[0], acc[t], 0, 0, 0);
+  };
+
+  for (int64_t ks = kb; ks < ke; ks += KSUB) {
+    const int klen = static_cast<int>((ke - ks < KSUB) ? ke - ks : KSUB);
+    const int kpad = (klen + GS - 1) / GS * GS;
+    const int ng = kpad / GS;
+    // blocks 0-1's words, issued before B is staged; each later block's two
+    // blocks ahead of its MFMAs
+    uint32_t wa[TILES], wb[TILES];
+    load_words(ks + rho, wa);
+    load_words(ks + 64 + rho, wb);
+    if (ks != kb) __syncthreads();  // the previous sub-chunk's fragments are read
+    auto put = [&](int n, int kk, float v) {
+      if constexpr (NP == 3) {
+        uint16_t h, mid, l;
+        split3(v, h, mid, l);
+        sb.b[0][n][kk] = h;
+        sb.b[1][n][kk] = mid;
+        sb.b[2][n][kk] = l;
+      } else {
+        sb.b[0][n][kk] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+      }
+    };
+    // 10 loads in flight per thread: the 256 x 20 sub-chunk in two rounds
+    stage_narrow<false, decltype(put), 10>(g, ks, klen, kpad, N, tid, 64 * WAVES, put);
+    __syncthreads();
+#pragma unroll 1
+    for (int s = 0; 4 * s < ng; ++s) {
+      uint32_t x[TILES], x8[TILES];
+      transpose(wa, x, x8);
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) wa[t] = wb[t];
+      if (4 * s + 8 < ng) load_words(ks + 64 * (s + 2) + rho, wb);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (4 * s + q < ng) group(4 * s + q, q, x, x8);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    if (!on[t]) continue;
+    if constexpr (NP > 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][r] = acc[t][r] + acc_s[t][r];
+    }
+    store_acc(g, acc[t], 32 * (col0 + t), lane & 31, lane, blockIdx.y);
+  }
 }
 
 // Rounds an operand value to the MFMA input type of the precision (bf16:
@@ -3500,6 +3693,13 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
         gemm_narrow_bits<3><<<wide, dim3(64 * NarrowBits<3>::WAVES), 0, s>>>(g);
       else
         gemm_narrow_bits<1><<<wide, dim3(64 * NarrowBits<1>::WAVES), 0, s>>>(g);
+    } else if (bits && ta && !tb) {
+      // transposed bit rows (dW_o): word columns turned around in registers
+      const dim3 cols(static_cast<unsigned>(cdiv(cdiv(g.M, 32), NarrowBitsT<1>::COLS)), static_cast<unsigned>(splits));
+      if constexpr (PREC == 0)
+        gemm_narrow_bits_t<3><<<cols, dim3(64 * NarrowBitsT<3>::WAVES), 0, s>>>(g);
+      else
+        gemm_narrow_bits_t<1><<<cols, dim3(64 * NarrowBitsT<1>::WAVES), 0, s>>>(g);
     } else if constexpr (PREC == 0) {
       // fp32: the exact three-plane split on the bf16 MFMA
       if (bits)

@@ -30,8 +30,8 @@ import myelin_amd as myelin
 from myelin_amd import _lib
 from myelin_amd.linear import _gemm, linear
 from oracle import torch_ref as R
-from tests.helpers import (assert_elementwise_close_or_truer, assert_norm_close, f32_params, raster_agreement, seeded,
-                           to_np)
+from tests.helpers import (assert_elementwise_close_or_truer, assert_norm_close, assert_same_bits, f32_params,
+                           raster_agreement, seeded, to_np)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -694,6 +694,38 @@ def test_narrow_gemm_rows_independent_of_m(bits, prec, K):
     if prec == "fp32":
         ref = A.double() @ W.double()
         assert_norm_close(full.cpu().double(), ref, 1e-6, "narrow fp32 (exact split) vs float64")
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+@pytest.mark.parametrize("M,K", [(4096, 64000), (4056, 63993)])
+def test_transposed_bit_operand_at_readout_scale(prec, M, K):
+    """dW_o = S^T G_o of the 4096 -> 20 readout at T = 2000, B = 32 (K =
+    64000 batch-step rows in 63 K splits; the transposed packed-bit operand
+    runs its own kernel, which turns 32 x 32 bit blocks around across lanes)
+    and a ragged variant (a partial word column and workgroup, a partial
+    last group): the same bits as the same 0/1 matrix given densely, and at
+    fp32 precision within 1e-6 of float64."""
+
+    N = 20
+    _print_case(test="bits_transposed", M=M, K=K, prec=prec)
+    g = torch.Generator(device=DEV).manual_seed(M + K + 2 * (prec == "fp32"))
+    Ad = (torch.rand(K, M, generator=g, device=DEV) < 0.1).float()
+    Bd = torch.randn(K, N, generator=g, device=DEV) * 1e-3
+    bias = torch.randn(N, generator=g, device=DEV)
+    words = myelin.pack_spikes(Ad).data
+    stream = _lib.stream(torch.device(DEV))
+    for acc in (False, True):
+        C0 = torch.randn(M, N, generator=g, device=DEV)
+        dense, bits = C0.clone(), C0.clone()
+        _gemm(Ad, Bd, dense, M, N, K, M, N, N, True, False, acc, _lib.PREC[prec], stream, bias=bias)
+        _gemm(words, Bd, bits, M, N, K, words.shape[1], N, N, True, False, acc, _lib.PREC[prec], stream, bias=bias,
+              a_bits=True)
+        assert_same_bits(bits, dense, f"transposed bits, accumulate={acc}")
+    if prec == "fp32":
+        C = torch.empty(M, N, device=DEV)
+        _gemm(words, Bd, C, M, N, K, words.shape[1], N, N, True, False, False, _lib.PREC[prec], stream, a_bits=True)
+        ref = Ad.double().t() @ Bd.double()
+        assert_norm_close(C.double(), ref, 1e-6, "transposed bits (exact split) vs float64")
 
 
 def test_gemm_packed_bit_operand_checks():
