@@ -475,9 +475,15 @@ __global__ __launch_bounds__(256) void fwd_packed(FwdArgs p) {
   const int64_t flat = b * p.N + n;
   const int64_t T = p.T, BN = p.BN;
   const int64_t words_per_step = p.B * p.W;
+  // rows of an even word count from an 8-byte aligned base: the wave's two
+  // words (g_wave is even) are one aligned 8-byte store
+  const bool pair = words_per_step % 2 == 0 && (reinterpret_cast<uintptr_t>(p.packed) & 7) == 0;
   const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
-  // the wave's first word; waves start at multiples of 64 lanes, i.e. even words
-  const int64_t g_wave = (gid - lane) >> 5;
+  // the wave's first word; waves start at multiples of 64 lanes, i.e. even
+  // words (wave-uniform: made a scalar)
+  const int64_t g_v = (gid - lane) >> 5;
+  const int64_t g_wave = static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(g_v)))) |
+                         (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(g_v >> 32))) << 32);
 
   float m = active ? p.m0[flat] : 0.0f;
   float a = (ALIF && active) ? p.a0[flat] : 0.0f;
@@ -510,8 +516,14 @@ __global__ __launch_bounds__(256) void fwd_packed(FwdArgs p) {
         if (active) s = neuron_step<ALIF, RULE>(m, a, cur[u], p) != 0.0f;
         const uint64_t bits = __ballot(s);
         int32_t *row = p.packed + t * words_per_step;
-        if (lane == 0 && g_wave < words_per_step) row[g_wave] = static_cast<int32_t>(bits & 0xffffffffu);
-        if (lane == 32 && g_wave + 1 < words_per_step) row[g_wave + 1] = static_cast<int32_t>(bits >> 32);
+        if (pair) {
+          // the wave's two words as one 8-byte store, the same value from
+          // every lane: no lane-selected branch a step
+          if (g_wave < words_per_step) *reinterpret_cast<uint64_t *>(row + g_wave) = bits;
+        } else {
+          if (lane == 0 && g_wave < words_per_step) row[g_wave] = static_cast<int32_t>(bits & 0xffffffffu);
+          if (lane == 32 && g_wave + 1 < words_per_step) row[g_wave + 1] = static_cast<int32_t>(bits >> 32);
+        }
       }
     }
   }

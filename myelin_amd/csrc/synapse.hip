@@ -2334,8 +2334,11 @@ __global__ __launch_bounds__(256) void linear_lif_fwd(LinArgs p) {
           const uint64_t bits = __ballot(s[q]);
           const int64_t b = b0 + Q * w + q;
           const int64_t word = n0 / 32 + (lane >> 5);
-          if ((lane & 31) == 0 && b < p.B && word < p.W)
-            p.packed[(t * p.B + b) * p.W + word] = static_cast<int32_t>(lane ? (bits >> 32) : (bits & 0xffffffffu));
+          // every lane of a half-wave stores its half's word (one value to
+          // one address): no lane-selected branch a step
+          if (b < p.B && word < p.W)
+            p.packed[(t * p.B + b) * p.W + word] =
+                static_cast<int32_t>((lane & 32) ? (bits >> 32) : (bits & 0xffffffffu));
         }
       }
     }
@@ -2582,8 +2585,11 @@ __global__ __launch_bounds__(256) void linear_lif_fwd_big(LinArgs p) {
           const uint64_t bits = __ballot(s[q]);
           const int64_t b = brow + q;
           const int64_t word = (n0 + 64 * h) / 32 + (lane >> 5);
-          if ((lane & 31) == 0 && b < p.B && word < p.W)
-            p.packed[(t * p.B + b) * p.W + word] = static_cast<int32_t>(lane ? (bits >> 32) : (bits & 0xffffffffu));
+          // every lane of a half-wave stores its half's word (one value to
+          // one address): no lane-selected branch a step
+          if (b < p.B && word < p.W)
+            p.packed[(t * p.B + b) * p.W + word] =
+                static_cast<int32_t>((lane & 32) ? (bits >> 32) : (bits & 0xffffffffu));
         }
       }
     }
@@ -2870,9 +2876,11 @@ __global__ __launch_bounds__(acc_fwd::NT) __attribute__((amdgpu_waves_per_eu(2))
         if (outs & 16) cnt[i][j] = cnt[i][j] + (sp ? 1.0f : 0.0f);
         if (outs & 4) {
           // lanes 0-31: 32 neurons of the block's first batch row; 32-63: the next row
+          // (every lane of a half stores its half's word: one value to one address)
           const uint64_t bits = __ballot(bok[i] && nok[j] && sp);
-          if ((lane & 31) == 0 && bok[i] && wpk + j < p.W)
-            store_at(pk_c + 4 * j, pk_off[i], __builtin_bit_cast(float, static_cast<uint32_t>(lane ? (bits >> 32) : bits)));
+          if (bok[i] && wpk + j < p.W)
+            store_at(pk_c + 4 * j, pk_off[i],
+                     __builtin_bit_cast(float, static_cast<uint32_t>((lane & 32) ? (bits >> 32) : bits)));
         }
       }
     }
@@ -3292,8 +3300,14 @@ __device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, b
   cnt = cnt + (sp ? 1.0f : 0.0f);
   if constexpr (PK) {
     const uint64_t bits = __ballot(act && sp);
-    if (lane == 0 && gw < p.B * p.W) o.pk[gw] = static_cast<int32_t>(bits & 0xffffffffu);
-    if (lane == 32 && gw + 1 < p.B * p.W) o.pk[gw + 1] = static_cast<int32_t>(bits >> 32);
+    if (p.B * p.W % 2 == 0 && (reinterpret_cast<uintptr_t>(p.packed) & 7) == 0) {
+      // the wave's two words as one 8-byte store, the same value from every
+      // lane (gw is even and wave-uniform): no lane-selected branch a step
+      if (gw < p.B * p.W) *reinterpret_cast<uint64_t *>(o.pk + gw) = bits;
+    } else {
+      if (lane == 0 && gw < p.B * p.W) o.pk[gw] = static_cast<int32_t>(bits & 0xffffffffu);
+      if (lane == 32 && gw + 1 < p.B * p.W) o.pk[gw + 1] = static_cast<int32_t>(bits >> 32);
+    }
     o.pk += p.B * p.W;
   }
 }
@@ -3308,7 +3322,10 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const bool act = (b < p.B) && (n < p.N);
   const int64_t flat = act ? b * p.N + n : 0, BN = p.B * p.N;
   const int lane = static_cast<int>(threadIdx.x & 63);
-  const int64_t gw = (gid - lane) >> 5;  // the wave's first packed word
+  // the wave's first packed word (wave-uniform: made a scalar)
+  const int64_t gw_v = (gid - lane) >> 5;
+  const int64_t gw = static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(gw_v)))) |
+                     (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(gw_v >> 32))) << 32);
   float m = (act && p.m0 != nullptr) ? p.m0[flat] : 0.0f;
   float cnt = (act && p.counts != nullptr) ? p.counts[flat] : 0.0f;
   // checkpoint rows are counted from ck_origin: row k holds the state before
