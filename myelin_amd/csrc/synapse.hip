@@ -3276,9 +3276,10 @@ struct CurCursor {
 template <bool PRE, bool SPK, bool PK, int RULE, bool CK>
 __device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, bool act, int64_t BN, int64_t gw,
                                          int lane, float &m, float &cnt, CurCursor &o) {
+  // (stores from every lane: a lane past B or N repeats its owner's)
   if constexpr (CK) {
     if (t == o.next_ck) {
-      if (act) *o.ck = m;
+      *o.ck = m;
       o.ck += BN;
       o.next_ck += p.ckpt_every;
     }
@@ -3290,10 +3291,8 @@ __device__ __forceinline__ void cur_step(const CurArgs &p, int64_t t, float c, b
     sp = mp >= p.thr;
   else
     sp = p.slope * (mp - p.thr) >= 0.0f;
-  if (act) {
-    if constexpr (PRE) *o.pre = mp;
-    if constexpr (SPK) *o.spk = sp ? 1.0f : 0.0f;
-  }
+  if constexpr (PRE) *o.pre = mp;
+  if constexpr (SPK) *o.spk = sp ? 1.0f : 0.0f;
   if constexpr (PRE) o.pre += BN;
   if constexpr (SPK) o.spk += BN;
   m = sp ? p.reset : mp;
@@ -3320,17 +3319,19 @@ __global__ __launch_bounds__(256) void lif_currents_fwd(CurArgs p) {
   const int64_t b = g / p.W;
   const int64_t n = (g - b * p.W) * 32 + bit;
   const bool act = (b < p.B) && (n < p.N);
-  const int64_t flat = act ? b * p.N + n : 0, BN = p.B * p.N;
+  // lanes past B or N run the chain of batch row B - 1 / neuron N - 1 and
+  // store the same values to the same addresses as the lane that owns it,
+  // so a step stores without a lane test
+  const int64_t flat = (b < p.B ? b : p.B - 1) * p.N + (n < p.N ? n : p.N - 1), BN = p.B * p.N;
   const int lane = static_cast<int>(threadIdx.x & 63);
   // the wave's first packed word (wave-uniform: made a scalar)
   const int64_t gw_v = (gid - lane) >> 5;
   const int64_t gw = static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(gw_v)))) |
                      (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(gw_v >> 32))) << 32);
-  float m = (act && p.m0 != nullptr) ? p.m0[flat] : 0.0f;
-  float cnt = (act && p.counts != nullptr) ? p.counts[flat] : 0.0f;
+  float m = p.m0 != nullptr ? p.m0[flat] : 0.0f;
+  float cnt = p.counts != nullptr ? p.counts[flat] : 0.0f;
   // checkpoint rows are counted from ck_origin: row k holds the state before
-  // step ck_origin + k*ckpt_every.  Inactive lanes point at element 0 and
-  // store nothing.
+  // step ck_origin + k*ckpt_every.
   CurCursor o{};
   if constexpr (PRE) o.pre = p.pre + (p.t_begin - p.pre_origin) * BN + flat;
   if constexpr (SPK) o.spk = p.spikes + p.t_begin * BN + flat;
