@@ -1000,6 +1000,9 @@ __global__ __launch_bounds__(64 * NarrowBits<NP>::WAVES) void gemm_narrow_bits(G
 // of the fp32 kernel: MFMA busy 31 %, VALU busy ~37 %, a third of each
 // wave's cycles waiting (two waves a SIMD: the transposes' lane shuffles
 // and the loads are latency the other wave only partly covers).
+#ifndef MYELIN_BITS_T_MIN_WG
+#define MYELIN_BITS_T_MIN_WG 256  // workgroups below which the four-wave kernels keep the shape
+#endif
 template <int NP>
 struct NarrowBitsT {
   static constexpr int KSUB = 256, LD = KSUB + 8, WAVES = 4, TILES = 4, COLS = WAVES * TILES;
@@ -3711,7 +3714,7 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
         gemm_narrow_bits<3><<<wide, dim3(64 * NarrowBits<3>::WAVES), 0, s>>>(g);
       else
         gemm_narrow_bits<1><<<wide, dim3(64 * NarrowBits<1>::WAVES), 0, s>>>(g);
-    } else if (bits && ta && !tb) {
+    } else if (bits && ta && !tb && cdiv(cdiv(g.M, 32), NarrowBitsT<1>::COLS) * splits >= MYELIN_BITS_T_MIN_WG) {
       // transposed bit rows (dW_o): word columns turned around in registers
       const dim3 cols(static_cast<unsigned>(cdiv(cdiv(g.M, 32), NarrowBitsT<1>::COLS)), static_cast<unsigned>(splits));
       if constexpr (PREC == 0)
