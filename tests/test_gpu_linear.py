@@ -703,8 +703,10 @@ def test_transposed_bit_operand_at_readout_scale(prec, M, K):
     64000 batch-step rows in 63 K splits; the transposed packed-bit operand
     runs its own kernel, which turns 32 x 32 bit blocks around across lanes)
     and a ragged variant (a partial word column and workgroup, a partial
-    last group): the same bits as the same 0/1 matrix given densely, and at
-    fp32 precision within 1e-6 of float64."""
+    last group), each also with rows of an odd word pitch: the same bits as
+    the same 0/1 matrix given densely, and at fp32 precision within 1e-6 of
+    float64.  (Shapes under one round of the chip's workgroups run the
+    four-wave kernels; the small-shape bits test covers those.)"""
 
     N = 20
     _print_case(test="bits_transposed", M=M, K=K, prec=prec)
@@ -713,14 +715,21 @@ def test_transposed_bit_operand_at_readout_scale(prec, M, K):
     Bd = torch.randn(K, N, generator=g, device=DEV) * 1e-3
     bias = torch.randn(N, generator=g, device=DEV)
     words = myelin.pack_spikes(Ad).data
+    # the same words in rows with 3 slack words (an odd pitch: one word per
+    # load instead of a lane's four columns in one 16-byte load)
+    wide = torch.full((K, words.shape[1] + 3), -1, dtype=torch.int32, device=DEV)
+    wide[:, :words.shape[1]] = words
     stream = _lib.stream(torch.device(DEV))
     for acc in (False, True):
         C0 = torch.randn(M, N, generator=g, device=DEV)
-        dense, bits = C0.clone(), C0.clone()
+        dense, bits, bits_wide = C0.clone(), C0.clone(), C0.clone()
         _gemm(Ad, Bd, dense, M, N, K, M, N, N, True, False, acc, _lib.PREC[prec], stream, bias=bias)
         _gemm(words, Bd, bits, M, N, K, words.shape[1], N, N, True, False, acc, _lib.PREC[prec], stream, bias=bias,
               a_bits=True)
+        _gemm(wide, Bd, bits_wide, M, N, K, wide.shape[1], N, N, True, False, acc, _lib.PREC[prec], stream,
+              bias=bias, a_bits=True)
         assert_same_bits(bits, dense, f"transposed bits, accumulate={acc}")
+        assert_same_bits(bits_wide, dense, f"transposed bits, padded rows, accumulate={acc}")
     if prec == "fp32":
         C = torch.empty(M, N, device=DEV)
         _gemm(words, Bd, C, M, N, K, words.shape[1], N, N, True, False, False, _lib.PREC[prec], stream, a_bits=True)
