@@ -2989,12 +2989,19 @@ struct PreBwdArgs {
 constexpr int kPipe = 16;
 
 // One reverse step of one neuron: gp = dL/dI_j (reference op order), then
-// the carried gm = gp * decay; gb accumulates gp.
-template <int SID, bool GS>
+// the carried gm = gp * decay; gb accumulates gp.  RULE: the spike rule at
+// compile time (MYELIN_RULE_*), or -1 to read p.rule.
+template <int SID, bool GS, int RULE = -1>
 __device__ __forceinline__ float pre_bwd_gp(const PreBwdArgs &p, float pre, float gsv, float gstep, float &gm,
                                             float &gb) {
   const float c = p.slope * (pre - p.thr);
-  const bool sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (pre >= p.thr) : (c >= 0.0f);
+  bool sp;
+  if constexpr (RULE == MYELIN_RULE_THRESHOLD)
+    sp = pre >= p.thr;
+  else if constexpr (RULE == MYELIN_RULE_SURROGATE)
+    sp = c >= 0.0f;
+  else
+    sp = (p.rule == MYELIN_RULE_THRESHOLD) ? (pre >= p.thr) : (c >= 0.0f);
   const float s = sp ? 1.0f : 0.0f;
   const float d = p.slope * sg_deriv<SID>(c);
   float gp = gm * ((1.0f - s) + (p.reset - pre) * d);
@@ -3056,13 +3063,13 @@ __device__ __forceinline__ void store_g(const PreBwdArgs &p, int64_t i, int64_t 
   }
 }
 
-template <int SID, bool GS, int GM, int V, typename VT>
+template <int SID, bool GS, int GM, int V, int RULE = -1, typename VT>
 __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int64_t j, VT pre, VT gsv,
                                              const float (&gstep)[V], float (&gm)[V], float (&gb)[V]) {
   float gp[V];
 #pragma unroll
   for (int e = 0; e < V; ++e)
-    gp[e] = pre_bwd_gp<SID, GS>(p, PreVec<V>::at(pre, e), PreVec<V>::at(gsv, e), gstep[e], gm[e], gb[e]);
+    gp[e] = pre_bwd_gp<SID, GS, RULE>(p, PreVec<V>::at(pre, e), PreVec<V>::at(gsv, e), gstep[e], gm[e], gb[e]);
   store_g<GM, V>(p, i, j, gp);
 }
 
@@ -3075,8 +3082,11 @@ __device__ __forceinline__ void pre_bwd_step(const PreBwdArgs &p, int64_t i, int
 // and so occupancy (3 waves per SIMD instead of 8; 524288 neurons x 50
 // steps: 54 -> 42 us, x 256 steps: 310 -> 293 us, 131072 x 225 with the
 // three-plane G: 86 -> 78 us), and kPipe on the narrow ones, whose few
-// waves need every load of a long serial walk in flight.
-template <int SID, bool GS, int GM, int V>
+// waves need every load of a long serial walk in flight.  RULE: the spike
+// rule at compile time on the narrow grids (a step of the 640-neuron,
+// 2000-step readout walk is 28 instructions with it read at run time, 7 of
+// them choosing the rule), -1 (read p.rule) on the wide ones.
+template <int SID, bool GS, int GM, int V, int RULE = -1>
 __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
   using VT = typename PreVec<V>::T;
   constexpr int DEPTH = V == 2 ? 4 : kPipe;
@@ -3114,7 +3124,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     }
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u)
-      if (u < f) pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
+      if (u < f) pre_bwd_step<SID, GS, GM, V, RULE>(p, i, C - 1 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u) {
       pv[u] = np[u];
@@ -3132,7 +3142,7 @@ __global__ __launch_bounds__(256) void linear_pre_bwd(PreBwdArgs p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u)
-      pre_bwd_step<SID, GS, GM, V>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
+      pre_bwd_step<SID, GS, GM, V, RULE>(p, i, C - 1 - r0 - u, pv[u], GS ? gv[u] : zero, gstep, gm, gb);
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u) {
       pv[u] = np[u];
@@ -3830,22 +3840,34 @@ int launch_gemm(GemmArgs g, int ta, int tb, bool half, int64_t ws_elems, hipStre
   return MYELIN_OK;
 }
 
-template <int SID, int V>
-void launch_pre_bwd_v(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
+template <int SID, int V, int RULE>
+void launch_pre_bwd_r(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
   if (gs) {
     if (gm == 2)
-      linear_pre_bwd<SID, true, 2, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 2, V, RULE><<<grid, dim3(256), 0, s>>>(a);
     else if (gm == 1)
-      linear_pre_bwd<SID, true, 1, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 1, V, RULE><<<grid, dim3(256), 0, s>>>(a);
     else
-      linear_pre_bwd<SID, true, 0, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, true, 0, V, RULE><<<grid, dim3(256), 0, s>>>(a);
   } else {
     if (gm == 2)
-      linear_pre_bwd<SID, false, 2, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 2, V, RULE><<<grid, dim3(256), 0, s>>>(a);
     else if (gm == 1)
-      linear_pre_bwd<SID, false, 1, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 1, V, RULE><<<grid, dim3(256), 0, s>>>(a);
     else
-      linear_pre_bwd<SID, false, 0, V><<<grid, dim3(256), 0, s>>>(a);
+      linear_pre_bwd<SID, false, 0, V, RULE><<<grid, dim3(256), 0, s>>>(a);
+  }
+}
+
+template <int SID, int V>
+void launch_pre_bwd_v(const PreBwdArgs &a, bool gs, int gm, dim3 grid, hipStream_t s) {
+  if constexpr (V == 1) {
+    if (a.rule == MYELIN_RULE_THRESHOLD)
+      launch_pre_bwd_r<SID, V, MYELIN_RULE_THRESHOLD>(a, gs, gm, grid, s);
+    else
+      launch_pre_bwd_r<SID, V, MYELIN_RULE_SURROGATE>(a, gs, gm, grid, s);
+  } else {
+    launch_pre_bwd_r<SID, V, -1>(a, gs, gm, grid, s);
   }
 }
 
