@@ -238,11 +238,12 @@ def test_linear_checkpoint_sizes_agree_and_match_oracle(T, B, F, N):
     xr, wr, br = (t.clone().requires_grad_() for t in (x, w, b))
     _, es = R.linear_surrogate_lif_checkpoint(xr, wr, br, 9.0, 0.7, -0.2, "fast_sigmoid", 5.0, 4)
     es.backward(gs)
-    assert raster_agreement(res[0][0], es) >= 0.9999
-    if raster_agreement(res[0][0], es) == 1.0:
-        assert_norm_close(res[0][1], xr.grad, 1e-5, "grad_x")
-        assert_norm_close(res[0][2], wr.grad, 1e-5, "grad_w")
-        assert_norm_close(res[0][3], br.grad, 1e-5, "grad_b")
+    # the shapes here give the oracle's raster exactly (every spike on the
+    # same side of the threshold), so the gradients are compared always
+    assert raster_agreement(res[0][0], es) == 1.0
+    assert_norm_close(res[0][1], xr.grad, 1e-5, "grad_x")
+    assert_norm_close(res[0][2], wr.grad, 1e-5, "grad_w")
+    assert_norm_close(res[0][3], br.grad, 1e-5, "grad_b")
 
 
 @pytest.mark.parametrize("N", [17, 31, 32, 33, 64, 100])
