@@ -70,6 +70,21 @@ def _ds_fused(prec: int, O: int, H: int, L: int) -> bool:
     return prec == _lib.PREC["fp32"] and 0 < O <= 32 and H % 256 == 0 and L * kmax * 4 <= 65536
 
 
+def _zeros_views(dev, *shapes):
+    """Zero-filled float32 tensors of the given shapes (None gives None), all
+    views of one allocation at 256-byte boundaries: one fill launch where
+    separate torch.zeros calls would each launch one."""
+
+    sizes = [0 if sh is None else math.prod(sh) for sh in shapes]
+    pads = [-(-n // 64) * 64 for n in sizes]
+    buf = torch.zeros(max(1, sum(pads)), device=dev)
+    out, at = [], 0
+    for sh, n, pn in zip(shapes, sizes, pads):
+        out.append(None if sh is None else buf[at:at + n].view(sh))
+        at += pn
+    return out
+
+
 def _readout_chunk(cur, hs, wo, bo, m0, m_final, pre, counts, rates, ckpt, T, t0, t1, C, decay, threshold, reset,
                    slope, prec, stream, exact=False):
     """Readout currents ``hs @ W_o + b_o`` for steps [t0, t1) then the LIF
@@ -112,9 +127,7 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         keep = need and _keep_trace(H, O)
         ck_h = torch.empty((K, B, H), device=dev) if need else None
         ck_o = torch.empty((K, B, O), device=dev) if need and not keep else None
-        m_h = torch.zeros((B, H), device=dev)
-        m_o = torch.zeros((B, O), device=dev)
-        counts = torch.zeros((B, O), device=dev)
+        m_h, m_o, counts = _zeros_views(dev, (B, H), (B, O), (B, O))
         rates = torch.empty((B, O), device=dev)
         # the forward has no per-chunk state to keep beyond the checkpoints,
         # so it runs whole groups of chunks: a group's hidden currents fill
@@ -196,15 +209,14 @@ class HipTwoLayerRateFunction(torch.autograd.Function):
         with torch.cuda.device(dev):
             stream = _lib.stream(dev)
             g_rates = g_rates.float().contiguous()
-            gm_o = torch.zeros((B, O), device=dev)
-            gm_h = torch.zeros((B, H), device=dev) if need_hidden else None
+            gm_o, gm_h, gbh_acc, gbo_acc = _zeros_views(
+                dev, (B, O), (B, H) if need_hidden else None, (B, H) if (need_bh and has_bh) else None,
+                (B, O) if (need_bo and has_bo) else None)
             gx = torch.empty((T, B, F), device=dev) if need_x else None
             whg = _cast_bf16(wh, stream) if (half and need_x) else wh
             # the first (last-in-time) span overwrites the weight gradients
             gwh = torch.empty_like(wh) if need_wh else None
             gwo = torch.empty_like(wo) if need_wo else None
-            gbh_acc = torch.zeros((B, H), device=dev) if (need_bh and has_bh) else None
-            gbo_acc = torch.zeros((B, O), device=dev) if (need_bo and has_bo) else None
             # the bias gradients (column sums of the accumulators, complete
             # once the first span's reverse passes have run) ride with that
             # span's weight-gradient launches
